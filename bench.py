@@ -1,0 +1,188 @@
+#!/usr/bin/env python3
+"""Benchmark of the shared last-layer KV decode attention on one MI355X.
+
+Workload: one last-layer K/V cache [32, 8, 8192, 128] bf16, N(0, 1),
+read by the queries [32, 32, 1, 128] of 32 layers (distinct q per layer, softmax scale
+1/sqrt(128)).  One "step" is one decode step's attention: 32 sequential layer-calls of
+lkv_decode_attn over the shared cache, i.e. 32 new tokens (one per sequence) through 32 layers.
+Inputs are resident in HBM before timing starts.
+
+Printed JSON line (one, from this single process):
+  value          decode tok/s of the attention step (32 tokens / step time)
+  roofline       HBM roofline of lkv_decode_attn: algorithmic bytes per layer-call
+                 (K + V of 8192 tokens x 8 heads x 32 sequences + Q + O = 1,074,266,112 B) over
+                 the kernel's mean duration measured with HIP events on its stream
+  cpu_baseline   the reference path restated with torch ops (torch.cat-free here: config 2 is
+                 all shared history; F.scaled_dot_product_attention with enable_gqa) timed on
+                 this host's CPU cores for a bounded sample
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+METRIC = "decode tok/s + shared-KV attn HBM GB/s (8B shape, 8K ctx, bs32); prefill MFMA %"
+B, HQ, HKV, T, D, LAYERS = 32, 32, 8, 8192, 128, 32
+BYTES_PER_CALL = 2 * B * HKV * T * D * 2 + 2 * B * HQ * D * 2  # 1,074,266,112
+FLOPS_PER_CALL = 4 * B * HQ * T * D
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "decode_config2_traffic.json")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--splits", type=int, default=None, help="key splits per (sequence, kv head); default: heuristic")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sweep-splits", action="store_true", help="print the kernel time for several split counts")
+    return ap.parse_args()
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """Reference CPU path: one full config-2 layer-call (B=32) per repetition, bf16, all host cores."""
+
+    import torch
+
+    from oracle.reference_path import sdpa_bottom_right
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(1)
+    k = torch.randn((B, HKV, T, D), generator=g).bfloat16()
+    v = torch.randn((B, HKV, T, D), generator=g).bfloat16()
+    q = torch.randn((B, HQ, 1, D), generator=g).bfloat16()
+    sdpa_bottom_right(q, k, v, native_gqa=True)  # warm-up
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < seconds and len(times) < 200):
+        t0 = time.perf_counter()
+        sdpa_bottom_right(q, k, v, native_gqa=True)
+        times.append(time.perf_counter() - t0)
+    per_call = statistics.median(times)
+    step = per_call * LAYERS
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((line.split(":", 1)[1].strip() for line in f if line.startswith("model name")), "")
+    except OSError:
+        pass
+    return {
+        "value": round(B / step, 3),
+        "unit": "tok/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} full config-2 layer-calls (B=32, 8192-token shared K/V, bf16) of the torch "
+                   f"restatement of the reference SDPA path; median {per_call * 1e3:.1f} ms/call = "
+                   f"{BYTES_PER_CALL / per_call / 1e9:.1f} GB/s; step = 32 calls; host '{model}', "
+                   f"os.cpu_count()={threads}"),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this path runs on one MI355X without sharding or "
+              "collectives (multi-GPU sharding is described in DESIGN.md, not measured).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from lastkv_amd import ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(2)
+    k = torch.randn((B, HKV, T, D), generator=g, device=dev).bfloat16()
+    v = torch.randn((B, HKV, T, D), generator=g, device=dev).bfloat16()
+    cache = ops.TiledKV.zeros(B, HKV, T, dev)
+    ops.pack_kv(k, v, cache)
+    del k, v
+    qs = torch.randn((LAYERS, B, HQ, D), generator=g, device=dev).bfloat16()
+    outs = torch.empty_like(qs)
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+
+    def run_step(splits, events=None):
+        for layer in range(LAYERS):
+            if events is not None:
+                events[layer][0].record()
+            ops.decode_attention(qs[layer], older=cache, older_len=T, out=outs[layer], num_splits=splits,
+                                 workspace=workspace)
+            if events is not None:
+                events[layer][1].record()
+
+    splits = args.splits or ops.default_decode_splits(B, HKV, T, cu)
+    if args.sweep_splits:
+        for s in (1, 2, 3, 4, 6, 8, 16):
+            workspace = torch.empty(max(1, B * HQ * s * 130 * 4), dtype=torch.uint8, device=dev)
+            run_step(s)
+            ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(LAYERS)]
+            torch.cuda.synchronize()
+            run_step(s, ev)
+            torch.cuda.synchronize()
+            ms = statistics.mean(e[0].elapsed_time(e[1]) for e in ev)
+            print(f"sweep splits={s}: {ms * 1e3:.1f} us/call {BYTES_PER_CALL / ms / 1e6:.0f} GB/s", file=sys.stderr, flush=True)
+    workspace = torch.empty(max(1, B * HQ * splits * 130 * 4), dtype=torch.uint8, device=dev)
+
+    for _ in range(args.warmup):
+        run_step(splits)
+    torch.cuda.synchronize()
+    events = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(LAYERS)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for step in range(args.steps):
+        run_step(splits, events[step])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    kernel_ms = statistics.mean(e[0].elapsed_time(e[1]) for ev in events for e in ev)
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    achieved = BYTES_PER_CALL / (kernel_ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    result = {
+        "metric": METRIC,
+        "value": round(B / (ms_per_step * 1e-3), 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) q/K/V, seeded (torch.Generator seed 2)",
+        "config": {
+            "workload": "BASELINE config 2: isolated shared-KV decode attention, 32 layer-calls per step",
+            "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": T, "layers_per_step": LAYERS,
+            "num_splits": splits, "cache_bytes": 2 * B * HKV * T * D * 2,
+        },
+        "attn_hbm_gbps": round(achieved, 1),
+        "kernel_us_per_call": round(kernel_ms * 1e3, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,119 @@
+"""ctypes binding of ``liblastkv_amd.so`` (the C ABI in ``include/lastkv_amd.h``).
+
+The library is loaded lazily from this package directory.  There is no fallback: if it is
+missing, every op raises ``LastKVNativeError`` naming the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import threading
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
+ABI_VERSION = 1
+
+
+class LastKVNativeError(RuntimeError):
+    """A C-ABI call failed, or the native library is unavailable."""
+
+
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_f32 = ctypes.c_float
+c_ptr = ctypes.c_void_p
+
+
+class DecodeArgs(ctypes.Structure):
+    """Mirror of ``lkv_decode_args``."""
+
+    _fields_ = [
+        ("struct_size", c_i32),
+        ("batch", c_i32),
+        ("num_q_heads", c_i32),
+        ("num_kv_heads", c_i32),
+        ("head_dim", c_i32),
+        ("num_splits", c_i32),
+        ("sm_scale", c_f32),
+        ("older_vscale_mode", c_i32),
+        ("q", c_ptr),
+        ("q_stride_b", c_i64),
+        ("out", c_ptr),
+        ("out_stride_b", c_i64),
+        ("lse", c_ptr),
+        ("older_k", c_ptr),
+        ("older_v", c_ptr),
+        ("older_seq_stride", c_i64),
+        ("older_head_stride", c_i64),
+        ("older_len", c_ptr),
+        ("older_len_const", c_i32),
+        ("older_capacity_tokens", c_i32),
+        ("older_slot", c_ptr),
+        ("older_num_slots", c_i32),
+        ("vscale", c_ptr),
+        ("local_k", c_ptr),
+        ("local_v", c_ptr),
+        ("local_seq_stride", c_i64),
+        ("local_head_stride", c_i64),
+        ("local_ring_blocks", c_i32),
+        ("local_len_const", c_i32),
+        ("local_len", c_ptr),
+        ("local_start_block", c_ptr),
+        ("local_slot", c_ptr),
+        ("local_num_slots", c_i32),
+        ("workspace", c_ptr),
+        ("workspace_bytes", c_i64),
+    ]
+
+
+# name -> (restype, argtypes)
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "lkv_abi_version": (c_i32, []),
+    "lkv_last_error": (ctypes.c_char_p, []),
+    "lkv_cache_pack": (
+        c_i32,
+        [c_ptr, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_ptr, c_i64, c_i64, c_i32, c_i32, c_ptr],
+    ),
+    "lkv_cache_unpack": (
+        c_i32,
+        [c_ptr, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr],
+    ),
+    "lkv_decode_workspace_bytes": (c_i64, [c_i32, c_i32, c_i32]),
+    "lkv_decode_attn": (c_i32, [ctypes.POINTER(DecodeArgs), c_ptr]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load and type the native library (once per process)."""
+
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise LastKVNativeError(
+                f"{LIB_PATH.name} is not built; run `python -m lastkv_amd.build` (hipcc, gfx950)"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.lkv_abi_version()
+        if version != ABI_VERSION:
+            raise LastKVNativeError(f"{LIB_PATH.name} ABI version {version}, expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def check(status: int, what: str) -> None:
+    """Raise ``LastKVNativeError`` carrying the library's message for a failed call."""
+
+    if status != 0:
+        message = load().lkv_last_error().decode(errors="replace")
+        raise LastKVNativeError(f"{what} failed (status {status}): {message}")

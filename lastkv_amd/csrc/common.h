@@ -1,0 +1,78 @@
+// Shared device helpers for the gfx950 LastKV kernels.
+//
+// Cache layout ("tiled", one 32-token block = 4096 bf16 = 8 KiB per (sequence, kv head)):
+//   K block: element (w, d), w = token in block, d = head dim, is stored at
+//            ((u * 4 + kb) * 16 + r) * 32 + (d & 31)
+//            with kb = d >> 5, u = (w >> 2) & 1, r = ((w >> 3) << 2) | (w & 3).
+//            A wave reads a 16-token x 32-dim MFMA operand tile as one contiguous 1 KiB run.
+//   V block: element (w, d) is stored at d * 32 + w (the block is V transposed),
+//            so the PV operand (8 consecutive tokens of one dim per lane) is a 16-byte load.
+// The token permutation inside K tiles makes the QK^T accumulator of lane (n, g) hold
+// exactly the tokens 8g..8g+7 that the PV MFMA wants as its A operand in that lane, so
+// the probabilities never cross lanes.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lkv {
+
+constexpr int kHeadDim = 128;
+constexpr int kBlockTokens = 32;
+constexpr int kBlockElems = kBlockTokens * kHeadDim;  // 4096
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__host__ __device__ inline int k_tile_offset(int w, int d) {
+  const int u = (w >> 2) & 1;
+  const int r = ((w >> 3) << 2) | (w & 3);
+  const int kb = d >> 5;
+  return ((u * 4 + kb) * 16 + r) * 32 + (d & 31);
+}
+
+__host__ __device__ inline int v_tile_offset(int w, int d) { return d * 32 + w; }
+
+__device__ inline float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+__device__ inline float bf16_lo(uint32_t packed) { return __uint_as_float(packed << 16); }
+__device__ inline float bf16_hi(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950), NaN preserved.
+__device__ inline uint16_t f32_to_bf16_bits(float x) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+}
+
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+}
+
+__device__ inline bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+__device__ inline f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+__device__ inline f32x4 mfma_f16(uint4 a, uint4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline float wave_max_across_rows(float x) {
+  // lanes n, n+16, n+32, n+48 hold the same head; reduce over the four 16-lane rows
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
+__device__ inline float wave_sum_across_rows(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+}  // namespace lkv

@@ -1,0 +1,420 @@
+// Split-K shared-KV decode attention for gfx950.
+//
+// One workgroup = 4 waves = one (sequence, kv head, key split).  Each wave streams 32-token
+// blocks of the tiled K/V cache straight from HBM into registers with 16-byte loads (each load
+// instruction of the wave covers one contiguous 1 KiB run), double-buffered so that the next
+// block is in flight while the current one is computed:
+//   S^T[32 tok x 16 col] = K_tile * Q^T   two 16x16x32 bf16 MFMAs per 32 dims, 8 per block;
+//                                          columns are the (<=16) query heads of the GQA group
+//   online softmax in the exp2 domain, row max / row sum over the four 16-lane rows (DPP)
+//   O[16 x 128] += P * V                  P split into bf16 hi + lo parts, 16 MFMAs per block,
+//                                          so P*V carries ~16 mantissa bits instead of 8
+// The waves of a workgroup merge their (m, l, O) states through LDS.  With one split the
+// workgroup writes the normalised bf16 output; otherwise it writes an unnormalised partial
+// state and lkv_decode_combine merges the splits.
+#include "common.h"
+#include "runtime.h"
+
+namespace lkv {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr float kNegInf = -__builtin_inff();
+
+struct DecodeParams {
+  const uint16_t* q;
+  int64_t q_sb;
+  uint16_t* out;
+  int64_t out_sb;
+  float* lse;
+  const uint16_t* ok;
+  const uint16_t* ov;
+  int64_t o_ss, o_hs;
+  const int32_t* o_len;
+  int32_t o_len_c, o_cap;
+  const int32_t* o_slot;
+  int32_t o_nslots;
+  const float* vscale;
+  const uint16_t* lk;
+  const uint16_t* lv;
+  int64_t l_ss, l_hs;
+  int32_t ring_blocks;
+  const int32_t* l_len;
+  int32_t l_len_c;
+  const int32_t* l_start;
+  const int32_t* l_slot;
+  int32_t l_nslots;
+  float* ws_o;
+  float* ws_ml;
+  int32_t hq, group, splits;
+  float scale_log2;
+};
+
+struct BlockFrags {
+  uint4 k[2][4];
+  uint4 v[8];
+};
+
+struct BlockRef {
+  const uint16_t* k;
+  const uint16_t* v;
+  int valid;
+  bool older;
+};
+
+struct SeqView {
+  const uint16_t* ok;
+  const uint16_t* ov;
+  const uint16_t* lk;
+  const uint16_t* lv;
+  int n0, n1, nb0, lstart, ring_blocks;
+};
+
+__device__ inline BlockRef block_ref(const SeqView& s, int blk) {
+  BlockRef r;
+  if (blk < s.nb0) {
+    r.k = s.ok + static_cast<int64_t>(blk) * kBlockElems;
+    r.v = s.ov + static_cast<int64_t>(blk) * kBlockElems;
+    r.valid = min(kBlockTokens, s.n0 - blk * kBlockTokens);
+    r.older = true;
+  } else {
+    const int j = blk - s.nb0;
+    int rb = s.lstart + j;
+    if (rb >= s.ring_blocks) rb -= s.ring_blocks;
+    r.k = s.lk + static_cast<int64_t>(rb) * kBlockElems;
+    r.v = s.lv + static_cast<int64_t>(rb) * kBlockElems;
+    r.valid = min(kBlockTokens, s.n1 - j * kBlockTokens);
+    r.older = false;
+  }
+  return r;
+}
+
+__device__ inline void load_block(BlockFrags& f, const BlockRef& r, int n16, int g4) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      f.k[u][kb] = *reinterpret_cast<const uint4*>(r.k + ((u * 4 + kb) * 16 + n16) * 32 + 8 * g4);
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) f.v[nb] = *reinterpret_cast<const uint4*>(r.v + (16 * nb + n16) * 32 + 8 * g4);
+}
+
+// bf16(v * s) for the 8 bf16 values of one fragment (the reference materialises s * V in bf16).
+__device__ inline uint4 scale_frag(uint4 v, float s) {
+  uint4 r;
+  r.x = pack_bf16x2(bf16_lo(v.x) * s, bf16_hi(v.x) * s);
+  r.y = pack_bf16x2(bf16_lo(v.y) * s, bf16_hi(v.y) * s);
+  r.z = pack_bf16x2(bf16_lo(v.z) * s, bf16_hi(v.z) * s);
+  r.w = pack_bf16x2(bf16_lo(v.w) * s, bf16_hi(v.w) * s);
+  return r;
+}
+
+struct SoftmaxState {
+  float m, l;
+  f32x4 o[8];  // O rows (heads 4*g4 + i) x dims 16*nb + n16
+};
+
+template <bool kVScale>
+__device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, const uint4 (&qf)[4], float vs,
+                                     float scale_log2, int n16, int g4, SoftmaxState& st) {
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    s0 = mfma_bf16(f.k[0][kb], qf[kb], s0);
+    s1 = mfma_bf16(f.k[1][kb], qf[kb], s1);
+  }
+  // lane (n16 = head column, g4) holds the scores of tokens 8*g4 + j, j = 0..7
+  float s[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s[i] = s0[i] * scale_log2;
+    s[4 + i] = s1[i] * scale_log2;
+  }
+  if (r.valid < kBlockTokens) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (8 * g4 + j >= r.valid) s[j] = kNegInf;
+  }
+  float mx = s[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) mx = fmaxf(mx, s[j]);
+  mx = wave_max_across_rows(mx);
+  const float m_new = fmaxf(st.m, mx);
+  float alpha = 1.f;
+  float p[8];
+  if (m_new == kNegInf) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p[j] = 0.f;
+  } else {
+    alpha = fast_exp2(st.m - m_new);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p[j] = fast_exp2(s[j] - m_new);
+  }
+  float rs = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+  rs = wave_sum_across_rows(rs);
+  st.l = st.l * alpha + rs;
+  st.m = m_new;
+  // rows of this lane's O accumulators are heads 4*g4 + i; their factors live in lanes 4*g4 + i
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = __shfl(alpha, 4 * g4 + i);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) st.o[nb][i] *= a;
+  }
+  uint4 phi, plo;
+  float hi[8];
+  phi.x = pack_bf16x2(p[0], p[1]);
+  phi.y = pack_bf16x2(p[2], p[3]);
+  phi.z = pack_bf16x2(p[4], p[5]);
+  phi.w = pack_bf16x2(p[6], p[7]);
+  hi[0] = bf16_lo(phi.x);
+  hi[1] = bf16_hi(phi.x);
+  hi[2] = bf16_lo(phi.y);
+  hi[3] = bf16_hi(phi.y);
+  hi[4] = bf16_lo(phi.z);
+  hi[5] = bf16_hi(phi.z);
+  hi[6] = bf16_lo(phi.w);
+  hi[7] = bf16_hi(phi.w);
+  plo.x = pack_bf16x2(p[0] - hi[0], p[1] - hi[1]);
+  plo.y = pack_bf16x2(p[2] - hi[2], p[3] - hi[3]);
+  plo.z = pack_bf16x2(p[4] - hi[4], p[5] - hi[5]);
+  plo.w = pack_bf16x2(p[6] - hi[6], p[7] - hi[7]);
+  const bool scale_v = kVScale && r.older;
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) {
+    const uint4 v = scale_v ? scale_frag(f.v[nb], vs) : f.v[nb];
+    st.o[nb] = mfma_bf16(phi, v, st.o[nb]);
+    st.o[nb] = mfma_bf16(plo, v, st.o[nb]);
+  }
+}
+
+template <bool kVScale>
+__global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p) {
+  __shared__ float sm_m[kWaves][16];
+  __shared__ float sm_l[kWaves][16];
+  __shared__ float sm_o[kWaves][16][kHeadDim];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n16 = lane & 15, g4 = lane >> 4;
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = p.group;
+
+  SeqView sv;
+  {
+    const int oslot = p.o_slot ? p.o_slot[b] : b;
+    const int lslot = p.l_slot ? p.l_slot[b] : b;
+    int n0 = p.o_len ? p.o_len[b] : p.o_len_c;
+    int n1 = p.lk ? (p.l_len ? p.l_len[b] : p.l_len_c) : 0;
+    n0 = (oslot < 0 || oslot >= p.o_nslots || p.ok == nullptr) ? 0 : min(max(n0, 0), p.o_cap);
+    n1 = (lslot < 0 || lslot >= p.l_nslots) ? 0 : min(max(n1, 0), p.ring_blocks * kBlockTokens);
+    int ls = p.l_start ? p.l_start[b] : 0;
+    ls = (ls < 0 || ls >= p.ring_blocks) ? 0 : ls;
+    sv.ok = p.ok ? p.ok + static_cast<int64_t>(oslot) * p.o_ss + kvh * p.o_hs : nullptr;
+    sv.ov = p.ov ? p.ov + static_cast<int64_t>(oslot) * p.o_ss + kvh * p.o_hs : nullptr;
+    sv.lk = p.lk ? p.lk + static_cast<int64_t>(lslot) * p.l_ss + kvh * p.l_hs : nullptr;
+    sv.lv = p.lv ? p.lv + static_cast<int64_t>(lslot) * p.l_ss + kvh * p.l_hs : nullptr;
+    sv.n0 = n0;
+    sv.n1 = n1;
+    sv.nb0 = (n0 + kBlockTokens - 1) / kBlockTokens;
+    sv.lstart = ls;
+    sv.ring_blocks = p.ring_blocks;
+  }
+  const int nbt = sv.nb0 + (sv.n1 + kBlockTokens - 1) / kBlockTokens;
+  const int bps = (nbt + p.splits - 1) / p.splits;
+  const int blk_begin = split * bps;
+  const int blk_end = min(blk_begin + bps, nbt);
+
+  uint4 qf[4];
+  {
+    const uint16_t* qrow = p.q + b * p.q_sb + static_cast<int64_t>(kvh * G + n16) * kHeadDim;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      qf[kb] = n16 < G ? *reinterpret_cast<const uint4*>(qrow + 32 * kb + 8 * g4) : make_uint4(0, 0, 0, 0);
+  }
+  const float vs = kVScale ? p.vscale[kvh] : 1.f;
+
+  SoftmaxState st;
+  st.m = kNegInf;
+  st.l = 0.f;
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) st.o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int blk = blk_begin + wave;
+  if (blk < blk_end) {
+    const int last = blk + ((blk_end - 1 - blk) / kWaves) * kWaves;
+    BlockFrags fa, fb;
+    BlockRef ra = block_ref(sv, blk);
+    load_block(fa, ra, n16, g4);
+    // The prefetch of the block after the last one re-reads the last block (an L2 hit), which
+    // keeps the loads unconditional so the compiler can count them for s_waitcnt.
+    while (true) {
+      const BlockRef rb = block_ref(sv, min(blk + kWaves, last));
+      load_block(fb, rb, n16, g4);
+      compute_block<kVScale>(fa, ra, qf, vs, p.scale_log2, n16, g4, st);
+      if (blk + kWaves > last) break;
+      blk += kWaves;
+      ra = block_ref(sv, min(blk + kWaves, last));
+      load_block(fa, ra, n16, g4);
+      compute_block<kVScale>(fb, rb, qf, vs, p.scale_log2, n16, g4, st);
+      if (blk + kWaves > last) break;
+      blk += kWaves;
+    }
+  }
+
+  // merge the four waves' states
+  if (g4 == 0 && n16 < G) {
+    sm_m[wave][n16] = st.m;
+    sm_l[wave][n16] = st.l;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * g4 + i;
+    if (h < G) {
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) sm_o[wave][h][16 * nb + n16] = st.o[nb][i];
+    }
+  }
+  __syncthreads();
+  const int bh0 = b * p.hq + kvh * G;
+  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += 256) {
+    const int h = idx >> 7, d = idx & (kHeadDim - 1);
+    float M = sm_m[0][h];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = sm_m[w][h] == kNegInf ? 0.f : fast_exp2(sm_m[w][h] - M);
+      L += f * sm_l[w][h];
+      O += f * sm_o[w][h][d];
+    }
+    if (p.splits == 1) {
+      p.out[b * p.out_sb + static_cast<int64_t>(kvh * G + h) * kHeadDim + d] = f32_to_bf16_bits(L > 0.f ? O / L : 0.f);
+      if (p.lse != nullptr && d == 0) p.lse[bh0 + h] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
+    } else {
+      const int64_t row = static_cast<int64_t>(bh0 + h) * p.splits + split;
+      p.ws_o[row * kHeadDim + d] = O;
+      if (d == 0) {
+        p.ws_ml[row * 2] = M;
+        p.ws_ml[row * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Merges the per-split states of one (sequence, query head); one thread per head dim.
+__global__ __launch_bounds__(128) void decode_combine_kernel(const DecodeParams p) {
+  const int bh = blockIdx.x;
+  const int d = threadIdx.x;
+  const int b = bh / p.hq, h = bh % p.hq;
+  const float* ml = p.ws_ml + static_cast<int64_t>(bh) * p.splits * 2;
+  const float* o = p.ws_o + static_cast<int64_t>(bh) * p.splits * kHeadDim;
+  float M = kNegInf;
+  for (int s = 0; s < p.splits; ++s) M = fmaxf(M, ml[2 * s]);
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < p.splits; ++s) {
+    const float ms = ml[2 * s];
+    const float f = ms == kNegInf ? 0.f : fast_exp2(ms - M);
+    L += f * ml[2 * s + 1];
+    O += f * o[s * kHeadDim + d];
+  }
+  p.out[b * p.out_sb + static_cast<int64_t>(h) * kHeadDim + d] = f32_to_bf16_bits(L > 0.f ? O / L : 0.f);
+  if (p.lse != nullptr && d == 0) p.lse[bh] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
+}
+
+}  // namespace
+}  // namespace lkv
+
+extern "C" int64_t lkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_splits) {
+  if (batch <= 0 || num_q_heads <= 0 || num_splits <= 1) return 0;
+  return static_cast<int64_t>(batch) * num_q_heads * num_splits * (lkv::kHeadDim + 2) * 4;
+}
+
+extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream) {
+  using namespace lkv;
+  LKV_REQUIRE(a != nullptr, "null args");
+  LKV_REQUIRE(a->struct_size == static_cast<int32_t>(sizeof(lkv_decode_args)),
+              "lkv_decode_args size mismatch (caller %d, library %d)", a->struct_size,
+              static_cast<int32_t>(sizeof(lkv_decode_args)));
+  LKV_REQUIRE(a->head_dim == kHeadDim, "head_dim must be 128, got %d", a->head_dim);
+  LKV_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->num_q_heads > 0, "bad sizes");
+  LKV_REQUIRE(a->num_q_heads % a->num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
+  const int group = a->num_q_heads / a->num_kv_heads;
+  LKV_REQUIRE(group <= 16, "GQA group %d exceeds 16", group);
+  LKV_REQUIRE(a->num_splits >= 1 && a->num_splits <= 1024, "num_splits must be in [1, 1024]");
+  LKV_REQUIRE(a->older_vscale_mode == 0 || a->older_vscale_mode == 1, "older_vscale_mode must be 0 or 1");
+  LKV_REQUIRE(a->older_vscale_mode == 0 || a->vscale != nullptr, "older_vscale_mode 1 needs vscale");
+  LKV_REQUIRE(a->q != nullptr && a->out != nullptr, "null q/out");
+  LKV_REQUIRE((a->older_k == nullptr) == (a->older_v == nullptr), "older_k and older_v must both be set");
+  LKV_REQUIRE((a->local_k == nullptr) == (a->local_v == nullptr), "local_k and local_v must both be set");
+  LKV_REQUIRE(a->older_k == nullptr || a->older_capacity_tokens % kBlockTokens == 0,
+              "older capacity must be a multiple of 32 tokens");
+  LKV_REQUIRE(a->older_k == nullptr || a->older_num_slots > 0, "older_num_slots must be positive");
+  LKV_REQUIRE(a->older_k == nullptr || a->older_slot != nullptr || a->older_num_slots >= a->batch,
+              "older_num_slots < batch with identity slots");
+  LKV_REQUIRE(a->local_k == nullptr || a->local_ring_blocks > 0, "local ring needs at least one block");
+  LKV_REQUIRE(a->local_k == nullptr || a->local_num_slots > 0, "local_num_slots must be positive");
+  LKV_REQUIRE(a->local_k == nullptr || a->local_slot != nullptr || a->local_num_slots >= a->batch,
+              "local_num_slots < batch with identity slots");
+  LKV_REQUIRE((a->q_stride_b % 8) == 0 && (reinterpret_cast<uintptr_t>(a->q) & 15) == 0,
+              "q rows must be 16-byte aligned");
+  const uintptr_t align_or = reinterpret_cast<uintptr_t>(a->older_k) | reinterpret_cast<uintptr_t>(a->older_v) |
+                             reinterpret_cast<uintptr_t>(a->local_k) | reinterpret_cast<uintptr_t>(a->local_v);
+  LKV_REQUIRE((align_or & 15) == 0, "caches must be 16-byte aligned");
+  LKV_REQUIRE((a->older_seq_stride | a->older_head_stride | a->local_seq_stride | a->local_head_stride) % 8 == 0,
+              "cache strides must be multiples of 8 elements");
+  if (a->batch == 0) return LKV_OK;
+  const int64_t need = lkv_decode_workspace_bytes(a->batch, a->num_q_heads, a->num_splits);
+  if (need > 0) {
+    if (a->workspace == nullptr || a->workspace_bytes < need)
+      return fail(LKV_ERR_WORKSPACE, "decode workspace needs %lld bytes, got %lld", static_cast<long long>(need),
+                  static_cast<long long>(a->workspace_bytes));
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 15) != 0)
+      return fail(LKV_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  }
+  DecodeParams p;
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.q_sb = a->q_stride_b;
+  p.out = static_cast<uint16_t*>(a->out);
+  p.out_sb = a->out_stride_b;
+  p.lse = a->lse;
+  p.ok = static_cast<const uint16_t*>(a->older_k);
+  p.ov = static_cast<const uint16_t*>(a->older_v);
+  p.o_ss = a->older_seq_stride;
+  p.o_hs = a->older_head_stride;
+  p.o_len = a->older_len;
+  p.o_len_c = a->older_len_const;
+  p.o_cap = a->older_capacity_tokens;
+  p.o_slot = a->older_slot;
+  p.o_nslots = a->older_num_slots;
+  p.vscale = a->vscale;
+  p.lk = static_cast<const uint16_t*>(a->local_k);
+  p.lv = static_cast<const uint16_t*>(a->local_v);
+  p.l_ss = a->local_seq_stride;
+  p.l_hs = a->local_head_stride;
+  p.ring_blocks = a->local_k ? a->local_ring_blocks : 1;
+  p.l_len = a->local_len;
+  p.l_len_c = a->local_len_const;
+  p.l_start = a->local_start_block;
+  p.l_slot = a->local_slot;
+  p.l_nslots = a->local_num_slots;
+  p.ws_o = static_cast<float*>(a->workspace);
+  p.ws_ml = need > 0 ? p.ws_o + static_cast<int64_t>(a->batch) * a->num_q_heads * a->num_splits * kHeadDim : nullptr;
+  p.hq = a->num_q_heads;
+  p.group = group;
+  p.splits = a->num_splits;
+  p.scale_log2 = a->sm_scale * kLog2e;
+  const dim3 grid(a->num_splits, a->num_kv_heads, a->batch);
+  hipStream_t s = as_stream(stream);
+  if (a->older_vscale_mode == 1)
+    decode_split_kernel<true><<<grid, 256, 0, s>>>(p);
+  else
+    decode_split_kernel<false><<<grid, 256, 0, s>>>(p);
+  if (int32_t st = check_launch("lkv_decode_attn split kernel")) return st;
+  if (a->num_splits > 1) {
+    decode_combine_kernel<<<a->batch * a->num_q_heads, kHeadDim, 0, s>>>(p);
+    return check_launch("lkv_decode_attn combine kernel");
+  }
+  return LKV_OK;
+}

@@ -1,0 +1,276 @@
+"""Torch-facing wrappers of the C-ABI kernels.
+
+Each wrapper validates shapes, dtypes and devices, then passes raw device pointers and the
+current HIP stream of the tensors' device to ``liblastkv_amd.so``.  Nothing here computes on
+the CPU; a missing library raises ``LastKVNativeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+BLOCK_TOKENS = 32
+BLOCK_ELEMS = BLOCK_TOKENS * HEAD_DIM
+KIND_K, KIND_V = 0, 1
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require(cond: bool, message: str) -> None:
+    if not cond:
+        raise ValueError(message)
+
+
+def _require_bf16_cuda(name: str, t: torch.Tensor) -> None:
+    _require(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+    _require(t.is_cuda, f"{name} must be on a GPU (the kernels have no CPU path)")
+    _require(t.dtype == torch.bfloat16, f"{name} must be bfloat16, got {t.dtype}")
+
+
+@dataclass
+class TiledKV:
+    """K and V caches in the tiled block layout: ``[slots, heads, blocks, 4096]`` bf16 each.
+
+    Slot ``s`` / head ``h`` owns ``blocks`` consecutive 32-token blocks; a slot is one
+    sequence's shared history (older region) or one layer's ring (recent + current chunk).
+    """
+
+    k: torch.Tensor
+    v: torch.Tensor
+
+    def __post_init__(self) -> None:
+        for name, t in (("k", self.k), ("v", self.v)):
+            _require_bf16_cuda(f"TiledKV.{name}", t)
+            _require(t.dim() == 4 and t.shape[-1] == BLOCK_ELEMS, f"TiledKV.{name} must be [slots, heads, blocks, 4096]")
+            _require(t.is_contiguous(), f"TiledKV.{name} must be contiguous")
+        _require(self.k.shape == self.v.shape, "TiledKV k and v shapes differ")
+
+    @classmethod
+    def zeros(cls, slots: int, heads: int, capacity_tokens: int, device: torch.device | str) -> "TiledKV":
+        _require(capacity_tokens % BLOCK_TOKENS == 0, "capacity must be a multiple of 32 tokens")
+        shape = (slots, heads, capacity_tokens // BLOCK_TOKENS, BLOCK_ELEMS)
+        return cls(torch.zeros(shape, dtype=torch.bfloat16, device=device), torch.zeros(shape, dtype=torch.bfloat16, device=device))
+
+    @property
+    def slots(self) -> int:
+        return int(self.k.shape[0])
+
+    @property
+    def heads(self) -> int:
+        return int(self.k.shape[1])
+
+    @property
+    def blocks(self) -> int:
+        return int(self.k.shape[2])
+
+    @property
+    def capacity_tokens(self) -> int:
+        return self.blocks * BLOCK_TOKENS
+
+    @property
+    def seq_stride(self) -> int:
+        return self.heads * self.blocks * BLOCK_ELEMS
+
+    @property
+    def head_stride(self) -> int:
+        return self.blocks * BLOCK_ELEMS
+
+    @property
+    def device(self) -> torch.device:
+        return self.k.device
+
+
+def cache_pack(src: torch.Tensor, cache: torch.Tensor, kind: int, token0: int = 0, *, capacity_tokens: int | None = None) -> None:
+    """Write ``src`` ``[B, H, T, 128]`` into cache tokens ``[token0, token0 + T)`` of slots ``0..B-1``."""
+
+    _require_bf16_cuda("src", src)
+    _require(src.dim() == 4 and src.shape[-1] == HEAD_DIM and src.stride(-1) == 1, "src must be [B, H, T, 128] with unit dim stride")
+    _require(cache.dim() == 4 and cache.shape[-1] == BLOCK_ELEMS, "cache must be [slots, heads, blocks, 4096]")
+    _require_bf16_cuda("cache", cache)
+    B, H, T, _ = src.shape
+    _require(B <= cache.shape[0] and H == cache.shape[1], "src batch/heads do not fit the cache")
+    cap = cache.shape[2] * BLOCK_TOKENS if capacity_tokens is None else capacity_tokens
+    lib = _lib.load()
+    _lib.check(
+        lib.lkv_cache_pack(
+            src.data_ptr(), src.stride(0), src.stride(1), src.stride(2), B, H, T, kind,
+            cache.data_ptr(), cache.stride(0), cache.stride(1), token0, cap, _stream(src.device),
+        ),
+        "lkv_cache_pack",
+    )
+
+
+def cache_unpack(cache: torch.Tensor, kind: int, token0: int, tokens: int, batch: int | None = None) -> torch.Tensor:
+    """Read cache tokens ``[token0, token0 + tokens)`` back as ``[B, H, tokens, 128]``."""
+
+    _require_bf16_cuda("cache", cache)
+    _require(cache.dim() == 4 and cache.shape[-1] == BLOCK_ELEMS, "cache must be [slots, heads, blocks, 4096]")
+    B = cache.shape[0] if batch is None else batch
+    H = cache.shape[1]
+    out = torch.empty((B, H, tokens, HEAD_DIM), dtype=torch.bfloat16, device=cache.device)
+    lib = _lib.load()
+    _lib.check(
+        lib.lkv_cache_unpack(
+            cache.data_ptr(), cache.stride(0), cache.stride(1), token0, cache.shape[2] * BLOCK_TOKENS,
+            B, H, tokens, kind, out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), _stream(cache.device),
+        ),
+        "lkv_cache_unpack",
+    )
+    return out
+
+
+def pack_kv(k: torch.Tensor, v: torch.Tensor, cache: TiledKV, token0: int = 0) -> None:
+    cache_pack(k, cache.k, KIND_K, token0)
+    cache_pack(v, cache.v, KIND_V, token0)
+
+
+def unpack_kv(cache: TiledKV, token0: int, tokens: int, batch: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    return cache_unpack(cache.k, KIND_K, token0, tokens, batch), cache_unpack(cache.v, KIND_V, token0, tokens, batch)
+
+
+_CU_COUNT: dict[int, int] = {}
+
+
+def _cu_count(device: torch.device) -> int:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _CU_COUNT:
+        _CU_COUNT[index] = int(torch.cuda.get_device_properties(index).multi_processor_count)
+    return _CU_COUNT[index]
+
+
+def default_decode_splits(batch: int, kv_heads: int, max_tokens: int, cu_count: int) -> int:
+    """Key splits per (sequence, kv head) so that roughly one 4-wave workgroup runs per CU."""
+
+    pairs = max(1, batch * kv_heads)
+    blocks = max(1, math.ceil(max_tokens / BLOCK_TOKENS))
+    splits = math.ceil(cu_count / pairs)
+    return int(max(1, min(splits, math.ceil(blocks / 4), 1024)))
+
+
+def _len_arg(value: int | torch.Tensor | None, batch: int, name: str, device: torch.device) -> tuple[int | None, int]:
+    if value is None:
+        return None, 0
+    if isinstance(value, torch.Tensor):
+        _require(value.dtype == torch.int32 and value.device == device and value.numel() == batch and value.is_contiguous(),
+                 f"{name} must be a contiguous int32 tensor of {batch} entries on {device}")
+        return value.data_ptr(), 0
+    return None, int(value)
+
+
+def decode_attention(
+    q: torch.Tensor,
+    *,
+    older: TiledKV | None = None,
+    older_len: int | torch.Tensor = 0,
+    older_slot: torch.Tensor | None = None,
+    vscale: torch.Tensor | None = None,
+    local: TiledKV | None = None,
+    local_len: int | torch.Tensor = 0,
+    local_start_block: torch.Tensor | None = None,
+    local_slot: torch.Tensor | None = None,
+    sm_scale: float | None = None,
+    num_splits: int | None = None,
+    out: torch.Tensor | None = None,
+    lse: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One-token-per-sequence attention over ``[older shared segment | local ring segment]``.
+
+    ``q`` is ``[B, Hq, 128]`` bf16 (or ``[B, Hq, 1, 128]``).  ``vscale`` ``[Hkv]`` fp32 switches
+    the older segment's V to ``bf16(V * vscale[h])``.  Returns ``out`` ``[B, Hq, 128]`` bf16.
+    """
+
+    _require_bf16_cuda("q", q)
+    if q.dim() == 4:
+        _require(q.shape[2] == 1, "decode_attention takes one query token per sequence")
+        q = q[:, :, 0]
+    _require(q.dim() == 3 and q.shape[-1] == HEAD_DIM, "q must be [B, Hq, 128]")
+    _require(q.stride(-1) == 1 and q.stride(1) == HEAD_DIM, "q heads must be contiguous rows of 128")
+    B, Hq, _ = q.shape
+    device = q.device
+    _require(older is not None or local is not None, "at least one key segment is required")
+    Hkv = (older if older is not None else local).heads
+    if older is not None and local is not None:
+        _require(older.heads == local.heads, "older and local caches have different kv head counts")
+    _require(Hq % Hkv == 0 and Hq // Hkv <= 16, "Hq must be a multiple of Hkv with group <= 16")
+    if out is None:
+        out = torch.empty((B, Hq, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    _require_bf16_cuda("out", out)
+    _require(out.shape[0] == B and out.shape[1] == Hq and out.shape[-1] == HEAD_DIM, "out shape mismatch")
+    _require(out.stride(-1) == 1 and out.stride(1) == HEAD_DIM, "out heads must be contiguous rows of 128")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() == B * Hq and lse.device == device,
+                 "lse must be a contiguous fp32 [B, Hq] tensor")
+    if vscale is not None:
+        _require(vscale.dtype == torch.float32 and vscale.numel() == Hkv and vscale.is_contiguous() and vscale.device == device,
+                 "vscale must be a contiguous fp32 [Hkv] tensor")
+    max_tokens = 0
+    if older is not None:
+        max_tokens += older.capacity_tokens if isinstance(older_len, torch.Tensor) else int(older_len)
+    if local is not None:
+        max_tokens += local.capacity_tokens if isinstance(local_len, torch.Tensor) else int(local_len)
+    if num_splits is None:
+        num_splits = default_decode_splits(B, Hkv, max_tokens, _cu_count(device))
+    lib = _lib.load()
+    need = lib.lkv_decode_workspace_bytes(B, Hq, num_splits)
+    if need > 0:
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=device)
+        _require(workspace.device == device and workspace.numel() * workspace.element_size() >= need, "workspace too small")
+
+    a = _lib.DecodeArgs()
+    a.struct_size = ctypes.sizeof(_lib.DecodeArgs)
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, HEAD_DIM
+    a.num_splits = num_splits
+    a.sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
+    a.older_vscale_mode = 1 if vscale is not None else 0
+    a.q, a.q_stride_b = q.data_ptr(), q.stride(0)
+    a.out, a.out_stride_b = out.data_ptr(), out.stride(0)
+    a.lse = _ptr(lse)
+    if older is not None:
+        _require(older.device == device, "older cache on another device")
+        a.older_k, a.older_v = older.k.data_ptr(), older.v.data_ptr()
+        a.older_seq_stride, a.older_head_stride = older.seq_stride, older.head_stride
+        a.older_len, a.older_len_const = _len_arg(older_len, B, "older_len", device)
+        a.older_capacity_tokens = older.capacity_tokens
+        a.older_slot = _ptr(older_slot)
+        a.older_num_slots = older.slots
+        if older_slot is None:
+            _require(older.slots >= B, "older cache has fewer slots than sequences")
+        if not isinstance(older_len, torch.Tensor):
+            _require(0 <= older_len <= older.capacity_tokens, "older_len exceeds the cache capacity")
+    if local is not None:
+        _require(local.device == device, "local cache on another device")
+        a.local_k, a.local_v = local.k.data_ptr(), local.v.data_ptr()
+        a.local_seq_stride, a.local_head_stride = local.seq_stride, local.head_stride
+        a.local_ring_blocks = local.blocks
+        a.local_len, a.local_len_const = _len_arg(local_len, B, "local_len", device)
+        a.local_start_block = _ptr(local_start_block)
+        a.local_slot = _ptr(local_slot)
+        a.local_num_slots = local.slots
+        if local_slot is None:
+            _require(local.slots >= B, "local cache has fewer slots than sequences")
+        if not isinstance(local_len, torch.Tensor):
+            _require(0 <= local_len <= local.capacity_tokens, "local_len exceeds the ring capacity")
+    for name, t in (("older_slot", older_slot), ("local_slot", local_slot), ("local_start_block", local_start_block)):
+        if t is not None:
+            _require(t.dtype == torch.int32 and t.device == device and t.numel() == B and t.is_contiguous(),
+                     f"{name} must be a contiguous int32 tensor of {B} entries on {device}")
+    a.vscale = _ptr(vscale)
+    a.workspace = _ptr(workspace)
+    a.workspace_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _lib.check(lib.lkv_decode_attn(ctypes.byref(a), _stream(device)), "lkv_decode_attn")
+    return out

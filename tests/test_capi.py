@@ -1,0 +1,72 @@
+"""The C-ABI library loads, exports every declared entry point and rejects bad arguments (no GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from lastkv_amd import _lib
+
+HEADERS = sorted((pathlib.Path(__file__).resolve().parents[1] / "include").glob("*.h"))
+
+
+def declared_functions() -> list[str]:
+    names = []
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names += re.findall(r"^[A-Za-z_][\w \*]*?\b(lkv_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert "lkv_decode_attn" in names and "lkv_cache_pack" in names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # and the Python binding types each of them
+    assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
+
+
+def test_abi_version_and_struct_size_guard():
+    lib = _lib.load()
+    assert lib.lkv_abi_version() == _lib.ABI_VERSION
+    a = _lib.DecodeArgs()
+    a.struct_size = ctypes.sizeof(a) - 8
+    assert lib.lkv_decode_attn(ctypes.byref(a), None) == 1
+    assert b"size mismatch" in lib.lkv_last_error()
+
+
+@pytest.mark.parametrize(
+    "field,value,message",
+    [
+        ("head_dim", 64, b"head_dim"),
+        ("num_kv_heads", 3, b"multiple"),
+        ("num_splits", 0, b"num_splits"),
+        ("older_vscale_mode", 1, b"vscale"),
+    ],
+)
+def test_decode_rejects_bad_arguments_before_any_launch(field, value, message):
+    lib = _lib.load()
+    a = _lib.DecodeArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.num_splits = 1, 8, 2, 128, 1
+    a.q = a.out = 16
+    setattr(a, field, value)
+    assert lib.lkv_decode_attn(ctypes.byref(a), None) == 1
+    assert message in lib.lkv_last_error()
+
+
+def test_decode_workspace_size():
+    lib = _lib.load()
+    assert lib.lkv_decode_workspace_bytes(32, 32, 1) == 0
+    assert lib.lkv_decode_workspace_bytes(32, 32, 4) == 32 * 32 * 4 * 130 * 4
+
+
+def test_pack_rejects_capacity_overflow():
+    lib = _lib.load()
+    st = lib.lkv_cache_pack(16, 0, 0, 128, 1, 1, 40, 0, 16, 0, 0, 0, 32, None)
+    assert st == 1 and b"capacity" in lib.lkv_last_error()

@@ -1,0 +1,195 @@
+"""GPU parity of the split-K shared-KV decode kernel (lkv_decode_attn) and the layout kernels.
+
+Tolerance (north star): attention outputs within max-abs 2e-2 and rel-L2 1e-3 in bf16 of the
+reference path evaluated on the same bf16 inputs.  "Reference path" here is the fp64 numpy
+oracle (small shapes) or the reference's torch composition + SDPA computed in fp32 on the GPU
+(full shapes); both outputs are rounded to bf16 before comparison, as the reference's output is.
+torch's own bf16 SDPA is also compared, within its measured deviation from the fp32 path.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from lastkv_amd import ops
+from oracle import attention as A
+from oracle import bf16, layout
+from oracle import reference_path as R
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+REL_L2 = 1e-3
+DEV = "cuda"
+
+
+def _bf(rng, shape, scale=1.0):
+    return bf16.round_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV, torch.bfloat16)
+
+
+def _close(actual: torch.Tensor, expected, label: str):
+    a = actual.float().cpu().numpy()
+    e = np.asarray(expected, np.float64)
+    ma, rl = A.max_abs(a, e), A.rel_l2(a, e)
+    print(f"{label}: max_abs={ma:.3e} rel_l2={rl:.3e}", flush=True)
+    assert ma <= MAX_ABS and rl <= REL_L2, f"{label}: max_abs={ma} rel_l2={rl}"
+    return ma, rl
+
+
+def test_pack_unpack_bit_exact_against_layout_oracle():
+    rng = np.random.default_rng(0)
+    x = _bf(rng, (2, 3, 77, 128))
+    for kind in (ops.KIND_K, ops.KIND_V):
+        cache = torch.zeros((2, 3, 4, 4096), dtype=torch.bfloat16, device=DEV)
+        ops.cache_pack(_t(x), cache, kind)
+        want = layout.pack(x, kind, 128)
+        assert np.array_equal(cache.float().cpu().numpy().view(np.uint32), want.view(np.uint32))
+        back = ops.cache_unpack(cache, kind, 0, 77)
+        assert np.array_equal(back.float().cpu().numpy(), x)
+        # offset write into a partially filled cache
+        ops.cache_pack(_t(x[:, :, :10]), cache, kind, token0=100)
+        assert np.array_equal(ops.cache_unpack(cache, kind, 100, 10).float().cpu().numpy(), x[:, :, :10])
+
+
+@pytest.mark.parametrize("tokens", [1, 31, 32, 33, 100, 1000])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_shared_only_decode_matches_oracle(tokens, splits):
+    rng = np.random.default_rng(tokens * 7 + splits)
+    B, Hq, Hkv = 3, 8, 2
+    q = _bf(rng, (B, Hq, 1, 128))
+    k = _bf(rng, (B, Hkv, tokens, 128))
+    v = _bf(rng, (B, Hkv, tokens, 128))
+    cap = -(-tokens // 32) * 32
+    cache = ops.TiledKV.zeros(B, Hkv, cap, DEV)
+    ops.pack_kv(_t(k), _t(v), cache)
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=DEV)
+    out = ops.decode_attention(_t(q), older=cache, older_len=tokens, num_splits=splits, lse=lse)
+    want, want_lse = A.attention(q, k, v)
+    _close(out, bf16.round_bf16(want[:, :, 0].astype(np.float32)), f"shared T={tokens} S={splits}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse[:, :, 0], rtol=1e-5, atol=1e-5)
+
+
+def _ring_case(rng, B, Hq, Hkv, chunk, position):
+    """Random final-layer history, this layer's previous/current chunks and parameters."""
+
+    r = A.plan_regions(position, chunk)
+    rec, cur = r.recent[0], r.current[0]
+    deep_k, deep_v = _bf(rng, (B, Hkv, cur, 128)), _bf(rng, (B, Hkv, cur, 128))
+    prev = (_bf(rng, (B, Hkv, chunk, 128)), _bf(rng, (B, Hkv, chunk, 128))) if cur else None
+    n_cur = position + 1 - cur
+    cur_kv = (_bf(rng, (B, Hkv, n_cur, 128)), _bf(rng, (B, Hkv, n_cur, 128)))
+    logits = bf16.round_bf16(rng.standard_normal(Hkv).astype(np.float32))
+    scale = bf16.round_bf16(rng.uniform(0.3, 1.3, Hkv).astype(np.float32))
+    q = _bf(rng, (B, Hq, 1, 128))
+    return r, deep_k, deep_v, prev, cur_kv, logits, scale, q
+
+
+def _ring_inputs(r, deep_k, deep_v, prev, cur_kv, logits, scale, chunk, B, Hkv):
+    """Build the kernel's caches: shared older history + the layer ring [recent blend | current]."""
+
+    rec, cur = r.recent[0], r.current[0]
+    older = ops.TiledKV.zeros(B, Hkv, max(32, -(-cur // 32) * 32), DEV)
+    if cur:
+        ops.pack_kv(_t(deep_k), _t(deep_v), older)
+    ring = ops.TiledKV.zeros(B, Hkv, 2 * chunk, DEV)
+    if cur:
+        # the boundary commit materialises the recent blend once (bf16, reference op order)
+        rk = A.blend_chunk_bf16(deep_k[:, :, rec:cur], prev[0], logits)
+        rv = A.blend_chunk_bf16(deep_v[:, :, rec:cur], prev[1], logits, scale)
+        ops.pack_kv(_t(rk), _t(rv), ring, token0=rec % (2 * chunk))
+    ops.pack_kv(_t(cur_kv[0]), _t(cur_kv[1]), ring, token0=cur % (2 * chunk))
+    start = torch.full((B,), (rec % (2 * chunk)) // 32, dtype=torch.int32, device=DEV)
+    return older, ring, start
+
+
+@pytest.mark.parametrize("position", [5, 63, 64, 100, 200, 300, 511])
+def test_lastkv_region_decode_matches_oracle(position):
+    rng = np.random.default_rng(position)
+    B, Hq, Hkv, C = 2, 8, 2, 64
+    r, deep_k, deep_v, prev, cur_kv, logits, scale, q = _ring_case(rng, B, Hq, Hkv, C, position)
+    older, ring, start = _ring_inputs(r, deep_k, deep_v, prev, cur_kv, logits, scale, C, B, Hkv)
+    rec = r.recent[0]
+    out = ops.decode_attention(
+        _t(q), older=older, older_len=rec, vscale=torch.from_numpy(scale).to(DEV),
+        local=ring, local_len=position + 1 - rec, local_start_block=start, num_splits=2,
+    )
+    full_k, full_v = A.compose_history_bf16(deep_k, deep_v, prev and prev[0], prev and prev[1], cur_kv[0], cur_kv[1],
+                                            logits, scale, C)
+    want, _ = A.attention(q, full_k, full_v)
+    _close(out, bf16.round_bf16(want[:, :, 0].astype(np.float32)), f"regions p={position}")
+    # the reference's torch path on the GPU, composed from the same pieces
+    tdeep = (_t(deep_k), _t(deep_v)) if r.current[0] else None
+    tprev = (_t(prev[0]), _t(prev[1])) if prev is not None else None
+    ref32 = R.lastkv_attention(_t(q), tdeep, tprev, (_t(cur_kv[0]), _t(cur_kv[1])), torch.from_numpy(logits).to(DEV),
+                               torch.from_numpy(scale).to(DEV), C, compute_dtype=torch.float32)
+    _close(out, ref32[:, :, 0].float().cpu().numpy(), f"regions p={position} vs torch fp32 path")
+
+
+def test_ragged_batch_with_device_lengths_and_slots():
+    rng = np.random.default_rng(11)
+    B, Hq, Hkv, cap = 5, 16, 4, 256
+    lens = np.array([1, 255, 64, 0, 130], np.int32)
+    slots = np.array([4, 0, 2, 1, 3], np.int32)
+    kv = [(_bf(rng, (1, Hkv, cap, 128)), _bf(rng, (1, Hkv, cap, 128))) for _ in range(5)]
+    cache = ops.TiledKV.zeros(5, Hkv, cap, DEV)
+    for s in range(5):
+        ops.cache_pack(_t(kv[s][0]), cache.k[s:s + 1], ops.KIND_K)
+        ops.cache_pack(_t(kv[s][1]), cache.v[s:s + 1], ops.KIND_V)
+    q = _bf(rng, (B, Hq, 1, 128))
+    out = ops.decode_attention(_t(q), older=cache, older_len=torch.from_numpy(lens).to(DEV),
+                               older_slot=torch.from_numpy(slots).to(DEV), num_splits=3)
+    for b in range(B):
+        s, n = slots[b], lens[b]
+        if n == 0:
+            assert torch.count_nonzero(out[b]) == 0
+            continue
+        want, _ = A.attention(q[b:b + 1], kv[s][0][:, :, :n], kv[s][1][:, :, :n])
+        _close(out[b:b + 1], bf16.round_bf16(want[:, :, 0].astype(np.float32)), f"ragged b={b} n={n}")
+    # an out-of-range slot reads nothing and yields zeros instead of faulting
+    bad = torch.tensor([7, 0, 2, 1, 3], dtype=torch.int32, device=DEV)
+    out = ops.decode_attention(_t(q), older=cache, older_len=torch.from_numpy(lens).to(DEV), older_slot=bad)
+    assert torch.count_nonzero(out[0]) == 0
+
+
+@pytest.fixture(scope="module")
+def config2():
+    """q [32, 32, 1, 128], one shared K/V [32, 8, 8192, 128], N(0, 1) bf16."""
+
+    g = torch.Generator(device=DEV).manual_seed(2)
+    k = torch.randn((32, 8, 8192, 128), generator=g, device=DEV).bfloat16()
+    v = torch.randn((32, 8, 8192, 128), generator=g, device=DEV).bfloat16()
+    q = torch.randn((32, 32, 1, 128), generator=g, device=DEV).bfloat16()
+    cache = ops.TiledKV.zeros(32, 8, 8192, DEV)
+    ops.pack_kv(k, v, cache)
+    return q, k, v, cache
+
+
+def test_config2_full_size_matches_reference_sdpa(config2):
+    q, k, v, cache = config2
+    out = ops.decode_attention(q, older=cache, older_len=8192)
+    ref32 = R.sdpa_bottom_right(q, k, v, compute_dtype=torch.float32)[:, :, 0]
+    _close(out, ref32.float().cpu().numpy(), "config2 vs fp32 SDPA")
+    ref16 = R.sdpa_bottom_right(q, k, v)[:, :, 0]
+    sdpa_dev = A.rel_l2(ref16.float().cpu().numpy(), ref32.float().cpu().numpy())
+    ours = A.rel_l2(out.float().cpu().numpy(), ref16.float().cpu().numpy())
+    print(f"config2: torch bf16 SDPA vs fp32 rel_l2={sdpa_dev:.3e}; ours vs torch bf16 rel_l2={ours:.3e}", flush=True)
+    assert ours <= max(REL_L2, 1.5 * sdpa_dev)
+    assert A.max_abs(out.float().cpu().numpy(), ref16.float().cpu().numpy()) <= MAX_ABS
+
+
+def test_config2_split_invariance_and_power_of_two_vscale_linearity(config2):
+    q, _, _, cache = config2
+    base = ops.decode_attention(q, older=cache, older_len=8192, num_splits=1)
+    for splits in (2, 8, 64):
+        other = ops.decode_attention(q, older=cache, older_len=8192, num_splits=splits)
+        _close(other, base.float().cpu().numpy(), f"config2 splits={splits} vs 1")
+    # s = 2 is exact in bf16 and commutes with every fp32 rounding: out(2V) == 2 out(V) bitwise
+    two = torch.full((8,), 2.0, dtype=torch.float32, device=DEV)
+    scaled = ops.decode_attention(q, older=cache, older_len=8192, vscale=two, num_splits=1)
+    assert torch.equal(scaled, base * 2)
