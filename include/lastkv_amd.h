@@ -74,8 +74,8 @@ int32_t lkv_cache_unpack(const void *src, int64_t src_seq_stride, int64_t src_he
  *           with older_vscale_mode 1 its V is used as bf16(V * vscale[h]), the reference's
  *           _scale() (modeling.py:93-96); with mode 0 V is used as stored.
  *   local : local_len[b] tokens of a per-layer ring of local_ring_blocks blocks starting at
- *           ring block local_start_block[b] (wrapping), e.g. the recent (already blended)
- *           chunk followed by the current chunk.
+ *           ring token local_start[b] (wrapping at 32 * local_ring_blocks), e.g. the recent
+ *           (already blended) chunk followed by the current chunk.
  * out[b, h, :] = softmax(q[b, h] . K^T * sm_scale) V for query head h, GQA group
  * Hq / Hkv <= 16 (query head h reads kv head h / group).  Optional lse[b * Hq + h] receives the
  * natural-log log-sum-exp of the scaled scores (-inf when there are no keys).
@@ -116,7 +116,8 @@ typedef struct lkv_decode_args {
   int32_t local_ring_blocks;
   int32_t local_len_const;
   const int32_t *local_len;         /* device [B] or NULL -> local_len_const */
-  const int32_t *local_start_block; /* device [B] or NULL -> 0 */
+  const int32_t *local_start;       /* device [B] ring token or NULL -> local_start_const */
+  int32_t local_start_const;
   const int32_t *local_slot;        /* device [B] or NULL -> slot b */
   int32_t local_num_slots;          /* slots addressable through local_slot */
   void *workspace;
@@ -126,6 +127,147 @@ typedef struct lkv_decode_args {
 int64_t lkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_splits);
 
 int32_t lkv_decode_attn(const lkv_decode_args *args, lkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Chunked-prefill attention (L >= 1 query tokens per sequence, MFMA).
+ *
+ * Replaces, for prefill calls (Lq > 1): the region composition + masked SDPA of
+ * LastKVAttention.forward (modeling.py:109-146, bottom-right causal mask :124-130), the merged
+ * FA3 varlen call of the serving fast path over [older pages | ring pages] (fastpath.py:644-651),
+ * and, with causal = 0, the Wan block attention over [history | current block] whose current
+ * block is bidirectional (videogen/src/lastkv/videogen/attention.py:9-32).
+ * Query token i of sequence b (q[b, i, h, :], bf16 [B, L, Hq, 128]) attends to the older
+ * segment (all of it) and to local tokens [0, local_len[b] - L + i] (causal = 1) or to all
+ * local tokens (causal = 0); the last L local tokens are the queries' own K/V.  Segments,
+ * slots, clamping and vscale are as in lkv_decode_args.  out is bf16 [B, L, Hq, 128]; optional
+ * lse is fp32 [B, L, Hq] (natural log).  P*V runs in fp16, which represents bf16 V exactly for
+ * |V| < 65504 (larger magnitudes saturate).
+ * ------------------------------------------------------------------------------------- */
+typedef struct lkv_prefill_args {
+  int32_t struct_size; /* sizeof(lkv_prefill_args) */
+  int32_t batch;
+  int32_t tokens; /* L */
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim; /* must be 128 */
+  float sm_scale;
+  int32_t causal;
+  int32_t older_vscale_mode;
+  const void *q;
+  int64_t q_stride_b;
+  int64_t q_stride_t;
+  void *out;
+  int64_t out_stride_b;
+  int64_t out_stride_t;
+  float *lse;
+  const void *older_k;
+  const void *older_v;
+  int64_t older_seq_stride;
+  int64_t older_head_stride;
+  const int32_t *older_len;
+  int32_t older_len_const;
+  int32_t older_capacity_tokens;
+  const int32_t *older_slot;
+  int32_t older_num_slots;
+  const float *vscale;
+  const void *local_k;
+  const void *local_v;
+  int64_t local_seq_stride;
+  int64_t local_head_stride;
+  int32_t local_ring_blocks;
+  int32_t local_len_const;
+  const int32_t *local_len;
+  const int32_t *local_start;
+  int32_t local_start_const;
+  const int32_t *local_slot;
+  int32_t local_num_slots;
+} lkv_prefill_args;
+
+int32_t lkv_prefill_attn(const lkv_prefill_args *args, lkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Fused per-layer QKV epilogue: RoPE, q/k RMSNorm and the K/V cache append in one launch.
+ *
+ * Replaces modeling.py:103-108 (apply_rotary_pos_emb, q_norm / k_norm, append of the new K/V to
+ * current[l]) and, on the serving path, fused_qkv.py:58-126 (_fused_qkv_kernel: rotary + RMSNorm
+ * + ring / slab K,V writes).  Arithmetic follows the torch op order of the reference's bf16
+ * model: rope = bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)); norm = bf16(w * bf16(x * r)) with
+ * r = 1 / sqrt(mean(x^2) + eps) in fp32 (transformers LlamaRMSNorm, modeling.py:90-91).
+ * For new token i of sequence b at cache position p = pos(b) + i (pos(b) = positions[b], or
+ * position_const when positions is NULL):
+ *   q_out[b, i, h, :] = norm_q(rope(q[b, i, h, :]))                  for h < Hq
+ *   K = norm_k(rope(k[b, i, g, :])); V = v[b, i, g, :]               for g < Hkv
+ *   ring (tiled, ring_tokens a multiple of 32): token p mod ring_tokens of (ring slot, g) := K, V
+ *   deep (optional, tiled): token p of (deep slot, g) := K, V            (the final layer)
+ * cos/sin are bf16 [Bc, L, 128] with Bc in {1, B} (cs_stride_b 0 broadcasts), as produced by the
+ * model's rotary embedding for positions p.  q_norm_w / k_norm_w NULL skips that norm.
+ * Writes to positions outside the deep capacity are dropped.
+ * ------------------------------------------------------------------------------------- */
+typedef struct lkv_qkv_args {
+  int32_t struct_size;
+  int32_t batch;
+  int32_t tokens; /* new tokens per sequence, L */
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim; /* must be 128 */
+  float eps;
+  int32_t position_const;
+  const int32_t *positions; /* device [B] or NULL */
+  const void *q;            /* bf16, row (b, i) at b * q_stride_b + i * q_stride_t, heads contiguous */
+  int64_t q_stride_b;
+  int64_t q_stride_t;
+  const void *k;
+  int64_t k_stride_b;
+  int64_t k_stride_t;
+  const void *v;
+  int64_t v_stride_b;
+  int64_t v_stride_t;
+  const void *cos;
+  const void *sin;
+  int64_t cs_stride_b;
+  int64_t cs_stride_t;
+  const void *q_norm_w; /* bf16 [128] or NULL */
+  const void *k_norm_w; /* bf16 [128] or NULL */
+  void *q_out;          /* bf16 [B, L, Hq, 128] */
+  int64_t q_out_stride_b;
+  int64_t q_out_stride_t;
+  void *ring_k;
+  void *ring_v;
+  int64_t ring_seq_stride;
+  int64_t ring_head_stride;
+  int32_t ring_tokens;
+  int32_t ring_num_slots;
+  const int32_t *ring_slot; /* device [B] or NULL -> slot b */
+  void *deep_k;             /* NULL: no deep write */
+  void *deep_v;
+  int64_t deep_seq_stride;
+  int64_t deep_head_stride;
+  int32_t deep_capacity_tokens;
+  int32_t deep_num_slots;
+  const int32_t *deep_slot; /* device [B] or NULL -> slot b */
+} lkv_qkv_args;
+
+int32_t lkv_qkv_epilogue(const lkv_qkv_args *args, lkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Chunk-boundary commit: materialise the recent-chunk blend of every layer once.
+ *
+ * Replaces the per-step recomputation of modeling.py:116-119 and the serving commit
+ * fused_qkv.py:158-201 (blend_chunk_) / batching.py:1099-1155 (_commit_previous_boundary).
+ * For layer l < layers, sequence b < batch, kv head g and tokens p in
+ * [chunk_start, chunk_start + chunk_len), with a = alpha[l*Hkv+g], om = one_minus_alpha[..],
+ * s = vscale[..] (bf16 values carried as fp32; vscale NULL means s = 1):
+ *   ringK[l][b][g][p mod R] = bf16(bf16(a * deepK[b][g][p]) + bf16(om * ringK[l][b][g][p mod R]))
+ *   ringV[l][b][g][p mod R] = bf16(bf16(a * bf16(deepV[b][g][p] * s)) + bf16(om * ringV[..]))
+ * which is the reference's bf16 expression evaluated op by op.  Both caches are tiled; R =
+ * ring_tokens (a multiple of 32).  Layer l's ring is ring + l * ring_layer_stride.
+ * ------------------------------------------------------------------------------------- */
+int32_t lkv_blend_chunk(int32_t layers, int32_t batch, int32_t kv_heads, int32_t chunk_start, int32_t chunk_len,
+                        void *ring_k, void *ring_v, int64_t ring_layer_stride, int64_t ring_seq_stride,
+                        int64_t ring_head_stride, int32_t ring_tokens, const void *deep_k, const void *deep_v,
+                        int64_t deep_seq_stride, int64_t deep_head_stride, int32_t deep_capacity_tokens,
+                        const float *alpha, const float *one_minus_alpha, const float *vscale,
+                        lkv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -58,11 +58,104 @@ class DecodeArgs(ctypes.Structure):
         ("local_ring_blocks", c_i32),
         ("local_len_const", c_i32),
         ("local_len", c_ptr),
-        ("local_start_block", c_ptr),
+        ("local_start", c_ptr),
+        ("local_start_const", c_i32),
         ("local_slot", c_ptr),
         ("local_num_slots", c_i32),
         ("workspace", c_ptr),
         ("workspace_bytes", c_i64),
+    ]
+
+
+class PrefillArgs(ctypes.Structure):
+    """Mirror of ``lkv_prefill_args``."""
+
+    _fields_ = [
+        ("struct_size", c_i32),
+        ("batch", c_i32),
+        ("tokens", c_i32),
+        ("num_q_heads", c_i32),
+        ("num_kv_heads", c_i32),
+        ("head_dim", c_i32),
+        ("sm_scale", c_f32),
+        ("causal", c_i32),
+        ("older_vscale_mode", c_i32),
+        ("q", c_ptr),
+        ("q_stride_b", c_i64),
+        ("q_stride_t", c_i64),
+        ("out", c_ptr),
+        ("out_stride_b", c_i64),
+        ("out_stride_t", c_i64),
+        ("lse", c_ptr),
+        ("older_k", c_ptr),
+        ("older_v", c_ptr),
+        ("older_seq_stride", c_i64),
+        ("older_head_stride", c_i64),
+        ("older_len", c_ptr),
+        ("older_len_const", c_i32),
+        ("older_capacity_tokens", c_i32),
+        ("older_slot", c_ptr),
+        ("older_num_slots", c_i32),
+        ("vscale", c_ptr),
+        ("local_k", c_ptr),
+        ("local_v", c_ptr),
+        ("local_seq_stride", c_i64),
+        ("local_head_stride", c_i64),
+        ("local_ring_blocks", c_i32),
+        ("local_len_const", c_i32),
+        ("local_len", c_ptr),
+        ("local_start", c_ptr),
+        ("local_start_const", c_i32),
+        ("local_slot", c_ptr),
+        ("local_num_slots", c_i32),
+    ]
+
+
+class QkvArgs(ctypes.Structure):
+    """Mirror of ``lkv_qkv_args``."""
+
+    _fields_ = [
+        ("struct_size", c_i32),
+        ("batch", c_i32),
+        ("tokens", c_i32),
+        ("num_q_heads", c_i32),
+        ("num_kv_heads", c_i32),
+        ("head_dim", c_i32),
+        ("eps", c_f32),
+        ("position_const", c_i32),
+        ("positions", c_ptr),
+        ("q", c_ptr),
+        ("q_stride_b", c_i64),
+        ("q_stride_t", c_i64),
+        ("k", c_ptr),
+        ("k_stride_b", c_i64),
+        ("k_stride_t", c_i64),
+        ("v", c_ptr),
+        ("v_stride_b", c_i64),
+        ("v_stride_t", c_i64),
+        ("cos", c_ptr),
+        ("sin", c_ptr),
+        ("cs_stride_b", c_i64),
+        ("cs_stride_t", c_i64),
+        ("q_norm_w", c_ptr),
+        ("k_norm_w", c_ptr),
+        ("q_out", c_ptr),
+        ("q_out_stride_b", c_i64),
+        ("q_out_stride_t", c_i64),
+        ("ring_k", c_ptr),
+        ("ring_v", c_ptr),
+        ("ring_seq_stride", c_i64),
+        ("ring_head_stride", c_i64),
+        ("ring_tokens", c_i32),
+        ("ring_num_slots", c_i32),
+        ("ring_slot", c_ptr),
+        ("deep_k", c_ptr),
+        ("deep_v", c_ptr),
+        ("deep_seq_stride", c_i64),
+        ("deep_head_stride", c_i64),
+        ("deep_capacity_tokens", c_i32),
+        ("deep_num_slots", c_i32),
+        ("deep_slot", c_ptr),
     ]
 
 
@@ -80,6 +173,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "lkv_decode_workspace_bytes": (c_i64, [c_i32, c_i32, c_i32]),
     "lkv_decode_attn": (c_i32, [ctypes.POINTER(DecodeArgs), c_ptr]),
+    "lkv_prefill_attn": (c_i32, [ctypes.POINTER(PrefillArgs), c_ptr]),
+    "lkv_qkv_epilogue": (c_i32, [ctypes.POINTER(QkvArgs), c_ptr]),
+    "lkv_blend_chunk": (
+        c_i32,
+        [c_i32, c_i32, c_i32, c_i32, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_i64, c_i64,
+         c_i32, c_ptr, c_ptr, c_ptr, c_ptr],
+    ),
 }
 
 _lock = threading.Lock()

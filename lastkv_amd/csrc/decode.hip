@@ -12,6 +12,7 @@
 // The waves of a workgroup merge their (m, l, O) states through LDS.  With one split the
 // workgroup writes the normalised bf16 output; otherwise it writes an unnormalised partial
 // state and lkv_decode_combine merges the splits.
+#include "attn_common.h"
 #include "common.h"
 #include "runtime.h"
 
@@ -42,6 +43,7 @@ struct DecodeParams {
   const int32_t* l_len;
   int32_t l_len_c;
   const int32_t* l_start;
+  int32_t l_start_c;
   const int32_t* l_slot;
   int32_t l_nslots;
   float* ws_o;
@@ -55,40 +57,6 @@ struct BlockFrags {
   uint4 v[8];
 };
 
-struct BlockRef {
-  const uint16_t* k;
-  const uint16_t* v;
-  int valid;
-  bool older;
-};
-
-struct SeqView {
-  const uint16_t* ok;
-  const uint16_t* ov;
-  const uint16_t* lk;
-  const uint16_t* lv;
-  int n0, n1, nb0, lstart, ring_blocks;
-};
-
-__device__ inline BlockRef block_ref(const SeqView& s, int blk) {
-  BlockRef r;
-  if (blk < s.nb0) {
-    r.k = s.ok + static_cast<int64_t>(blk) * kBlockElems;
-    r.v = s.ov + static_cast<int64_t>(blk) * kBlockElems;
-    r.valid = min(kBlockTokens, s.n0 - blk * kBlockTokens);
-    r.older = true;
-  } else {
-    const int j = blk - s.nb0;
-    int rb = s.lstart + j;
-    if (rb >= s.ring_blocks) rb -= s.ring_blocks;
-    r.k = s.lk + static_cast<int64_t>(rb) * kBlockElems;
-    r.v = s.lv + static_cast<int64_t>(rb) * kBlockElems;
-    r.valid = min(kBlockTokens, s.n1 - j * kBlockTokens);
-    r.older = false;
-  }
-  return r;
-}
-
 __device__ inline void load_block(BlockFrags& f, const BlockRef& r, int n16, int g4) {
 #pragma unroll
   for (int u = 0; u < 2; ++u)
@@ -97,16 +65,6 @@ __device__ inline void load_block(BlockFrags& f, const BlockRef& r, int n16, int
       f.k[u][kb] = *reinterpret_cast<const uint4*>(r.k + ((u * 4 + kb) * 16 + n16) * 32 + 8 * g4);
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) f.v[nb] = *reinterpret_cast<const uint4*>(r.v + (16 * nb + n16) * 32 + 8 * g4);
-}
-
-// bf16(v * s) for the 8 bf16 values of one fragment (the reference materialises s * V in bf16).
-__device__ inline uint4 scale_frag(uint4 v, float s) {
-  uint4 r;
-  r.x = pack_bf16x2(bf16_lo(v.x) * s, bf16_hi(v.x) * s);
-  r.y = pack_bf16x2(bf16_lo(v.y) * s, bf16_hi(v.y) * s);
-  r.z = pack_bf16x2(bf16_lo(v.z) * s, bf16_hi(v.z) * s);
-  r.w = pack_bf16x2(bf16_lo(v.w) * s, bf16_hi(v.w) * s);
-  return r;
 }
 
 struct SoftmaxState {
@@ -130,10 +88,10 @@ __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, con
     s[i] = s0[i] * scale_log2;
     s[4 + i] = s1[i] * scale_log2;
   }
-  if (r.valid < kBlockTokens) {
+  if (r.lo > 0 || r.hi < kBlockTokens) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (8 * g4 + j >= r.valid) s[j] = kNegInf;
+      if (8 * g4 + j < r.lo || 8 * g4 + j >= r.hi) s[j] = kNegInf;
   }
   float mx = s[0];
 #pragma unroll
@@ -208,8 +166,8 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     int n1 = p.lk ? (p.l_len ? p.l_len[b] : p.l_len_c) : 0;
     n0 = (oslot < 0 || oslot >= p.o_nslots || p.ok == nullptr) ? 0 : min(max(n0, 0), p.o_cap);
     n1 = (lslot < 0 || lslot >= p.l_nslots) ? 0 : min(max(n1, 0), p.ring_blocks * kBlockTokens);
-    int ls = p.l_start ? p.l_start[b] : 0;
-    ls = (ls < 0 || ls >= p.ring_blocks) ? 0 : ls;
+    int ls = p.l_start ? p.l_start[b] : p.l_start_c;
+    ls = (ls < 0 || ls >= p.ring_blocks * kBlockTokens) ? 0 : ls;
     sv.ok = p.ok ? p.ok + static_cast<int64_t>(oslot) * p.o_ss + kvh * p.o_hs : nullptr;
     sv.ov = p.ov ? p.ov + static_cast<int64_t>(oslot) * p.o_ss + kvh * p.o_hs : nullptr;
     sv.lk = p.lk ? p.lk + static_cast<int64_t>(lslot) * p.l_ss + kvh * p.l_hs : nullptr;
@@ -217,10 +175,11 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     sv.n0 = n0;
     sv.n1 = n1;
     sv.nb0 = (n0 + kBlockTokens - 1) / kBlockTokens;
-    sv.lstart = ls;
+    sv.lblk0 = ls >> 5;
+    sv.lead = ls & (kBlockTokens - 1);
     sv.ring_blocks = p.ring_blocks;
   }
-  const int nbt = sv.nb0 + (sv.n1 + kBlockTokens - 1) / kBlockTokens;
+  const int nbt = sv.nb0 + (sv.n1 > 0 ? (sv.lead + sv.n1 + kBlockTokens - 1) / kBlockTokens : 0);
   const int bps = (nbt + p.splits - 1) / p.splits;
   const int blk_begin = split * bps;
   const int blk_end = min(blk_begin + bps, nbt);
@@ -396,7 +355,8 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   p.ring_blocks = a->local_k ? a->local_ring_blocks : 1;
   p.l_len = a->local_len;
   p.l_len_c = a->local_len_const;
-  p.l_start = a->local_start_block;
+  p.l_start = a->local_start;
+  p.l_start_c = a->local_start_const;
   p.l_slot = a->local_slot;
   p.l_nslots = a->local_num_slots;
   p.ws_o = static_cast<float*>(a->workspace);

@@ -1,0 +1,285 @@
+// Fused QKV epilogue (RoPE + q/k RMSNorm + tiled K/V cache append) and the chunk-boundary blend.
+//
+// Epilogue: one wave per (token, head) of the Hq + Hkv heads; lane l owns dims l and l + 64, the
+// two halves that rotate_half pairs, so RoPE needs no lane exchange and RMSNorm one wave sum.
+// Every intermediate is rounded to bf16 where the reference's bf16 torch ops round.
+#include "common.h"
+#include "runtime.h"
+
+namespace lkv {
+namespace {
+
+// Value of the bf16 nearest to x (round to nearest even), as fp32.
+__device__ inline float rb(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+
+__device__ inline float wave_sum64(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+struct QkvParams {
+  int32_t batch, tokens, hq, hkv;
+  float eps;
+  int32_t pos_c;
+  const int32_t* pos;
+  const uint16_t *q, *k, *v;
+  int64_t q_sb, q_st, k_sb, k_st, v_sb, v_st;
+  const uint16_t *cos, *sin;
+  int64_t cs_sb, cs_st;
+  const uint16_t *qw, *kw;
+  uint16_t* q_out;
+  int64_t qo_sb, qo_st;
+  uint16_t *rk, *rv;
+  int64_t r_ss, r_hs;
+  int32_t ring_tokens, ring_slots;
+  const int32_t* ring_slot;
+  uint16_t *dk, *dv;
+  int64_t d_ss, d_hs;
+  int32_t deep_cap, deep_slots;
+  const int32_t* deep_slot;
+};
+
+__global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
+  const int lane = threadIdx.x & 63;
+  const int heads = p.hq + p.hkv;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= static_cast<int64_t>(p.batch) * p.tokens * heads) return;
+  const int h = static_cast<int>(item % heads);
+  const int64_t tok = item / heads;
+  const int i = static_cast<int>(tok % p.tokens);
+  const int b = static_cast<int>(tok / p.tokens);
+  const bool is_q = h < p.hq;
+  const int g = h - p.hq;
+  const uint16_t* src = is_q ? p.q + b * p.q_sb + i * p.q_st + static_cast<int64_t>(h) * kHeadDim
+                             : p.k + b * p.k_sb + i * p.k_st + static_cast<int64_t>(g) * kHeadDim;
+  const float x0 = bf16_bits_to_f32(src[lane]);
+  const float x1 = bf16_bits_to_f32(src[lane + 64]);
+  const uint16_t* cp = p.cos + b * p.cs_sb + i * p.cs_st;
+  const uint16_t* sp = p.sin + b * p.cs_sb + i * p.cs_st;
+  const float c0 = bf16_bits_to_f32(cp[lane]), c1 = bf16_bits_to_f32(cp[lane + 64]);
+  const float s0 = bf16_bits_to_f32(sp[lane]), s1 = bf16_bits_to_f32(sp[lane + 64]);
+  // q * cos + rotate_half(q) * sin, rotate_half(q) = cat(-q[64:], q[:64]); three bf16 roundings
+  float r0 = rb(rb(x0 * c0) + rb(-x1 * s0));
+  float r1 = rb(rb(x1 * c1) + rb(x0 * s1));
+  const uint16_t* w = is_q ? p.qw : p.kw;
+  if (w != nullptr) {
+    const float ss = wave_sum64(r0 * r0 + r1 * r1);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHeadDim) + p.eps);
+    r0 = rb(bf16_bits_to_f32(w[lane]) * rb(r0 * inv));
+    r1 = rb(bf16_bits_to_f32(w[lane + 64]) * rb(r1 * inv));
+  }
+  const uint16_t o0 = f32_to_bf16_bits(r0), o1 = f32_to_bf16_bits(r1);
+  if (is_q) {
+    uint16_t* dst = p.q_out + b * p.qo_sb + i * p.qo_st + static_cast<int64_t>(h) * kHeadDim;
+    dst[lane] = o0;
+    dst[lane + 64] = o1;
+    return;
+  }
+  const int position = (p.pos ? p.pos[b] : p.pos_c) + i;
+  if (position < 0) return;
+  const uint16_t* vrow = p.v + b * p.v_sb + i * p.v_st + static_cast<int64_t>(g) * kHeadDim;
+  const uint16_t v0 = vrow[lane], v1 = vrow[lane + 64];
+  {
+    const int slot = p.ring_slot ? p.ring_slot[b] : b;
+    if (slot >= 0 && slot < p.ring_slots) {
+      const int rt = position % p.ring_tokens;
+      uint16_t* kb = p.rk + slot * p.r_ss + g * p.r_hs + static_cast<int64_t>(rt >> 5) * kBlockElems;
+      uint16_t* vb = p.rv + slot * p.r_ss + g * p.r_hs + static_cast<int64_t>(rt >> 5) * kBlockElems;
+      const int wt = rt & 31;
+      kb[k_tile_offset(wt, lane)] = o0;
+      kb[k_tile_offset(wt, lane + 64)] = o1;
+      vb[v_tile_offset(wt, lane)] = v0;
+      vb[v_tile_offset(wt, lane + 64)] = v1;
+    }
+  }
+  if (p.dk != nullptr && position < p.deep_cap) {
+    const int slot = p.deep_slot ? p.deep_slot[b] : b;
+    if (slot >= 0 && slot < p.deep_slots) {
+      uint16_t* kb = p.dk + slot * p.d_ss + g * p.d_hs + static_cast<int64_t>(position >> 5) * kBlockElems;
+      uint16_t* vb = p.dv + slot * p.d_ss + g * p.d_hs + static_cast<int64_t>(position >> 5) * kBlockElems;
+      const int wt = position & 31;
+      kb[k_tile_offset(wt, lane)] = o0;
+      kb[k_tile_offset(wt, lane + 64)] = o1;
+      vb[v_tile_offset(wt, lane)] = v0;
+      vb[v_tile_offset(wt, lane + 64)] = v1;
+    }
+  }
+}
+
+struct BlendParams {
+  int32_t layers, batch, heads;
+  int32_t start, end;  // chunk tokens [start, end)
+  int32_t blk0, nblk;  // blocks covering the chunk
+  uint16_t *rk, *rv;
+  int64_t r_ls, r_ss, r_hs;
+  int32_t ring_tokens;
+  const uint16_t *dk, *dv;
+  int64_t d_ss, d_hs;
+  const float *alpha, *om, *vs;
+};
+
+// One thread per 8-element (16-byte) run of one block of one (layer, sequence, head).  K and
+// V runs are handled by separate threads (kind = item parity).
+__global__ __launch_bounds__(256) void blend_kernel(const BlendParams p) {
+  const int64_t per_block = kBlockElems / 8;
+  const int64_t total = static_cast<int64_t>(p.layers) * p.batch * p.heads * p.nblk * per_block * 2;
+  for (int64_t item = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; item < total;
+       item += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int kind = static_cast<int>(item & 1);
+    int64_t rest = item >> 1;
+    const int run = static_cast<int>(rest % per_block);
+    rest /= per_block;
+    const int blk = p.blk0 + static_cast<int>(rest % p.nblk);
+    rest /= p.nblk;
+    const int g = static_cast<int>(rest % p.heads);
+    rest /= p.heads;
+    const int b = static_cast<int>(rest % p.batch);
+    const int l = static_cast<int>(rest / p.batch);
+    const int off = run * 8;
+    const int base_tok = blk * kBlockTokens;
+    const int ring_blk = (base_tok % p.ring_tokens) >> 5;
+    const int lh = l * p.heads + g;
+    const float a = p.alpha[lh], om = p.om[lh];
+    const float s = (kind == 1 && p.vs != nullptr) ? p.vs[lh] : 1.f;
+    const uint16_t* dsrc = (kind == 0 ? p.dk : p.dv) + b * p.d_ss + g * p.d_hs +
+                           static_cast<int64_t>(blk) * kBlockElems + off;
+    uint16_t* rdst = (kind == 0 ? p.rk : p.rv) + l * p.r_ls + b * p.r_ss + g * p.r_hs +
+                     static_cast<int64_t>(ring_blk) * kBlockElems + off;
+    const uint4 dv4 = *reinterpret_cast<const uint4*>(dsrc);
+    uint4 rv4 = *reinterpret_cast<const uint4*>(rdst);
+    const uint16_t* de = reinterpret_cast<const uint16_t*>(&dv4);
+    uint16_t* re = reinterpret_cast<uint16_t*>(&rv4);
+    // token index of each element of the run: K runs hold 8 dims of one token, V runs 8 tokens
+    int w_k = 0;
+    if (kind == 0) {
+      const int r = (off >> 5) & 15, u = (off >> 11) & 1;
+      w_k = 8 * (r >> 2) + 4 * u + (r & 3);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int tokpos = base_tok + (kind == 0 ? w_k : ((off & 31) + j));
+      if (tokpos < p.start || tokpos >= p.end) continue;
+      const float src = bf16_bits_to_f32(de[j]);
+      const float own = bf16_bits_to_f32(re[j]);
+      const float scaled = kind == 1 ? rb(src * s) : src;
+      re[j] = f32_to_bf16_bits(rb(a * scaled) + rb(om * own));
+    }
+    *reinterpret_cast<uint4*>(rdst) = rv4;
+  }
+}
+
+}  // namespace
+}  // namespace lkv
+
+extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) {
+  using namespace lkv;
+  LKV_REQUIRE(a != nullptr, "null args");
+  LKV_REQUIRE(a->struct_size == static_cast<int32_t>(sizeof(lkv_qkv_args)), "lkv_qkv_args size mismatch");
+  LKV_REQUIRE(a->head_dim == kHeadDim, "head_dim must be 128, got %d", a->head_dim);
+  LKV_REQUIRE(a->batch >= 0 && a->tokens >= 0 && a->num_q_heads > 0 && a->num_kv_heads > 0, "bad sizes");
+  LKV_REQUIRE(a->q && a->k && a->v && a->cos && a->sin && a->q_out, "null tensor pointer");
+  LKV_REQUIRE(a->ring_k && a->ring_v, "ring cache required");
+  LKV_REQUIRE(a->ring_tokens > 0 && a->ring_tokens % kBlockTokens == 0, "ring_tokens must be a positive multiple of 32");
+  LKV_REQUIRE(a->ring_num_slots > 0, "ring_num_slots must be positive");
+  LKV_REQUIRE(a->ring_slot != nullptr || a->ring_num_slots >= a->batch, "ring has fewer slots than sequences");
+  LKV_REQUIRE((a->deep_k == nullptr) == (a->deep_v == nullptr), "deep_k and deep_v must both be set");
+  LKV_REQUIRE(a->deep_k == nullptr || a->deep_capacity_tokens % kBlockTokens == 0, "deep capacity must be a multiple of 32");
+  LKV_REQUIRE(a->deep_k == nullptr || a->deep_slot != nullptr || a->deep_num_slots >= a->batch,
+              "deep cache has fewer slots than sequences");
+  LKV_REQUIRE(a->positions != nullptr || a->position_const >= 0, "negative position");
+  const int64_t items = static_cast<int64_t>(a->batch) * a->tokens * (a->num_q_heads + a->num_kv_heads);
+  if (items == 0) return LKV_OK;
+  LKV_REQUIRE(items / 4 + 1 < (1LL << 31), "too many tokens in one call");
+  QkvParams p;
+  p.batch = a->batch;
+  p.tokens = a->tokens;
+  p.hq = a->num_q_heads;
+  p.hkv = a->num_kv_heads;
+  p.eps = a->eps;
+  p.pos_c = a->position_const;
+  p.pos = a->positions;
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.q_sb = a->q_stride_b;
+  p.q_st = a->q_stride_t;
+  p.k_sb = a->k_stride_b;
+  p.k_st = a->k_stride_t;
+  p.v_sb = a->v_stride_b;
+  p.v_st = a->v_stride_t;
+  p.cos = static_cast<const uint16_t*>(a->cos);
+  p.sin = static_cast<const uint16_t*>(a->sin);
+  p.cs_sb = a->cs_stride_b;
+  p.cs_st = a->cs_stride_t;
+  p.qw = static_cast<const uint16_t*>(a->q_norm_w);
+  p.kw = static_cast<const uint16_t*>(a->k_norm_w);
+  p.q_out = static_cast<uint16_t*>(a->q_out);
+  p.qo_sb = a->q_out_stride_b;
+  p.qo_st = a->q_out_stride_t;
+  p.rk = static_cast<uint16_t*>(a->ring_k);
+  p.rv = static_cast<uint16_t*>(a->ring_v);
+  p.r_ss = a->ring_seq_stride;
+  p.r_hs = a->ring_head_stride;
+  p.ring_tokens = a->ring_tokens;
+  p.ring_slots = a->ring_num_slots;
+  p.ring_slot = a->ring_slot;
+  p.dk = static_cast<uint16_t*>(a->deep_k);
+  p.dv = static_cast<uint16_t*>(a->deep_v);
+  p.d_ss = a->deep_seq_stride;
+  p.d_hs = a->deep_head_stride;
+  p.deep_cap = a->deep_k ? a->deep_capacity_tokens : 0;
+  p.deep_slots = a->deep_num_slots;
+  p.deep_slot = a->deep_slot;
+  const int blocks = static_cast<int>((items + 3) / 4);
+  qkv_epilogue_kernel<<<blocks, 256, 0, as_stream(stream)>>>(p);
+  return check_launch("lkv_qkv_epilogue");
+}
+
+extern "C" int32_t lkv_blend_chunk(int32_t layers, int32_t batch, int32_t kv_heads, int32_t chunk_start,
+                                   int32_t chunk_len, void* ring_k, void* ring_v, int64_t ring_layer_stride,
+                                   int64_t ring_seq_stride, int64_t ring_head_stride, int32_t ring_tokens,
+                                   const void* deep_k, const void* deep_v, int64_t deep_seq_stride,
+                                   int64_t deep_head_stride, int32_t deep_capacity_tokens, const float* alpha,
+                                   const float* one_minus_alpha, const float* vscale, lkv_stream_t stream) {
+  using namespace lkv;
+  LKV_REQUIRE(layers >= 0 && batch >= 0 && kv_heads > 0, "bad sizes");
+  LKV_REQUIRE(chunk_start >= 0 && chunk_len >= 0, "bad chunk range");
+  LKV_REQUIRE(ring_tokens > 0 && ring_tokens % kBlockTokens == 0, "ring_tokens must be a positive multiple of 32");
+  LKV_REQUIRE(chunk_len <= ring_tokens, "chunk longer than the ring");
+  LKV_REQUIRE(static_cast<int64_t>(chunk_start) + chunk_len <= deep_capacity_tokens, "chunk beyond the deep capacity");
+  LKV_REQUIRE(ring_k && ring_v && deep_k && deep_v && alpha && one_minus_alpha, "null pointer");
+  if (layers == 0 || batch == 0 || chunk_len == 0) return LKV_OK;
+  // two blocks of the chunk must not share a ring block, or their threads would race on it
+  const int first_blk = chunk_start / kBlockTokens;
+  const int last_blk = (chunk_start + chunk_len - 1) / kBlockTokens;
+  LKV_REQUIRE(last_blk - first_blk + 1 <= ring_tokens / kBlockTokens,
+              "chunk [%d, %d) spans more 32-token blocks than the ring holds (%d tokens)", chunk_start,
+              chunk_start + chunk_len, ring_tokens);
+  BlendParams p;
+  p.layers = layers;
+  p.batch = batch;
+  p.heads = kv_heads;
+  p.start = chunk_start;
+  p.end = chunk_start + chunk_len;
+  p.blk0 = first_blk;
+  p.nblk = last_blk - first_blk + 1;
+  p.rk = static_cast<uint16_t*>(ring_k);
+  p.rv = static_cast<uint16_t*>(ring_v);
+  p.r_ls = ring_layer_stride;
+  p.r_ss = ring_seq_stride;
+  p.r_hs = ring_head_stride;
+  p.ring_tokens = ring_tokens;
+  p.dk = static_cast<const uint16_t*>(deep_k);
+  p.dv = static_cast<const uint16_t*>(deep_v);
+  p.d_ss = deep_seq_stride;
+  p.d_hs = deep_head_stride;
+  p.alpha = alpha;
+  p.om = one_minus_alpha;
+  p.vs = vscale;
+  const int64_t total = static_cast<int64_t>(layers) * batch * kv_heads * p.nblk * (kBlockElems / 8) * 2;
+  const int64_t want = (total + 255) / 256;
+  const int grid = static_cast<int>(want < 65536 ? want : 65536);
+  blend_kernel<<<grid, 256, 0, as_stream(stream)>>>(p);
+  return check_launch("lkv_blend_chunk");
+}

@@ -170,6 +170,53 @@ def _len_arg(value: int | torch.Tensor | None, batch: int, name: str, device: to
     return None, int(value)
 
 
+def _fill_segments(a, B: int, device: torch.device, older, older_len, older_slot, vscale, local, local_len,
+                   local_start, local_slot) -> int:
+    """Fill the older/local segment fields shared by DecodeArgs and PrefillArgs; returns Hkv."""
+
+    _require(older is not None or local is not None, "at least one key segment is required")
+    Hkv = (older if older is not None else local).heads
+    if older is not None and local is not None:
+        _require(older.heads == local.heads, "older and local caches have different kv head counts")
+    if vscale is not None:
+        _require(vscale.dtype == torch.float32 and vscale.numel() == Hkv and vscale.is_contiguous() and vscale.device == device,
+                 "vscale must be a contiguous fp32 [Hkv] tensor on the query's device")
+    a.older_vscale_mode = 1 if vscale is not None else 0
+    a.vscale = _ptr(vscale)
+    for name, t in (("older_slot", older_slot), ("local_slot", local_slot)):
+        if t is not None:
+            _require(t.dtype == torch.int32 and t.device == device and t.numel() == B and t.is_contiguous(),
+                     f"{name} must be a contiguous int32 tensor of {B} entries on {device}")
+    if older is not None:
+        _require(older.device == device, "older cache on another device")
+        a.older_k, a.older_v = older.k.data_ptr(), older.v.data_ptr()
+        a.older_seq_stride, a.older_head_stride = older.seq_stride, older.head_stride
+        a.older_len, a.older_len_const = _len_arg(older_len, B, "older_len", device)
+        a.older_capacity_tokens = older.capacity_tokens
+        a.older_slot = _ptr(older_slot)
+        a.older_num_slots = older.slots
+        if older_slot is None:
+            _require(older.slots >= B, "older cache has fewer slots than sequences")
+        if not isinstance(older_len, torch.Tensor):
+            _require(0 <= older_len <= older.capacity_tokens, "older_len exceeds the cache capacity")
+    if local is not None:
+        _require(local.device == device, "local cache on another device")
+        a.local_k, a.local_v = local.k.data_ptr(), local.v.data_ptr()
+        a.local_seq_stride, a.local_head_stride = local.seq_stride, local.head_stride
+        a.local_ring_blocks = local.blocks
+        a.local_len, a.local_len_const = _len_arg(local_len, B, "local_len", device)
+        a.local_start, a.local_start_const = _len_arg(local_start, B, "local_start", device)
+        a.local_slot = _ptr(local_slot)
+        a.local_num_slots = local.slots
+        if local_slot is None:
+            _require(local.slots >= B, "local cache has fewer slots than sequences")
+        if not isinstance(local_len, torch.Tensor):
+            _require(0 <= local_len <= local.capacity_tokens, "local_len exceeds the ring capacity")
+        if not isinstance(local_start, torch.Tensor):
+            _require(0 <= local_start < local.capacity_tokens, "local_start outside the ring")
+    return Hkv
+
+
 def decode_attention(
     q: torch.Tensor,
     *,
@@ -179,7 +226,7 @@ def decode_attention(
     vscale: torch.Tensor | None = None,
     local: TiledKV | None = None,
     local_len: int | torch.Tensor = 0,
-    local_start_block: torch.Tensor | None = None,
+    local_start: int | torch.Tensor = 0,
     local_slot: torch.Tensor | None = None,
     sm_scale: float | None = None,
     num_splits: int | None = None,
@@ -201,22 +248,20 @@ def decode_attention(
     _require(q.stride(-1) == 1 and q.stride(1) == HEAD_DIM, "q heads must be contiguous rows of 128")
     B, Hq, _ = q.shape
     device = q.device
-    _require(older is not None or local is not None, "at least one key segment is required")
-    Hkv = (older if older is not None else local).heads
-    if older is not None and local is not None:
-        _require(older.heads == local.heads, "older and local caches have different kv head counts")
+    a = _lib.DecodeArgs()
+    a.struct_size = ctypes.sizeof(_lib.DecodeArgs)
+    Hkv = _fill_segments(a, B, device, older, older_len, older_slot, vscale, local, local_len, local_start, local_slot)
     _require(Hq % Hkv == 0 and Hq // Hkv <= 16, "Hq must be a multiple of Hkv with group <= 16")
     if out is None:
         out = torch.empty((B, Hq, HEAD_DIM), dtype=torch.bfloat16, device=device)
     _require_bf16_cuda("out", out)
+    if out.dim() == 4:
+        out = out[:, :, 0]
     _require(out.shape[0] == B and out.shape[1] == Hq and out.shape[-1] == HEAD_DIM, "out shape mismatch")
     _require(out.stride(-1) == 1 and out.stride(1) == HEAD_DIM, "out heads must be contiguous rows of 128")
     if lse is not None:
         _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() == B * Hq and lse.device == device,
                  "lse must be a contiguous fp32 [B, Hq] tensor")
-    if vscale is not None:
-        _require(vscale.dtype == torch.float32 and vscale.numel() == Hkv and vscale.is_contiguous() and vscale.device == device,
-                 "vscale must be a contiguous fp32 [Hkv] tensor")
     max_tokens = 0
     if older is not None:
         max_tokens += older.capacity_tokens if isinstance(older_len, torch.Tensor) else int(older_len)
@@ -230,47 +275,194 @@ def decode_attention(
         if workspace is None:
             workspace = torch.empty(need, dtype=torch.uint8, device=device)
         _require(workspace.device == device and workspace.numel() * workspace.element_size() >= need, "workspace too small")
-
-    a = _lib.DecodeArgs()
-    a.struct_size = ctypes.sizeof(_lib.DecodeArgs)
     a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, HEAD_DIM
     a.num_splits = num_splits
     a.sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
-    a.older_vscale_mode = 1 if vscale is not None else 0
     a.q, a.q_stride_b = q.data_ptr(), q.stride(0)
     a.out, a.out_stride_b = out.data_ptr(), out.stride(0)
     a.lse = _ptr(lse)
-    if older is not None:
-        _require(older.device == device, "older cache on another device")
-        a.older_k, a.older_v = older.k.data_ptr(), older.v.data_ptr()
-        a.older_seq_stride, a.older_head_stride = older.seq_stride, older.head_stride
-        a.older_len, a.older_len_const = _len_arg(older_len, B, "older_len", device)
-        a.older_capacity_tokens = older.capacity_tokens
-        a.older_slot = _ptr(older_slot)
-        a.older_num_slots = older.slots
-        if older_slot is None:
-            _require(older.slots >= B, "older cache has fewer slots than sequences")
-        if not isinstance(older_len, torch.Tensor):
-            _require(0 <= older_len <= older.capacity_tokens, "older_len exceeds the cache capacity")
-    if local is not None:
-        _require(local.device == device, "local cache on another device")
-        a.local_k, a.local_v = local.k.data_ptr(), local.v.data_ptr()
-        a.local_seq_stride, a.local_head_stride = local.seq_stride, local.head_stride
-        a.local_ring_blocks = local.blocks
-        a.local_len, a.local_len_const = _len_arg(local_len, B, "local_len", device)
-        a.local_start_block = _ptr(local_start_block)
-        a.local_slot = _ptr(local_slot)
-        a.local_num_slots = local.slots
-        if local_slot is None:
-            _require(local.slots >= B, "local cache has fewer slots than sequences")
-        if not isinstance(local_len, torch.Tensor):
-            _require(0 <= local_len <= local.capacity_tokens, "local_len exceeds the ring capacity")
-    for name, t in (("older_slot", older_slot), ("local_slot", local_slot), ("local_start_block", local_start_block)):
-        if t is not None:
-            _require(t.dtype == torch.int32 and t.device == device and t.numel() == B and t.is_contiguous(),
-                     f"{name} must be a contiguous int32 tensor of {B} entries on {device}")
-    a.vscale = _ptr(vscale)
     a.workspace = _ptr(workspace)
     a.workspace_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _lib.check(lib.lkv_decode_attn(ctypes.byref(a), _stream(device)), "lkv_decode_attn")
     return out
+
+
+def prefill_attention(
+    q: torch.Tensor,
+    *,
+    older: TiledKV | None = None,
+    older_len: int | torch.Tensor = 0,
+    older_slot: torch.Tensor | None = None,
+    vscale: torch.Tensor | None = None,
+    local: TiledKV | None = None,
+    local_len: int | torch.Tensor = 0,
+    local_start: int | torch.Tensor = 0,
+    local_slot: torch.Tensor | None = None,
+    causal: bool = True,
+    sm_scale: float | None = None,
+    out: torch.Tensor | None = None,
+    lse: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Attention of ``q`` ``[B, L, Hq, 128]`` (L query tokens per sequence, the last L tokens of
+    the local segment) over ``[older | local]``; the local segment is bottom-right causal
+    (``causal``) or fully visible.  Returns ``out`` ``[B, L, Hq, 128]`` bf16."""
+
+    _require_bf16_cuda("q", q)
+    _require(q.dim() == 4 and q.shape[-1] == HEAD_DIM, "q must be [B, L, Hq, 128]")
+    _require(q.stride(-1) == 1 and q.stride(2) == HEAD_DIM, "q heads must be contiguous rows of 128")
+    B, L, Hq, _ = q.shape
+    device = q.device
+    a = _lib.PrefillArgs()
+    a.struct_size = ctypes.sizeof(_lib.PrefillArgs)
+    Hkv = _fill_segments(a, B, device, older, older_len, older_slot, vscale, local, local_len, local_start, local_slot)
+    _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
+    if out is None:
+        out = torch.empty((B, L, Hq, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    _require_bf16_cuda("out", out)
+    _require(tuple(out.shape) == (B, L, Hq, HEAD_DIM), "out must be [B, L, Hq, 128]")
+    _require(out.stride(-1) == 1 and out.stride(2) == HEAD_DIM, "out heads must be contiguous rows of 128")
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() == B * L * Hq and lse.device == device,
+                 "lse must be a contiguous fp32 [B, L, Hq] tensor")
+    a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = B, L, Hq, Hkv, HEAD_DIM
+    a.sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
+    a.causal = 1 if causal else 0
+    a.q, a.q_stride_b, a.q_stride_t = q.data_ptr(), q.stride(0), q.stride(1)
+    a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
+    a.lse = _ptr(lse)
+    lib = _lib.load()
+    _lib.check(lib.lkv_prefill_attn(ctypes.byref(a), _stream(device)), "lkv_prefill_attn")
+    return out
+
+
+def _rows(name: str, t: torch.Tensor, heads: int) -> tuple[int, int, int]:
+    """(ptr, stride_b, stride_t) of a [B, L, heads * 128] (or [B, L, heads, 128]) bf16 tensor."""
+
+    _require_bf16_cuda(name, t)
+    if t.dim() == 4:
+        _require(t.shape[2] == heads and t.shape[3] == HEAD_DIM and t.stride(3) == 1 and t.stride(2) == HEAD_DIM,
+                 f"{name} must be [B, L, {heads}, 128] with contiguous heads")
+    else:
+        _require(t.dim() == 3 and t.shape[2] == heads * HEAD_DIM and t.stride(2) == 1, f"{name} must be [B, L, {heads}*128]")
+    _require(t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0 and t.data_ptr() % 16 == 0, f"{name} rows must be 16-byte aligned")
+    return t.data_ptr(), t.stride(0), t.stride(1)
+
+
+def qkv_epilogue(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    *,
+    num_q_heads: int,
+    num_kv_heads: int,
+    q_norm_weight: torch.Tensor | None,
+    k_norm_weight: torch.Tensor | None,
+    eps: float,
+    positions: int | torch.Tensor,
+    ring: TiledKV,
+    ring_slot: torch.Tensor | None = None,
+    deep: TiledKV | None = None,
+    deep_slot: torch.Tensor | None = None,
+    q_out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """RoPE + q/k RMSNorm of the projections and the append of K/V to the layer ring (and, for
+    the final layer, the shared cache) at positions ``positions + i``; returns the normalised
+    queries ``[B, L, Hq, 128]``."""
+
+    B, L = int(q.shape[0]), int(q.shape[1])
+    qp, qsb, qst = _rows("q", q, num_q_heads)
+    kp, ksb, kst = _rows("k", k, num_kv_heads)
+    vp, vsb, vst = _rows("v", v, num_kv_heads)
+    _require(tuple(k.shape[:2]) == (B, L) and tuple(v.shape[:2]) == (B, L), "q/k/v token shapes differ")
+    for name, t in (("cos", cos), ("sin", sin)):
+        _require_bf16_cuda(name, t)
+        _require(t.dim() == 3 and t.shape[1] == L and t.shape[2] == HEAD_DIM and t.shape[0] in (1, B) and t.stride(2) == 1,
+                 f"{name} must be [1 or B, L, 128]")
+    _require(cos.stride() == sin.stride(), "cos and sin strides differ")
+    device = q.device
+    for name, w in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if w is not None:
+            _require_bf16_cuda(name, w)
+            _require(w.numel() == HEAD_DIM and w.is_contiguous(), f"{name} must be a contiguous bf16 [128] tensor")
+    _require(ring.heads == num_kv_heads, "ring kv heads mismatch")
+    if q_out is None:
+        q_out = torch.empty((B, L, num_q_heads, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    _require(q_out.is_contiguous() and tuple(q_out.shape) == (B, L, num_q_heads, HEAD_DIM), "q_out must be contiguous [B, L, Hq, 128]")
+    a = _lib.QkvArgs()
+    a.struct_size = ctypes.sizeof(_lib.QkvArgs)
+    a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = B, L, num_q_heads, num_kv_heads, HEAD_DIM
+    a.eps = float(eps)
+    a.positions, a.position_const = _len_arg(positions, B, "positions", device)
+    a.q, a.q_stride_b, a.q_stride_t = qp, qsb, qst
+    a.k, a.k_stride_b, a.k_stride_t = kp, ksb, kst
+    a.v, a.v_stride_b, a.v_stride_t = vp, vsb, vst
+    a.cos, a.sin = cos.data_ptr(), sin.data_ptr()
+    a.cs_stride_b = cos.stride(0) if cos.shape[0] == B and B > 1 else 0
+    a.cs_stride_t = cos.stride(1)
+    a.q_norm_w, a.k_norm_w = _ptr(q_norm_weight), _ptr(k_norm_weight)
+    a.q_out, a.q_out_stride_b, a.q_out_stride_t = q_out.data_ptr(), q_out.stride(0), q_out.stride(1)
+    a.ring_k, a.ring_v = ring.k.data_ptr(), ring.v.data_ptr()
+    a.ring_seq_stride, a.ring_head_stride = ring.seq_stride, ring.head_stride
+    a.ring_tokens, a.ring_num_slots, a.ring_slot = ring.capacity_tokens, ring.slots, _ptr(ring_slot)
+    if deep is not None:
+        _require(deep.heads == num_kv_heads, "deep kv heads mismatch")
+        a.deep_k, a.deep_v = deep.k.data_ptr(), deep.v.data_ptr()
+        a.deep_seq_stride, a.deep_head_stride = deep.seq_stride, deep.head_stride
+        a.deep_capacity_tokens, a.deep_num_slots, a.deep_slot = deep.capacity_tokens, deep.slots, _ptr(deep_slot)
+        if not isinstance(positions, torch.Tensor):
+            _require(positions + L <= deep.capacity_tokens, "positions exceed the shared cache capacity")
+    lib = _lib.load()
+    _lib.check(lib.lkv_qkv_epilogue(ctypes.byref(a), _stream(device)), "lkv_qkv_epilogue")
+    return q_out
+
+
+def blend_chunk(
+    ring_k: torch.Tensor,
+    ring_v: torch.Tensor,
+    deep: TiledKV,
+    *,
+    batch: int,
+    chunk_start: int,
+    chunk_len: int,
+    alpha: torch.Tensor,
+    one_minus_alpha: torch.Tensor,
+    vscale: torch.Tensor | None,
+) -> None:
+    """Boundary commit: for every layer's ring (``ring_k``/``ring_v`` ``[layers, slots, H,
+    blocks, 4096]``) blend tokens ``[chunk_start, chunk_start + chunk_len)`` with the shared cache
+    in place.  ``alpha``, ``one_minus_alpha``, ``vscale``: fp32 ``[layers * H]`` bf16 values."""
+
+    for name, t in (("ring_k", ring_k), ("ring_v", ring_v)):
+        _require_bf16_cuda(name, t)
+        _require(t.dim() == 5 and t.shape[-1] == BLOCK_ELEMS and t.is_contiguous(), f"{name} must be contiguous [layers, slots, H, blocks, 4096]")
+    _require(ring_k.shape == ring_v.shape, "ring k/v shapes differ")
+    layers, slots, H, blocks, _ = ring_k.shape
+    _require(H == deep.heads and batch <= slots and batch <= deep.slots, "ring/deep geometry mismatch")
+    for name, t in (("alpha", alpha), ("one_minus_alpha", one_minus_alpha), ("vscale", vscale)):
+        if t is not None:
+            _require(t.dtype == torch.float32 and t.is_contiguous() and t.numel() == layers * H and t.device == deep.device,
+                     f"{name} must be a contiguous fp32 [layers * H] tensor")
+    lib = _lib.load()
+    _lib.check(
+        lib.lkv_blend_chunk(
+            layers, batch, H, chunk_start, chunk_len, ring_k.data_ptr(), ring_v.data_ptr(), ring_k.stride(0),
+            ring_k.stride(1), ring_k.stride(2), blocks * BLOCK_TOKENS, deep.k.data_ptr(), deep.v.data_ptr(),
+            deep.seq_stride, deep.head_stride, deep.capacity_tokens, alpha.data_ptr(), one_minus_alpha.data_ptr(),
+            _ptr(vscale), _stream(deep.device),
+        ),
+        "lkv_blend_chunk",
+    )
+
+
+def ring_tokens_for_chunk(chunk: int) -> int:
+    """Ring capacity of one layer: the two live chunks, rounded up to whole 32-token blocks, plus
+    one spare block when chunks straddle block boundaries (so no two blocks of one chunk share a
+    ring block)."""
+
+    _require(chunk >= 1, "chunk must be positive")
+    ring = -(-2 * chunk // BLOCK_TOKENS) * BLOCK_TOKENS
+    if chunk % BLOCK_TOKENS and BLOCK_TOKENS % chunk:
+        ring += BLOCK_TOKENS
+    return ring

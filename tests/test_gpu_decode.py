@@ -104,7 +104,7 @@ def _ring_inputs(r, deep_k, deep_v, prev, cur_kv, logits, scale, chunk, B, Hkv):
         rv = A.blend_chunk_bf16(deep_v[:, :, rec:cur], prev[1], logits, scale)
         ops.pack_kv(_t(rk), _t(rv), ring, token0=rec % (2 * chunk))
     ops.pack_kv(_t(cur_kv[0]), _t(cur_kv[1]), ring, token0=cur % (2 * chunk))
-    start = torch.full((B,), (rec % (2 * chunk)) // 32, dtype=torch.int32, device=DEV)
+    start = torch.full((B,), rec % (2 * chunk), dtype=torch.int32, device=DEV)
     return older, ring, start
 
 
@@ -117,7 +117,7 @@ def test_lastkv_region_decode_matches_oracle(position):
     rec = r.recent[0]
     out = ops.decode_attention(
         _t(q), older=older, older_len=rec, vscale=torch.from_numpy(scale).to(DEV),
-        local=ring, local_len=position + 1 - rec, local_start_block=start, num_splits=2,
+        local=ring, local_len=position + 1 - rec, local_start=start, num_splits=2,
     )
     full_k, full_v = A.compose_history_bf16(deep_k, deep_v, prev and prev[0], prev and prev[1], cur_kv[0], cur_kv[1],
                                             logits, scale, C)

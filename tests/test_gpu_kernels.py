@@ -1,0 +1,224 @@
+"""GPU parity of the chunked-prefill kernel, the fused QKV epilogue and the boundary blend.
+
+Tolerances: attention outputs within max-abs 2e-2 and rel-L2 1e-3 of the reference path
+(oracle fp64 over the reference's bf16-composed history, output rounded to bf16); the blend is
+bit-exact (elementwise bf16 ops in the reference's order); the epilogue is bit-exact except where
+the fp32 sum of squares inside RMSNorm rounds differently from torch's reduction order, bounded
+at 0.1% of elements and one bf16 ulp.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from lastkv_amd import ops
+from oracle import attention as A
+from oracle import bf16
+from oracle import model as M
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+REL_L2 = 1e-3
+DEV = "cuda"
+
+
+def _bf(rng, shape, scale=1.0):
+    return bf16.round_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV, torch.bfloat16)
+
+
+def _close(actual: torch.Tensor, expected, label: str):
+    a = actual.float().cpu().numpy()
+    e = np.asarray(expected, np.float64)
+    ma, rl = A.max_abs(a, e), A.rel_l2(a, e)
+    print(f"{label}: max_abs={ma:.3e} rel_l2={rl:.3e}", flush=True)
+    assert ma <= MAX_ABS and rl <= REL_L2, f"{label}: max_abs={ma} rel_l2={rl}"
+
+
+def _history(rng, B, Hkv, chunk, p0, L):
+    """Final-layer history, the layer's previous chunk and the current chunk up to p0 + L."""
+
+    r = A.plan_regions(p0 + L - 1, chunk)
+    rec, cur = r.recent[0], r.current[0]
+    assert p0 >= cur, "a prefill piece never crosses a chunk boundary"
+    deep = (_bf(rng, (B, Hkv, cur, 128)), _bf(rng, (B, Hkv, cur, 128)))
+    prev = (_bf(rng, (B, Hkv, chunk, 128)), _bf(rng, (B, Hkv, chunk, 128))) if cur else None
+    n_cur = p0 + L - cur
+    cur_kv = (_bf(rng, (B, Hkv, n_cur, 128)), _bf(rng, (B, Hkv, n_cur, 128)))
+    logits = bf16.round_bf16(rng.standard_normal(Hkv).astype(np.float32))
+    scale = bf16.round_bf16(rng.uniform(0.3, 1.3, Hkv).astype(np.float32))
+    return r, deep, prev, cur_kv, logits, scale
+
+
+def _caches(r, deep, prev, cur_kv, logits, scale, chunk, B, Hkv):
+    rec, cur = r.recent[0], r.current[0]
+    R = ops.ring_tokens_for_chunk(chunk)
+    older = ops.TiledKV.zeros(B, Hkv, max(32, -(-cur // 32) * 32), DEV)
+    if cur:
+        ops.pack_kv(_t(deep[0]), _t(deep[1]), older)
+    ring = ops.TiledKV.zeros(B, Hkv, R, DEV)
+
+    def put(k, v, pos):
+        # write token by token range, splitting where the ring wraps
+        n = k.shape[2]
+        first = min(n, R - pos % R)
+        ops.pack_kv(_t(k[:, :, :first]), _t(v[:, :, :first]), ring, token0=pos % R)
+        if first < n:
+            ops.pack_kv(_t(k[:, :, first:]), _t(v[:, :, first:]), ring, token0=0)
+
+    if cur:
+        put(A.blend_chunk_bf16(deep[0][:, :, rec:cur], prev[0], logits),
+            A.blend_chunk_bf16(deep[1][:, :, rec:cur], prev[1], logits, scale), rec)
+    put(cur_kv[0], cur_kv[1], cur)
+    return older, ring, rec % R
+
+
+@pytest.mark.parametrize("chunk,p0,L", [
+    (64, 0, 1), (64, 0, 37), (64, 128, 64), (64, 200, 20), (64, 70, 50), (64, 320, 1),
+    (4, 8, 4), (4, 13, 3), (12, 40, 8), (48, 150, 42), (1024, 2048, 300),
+])
+def test_prefill_regions_match_oracle(chunk, p0, L):
+    rng = np.random.default_rng(chunk * 1000 + p0 + L)
+    B, Hq, Hkv = 2, 8, 2
+    r, deep, prev, cur_kv, logits, scale = _history(rng, B, Hkv, chunk, p0, L)
+    older, ring, start = _caches(r, deep, prev, cur_kv, logits, scale, chunk, B, Hkv)
+    rec = r.recent[0]
+    q = _bf(rng, (B, L, Hq, 128))
+    lse = torch.empty((B, L, Hq), dtype=torch.float32, device=DEV)
+    out = ops.prefill_attention(_t(q), older=older, older_len=rec, vscale=torch.from_numpy(scale).to(DEV),
+                                local=ring, local_len=p0 + L - rec, local_start=start, causal=True, lse=lse)
+    full_k, full_v = A.compose_history_bf16(deep[0], deep[1], prev and prev[0], prev and prev[1], cur_kv[0], cur_kv[1],
+                                            logits, scale, chunk)
+    want, want_lse = A.attention(q.transpose(0, 2, 1, 3), full_k, full_v, causal_bottom_right=True)
+    _close(out, bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32)), f"prefill C={chunk} p0={p0} L={L}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("L,Hq,Hkv,T0,n_local", [(5, 8, 2, 100, 0), (300, 12, 12, 500, 300), (64, 32, 8, 40, 64)])
+def test_prefill_bidirectional_local_segment(L, Hq, Hkv, T0, n_local):
+    """causal = 0: every query sees every local token (Wan's current block)."""
+
+    rng = np.random.default_rng(L + T0)
+    B = 1
+    q = _bf(rng, (B, L, Hq, 128))
+    ok, ov = _bf(rng, (B, Hkv, T0, 128)), _bf(rng, (B, Hkv, T0, 128))
+    older = ops.TiledKV.zeros(B, Hkv, -(-T0 // 32) * 32, DEV)
+    ops.pack_kv(_t(ok), _t(ov), older)
+    kwargs = dict(older=older, older_len=T0, causal=False)
+    ks, vs = [ok], [ov]
+    if n_local:
+        lk, lv = _bf(rng, (B, Hkv, n_local, 128)), _bf(rng, (B, Hkv, n_local, 128))
+        ring = ops.TiledKV.zeros(B, Hkv, -(-n_local // 32) * 32 + 32, DEV)
+        ops.pack_kv(_t(lk), _t(lv), ring, token0=7)
+        kwargs.update(local=ring, local_len=n_local, local_start=7)
+        ks.append(lk)
+        vs.append(lv)
+    out = ops.prefill_attention(_t(q), **kwargs)
+    want, _ = A.attention(q.transpose(0, 2, 1, 3), np.concatenate(ks, 2), np.concatenate(vs, 2))
+    _close(out, bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32)), f"bidirectional L={L} Hq={Hq}")
+
+
+def test_prefill_agrees_with_decode_for_single_token():
+    rng = np.random.default_rng(5)
+    B, Hq, Hkv, C, p = 3, 16, 4, 64, 250
+    r, deep, prev, cur_kv, logits, scale = _history(rng, B, Hkv, C, p, 1)
+    older, ring, start = _caches(r, deep, prev, cur_kv, logits, scale, C, B, Hkv)
+    rec = r.recent[0]
+    q = _bf(rng, (B, 1, Hq, 128))
+    vs = torch.from_numpy(scale).to(DEV)
+    a = ops.prefill_attention(_t(q), older=older, older_len=rec, vscale=vs, local=ring, local_len=p + 1 - rec, local_start=start)
+    d = ops.decode_attention(_t(q)[:, 0], older=older, older_len=rec, vscale=vs, local=ring, local_len=p + 1 - rec,
+                             local_start=start)
+    _close(a[:, 0], d.float().cpu().numpy(), "prefill L=1 vs decode")
+
+
+# ------------------------------------------------------------------ epilogue
+def _ulp_stats(actual: np.ndarray, expected: np.ndarray):
+    diff = actual.view(np.uint32).astype(np.int64) - expected.view(np.uint32).astype(np.int64)
+    mism = np.count_nonzero(diff)
+    return mism / diff.size, int(np.max(np.abs(diff >> 16))) if mism else 0
+
+
+@pytest.mark.parametrize("B,L,p0,last", [(2, 1, 37, False), (3, 17, 100, True), (1, 64, 0, True)])
+def test_qkv_epilogue_matches_reference_ops(B, L, p0, last):
+    rng = np.random.default_rng(B * 100 + L)
+    Hq, Hkv, C = 8, 2, 32
+    q = _bf(rng, (B, L, Hq * 128))
+    k = _bf(rng, (B, L, Hkv * 128))
+    v = _bf(rng, (B, L, Hkv * 128))
+    cfg = M.config_8b(num_hidden_layers=2)
+    inv, sc = M.rope_inv_freq(cfg)
+    pos = torch.arange(p0, p0 + L)[None].expand(B, L)
+    cos, sin = M.rotary_cos_sin(inv, sc, pos, torch.bfloat16)
+    qw = torch.linspace(0.7, 1.3, 128).bfloat16()
+    kw = torch.linspace(1.2, 0.8, 128).bfloat16()
+    ring = ops.TiledKV.zeros(B, Hkv, ops.ring_tokens_for_chunk(C), DEV)
+    deep = ops.TiledKV.zeros(B, Hkv, 256, DEV) if last else None
+    q_out = ops.qkv_epilogue(_t(q), _t(k), _t(v), cos.to(DEV), sin.to(DEV), num_q_heads=Hq, num_kv_heads=Hkv,
+                             q_norm_weight=qw.to(DEV), k_norm_weight=kw.to(DEV), eps=1e-5, positions=p0, ring=ring, deep=deep)
+    # the reference's ops in bf16 on the CPU (modeling.py:100-106)
+    tq = torch.from_numpy(q).bfloat16().view(B, L, Hq, 128).transpose(1, 2)
+    tk = torch.from_numpy(k).bfloat16().view(B, L, Hkv, 128).transpose(1, 2)
+    rq, rk = M.apply_rope(tq, tk, cos, sin)
+    qn, kn = M.RMSNorm(128, 1e-5).bfloat16(), M.RMSNorm(128, 1e-5).bfloat16()
+    with torch.no_grad():
+        qn.weight.copy_(qw)
+        kn.weight.copy_(kw)
+        rq, rk = qn(rq), kn(rk)
+    frac, ulp = _ulp_stats(q_out.float().cpu().numpy(), rq.transpose(1, 2).float().numpy())
+    print(f"epilogue q: mismatch fraction {frac:.2e}, max ulp {ulp}", flush=True)
+    assert frac <= 1e-3 and ulp <= 1
+    R = ring.capacity_tokens
+    got_k = [ops.unpack_kv(ring, (p0 + i) % R, 1)[0] for i in range(L)]
+    got_v = [ops.unpack_kv(ring, (p0 + i) % R, 1)[1] for i in range(L)]
+    got_k = torch.cat(got_k, 2).float().cpu().numpy()
+    got_v = torch.cat(got_v, 2).float().cpu().numpy()
+    frac, ulp = _ulp_stats(got_k, rk.float().numpy())
+    assert frac <= 1e-3 and ulp <= 1
+    assert np.array_equal(got_v, torch.from_numpy(v).view(B, L, Hkv, 128).transpose(1, 2).numpy())
+    if last:
+        dk, dv = ops.unpack_kv(deep, p0, L)
+        assert np.array_equal(dk.float().cpu().numpy(), got_k) and np.array_equal(dv.float().cpu().numpy(), got_v)
+
+
+# ------------------------------------------------------------------ blend
+@pytest.mark.parametrize("chunk,cidx", [(64, 1), (64, 4), (1024, 2), (4, 3), (12, 5)])
+def test_blend_chunk_bit_exact(chunk, cidx):
+    rng = np.random.default_rng(chunk + cidx)
+    layers, B, H = 3, 2, 4
+    R = ops.ring_tokens_for_chunk(chunk)
+    start = cidx * chunk
+    deep_k, deep_v = _bf(rng, (B, H, start + chunk, 128)), _bf(rng, (B, H, start + chunk, 128))
+    deep = ops.TiledKV.zeros(B, H, -(-(start + chunk) // 32) * 32, DEV)
+    ops.pack_kv(_t(deep_k), _t(deep_v), deep)
+    ring_k = torch.zeros((layers, B, H, R // 32, 4096), dtype=torch.bfloat16, device=DEV)
+    ring_v = torch.zeros_like(ring_k)
+    own = []
+    for l in range(layers):
+        ok, ov = _bf(rng, (B, H, R, 128)), _bf(rng, (B, H, R, 128))
+        ops.cache_pack(_t(ok), ring_k[l], ops.KIND_K)
+        ops.cache_pack(_t(ov), ring_v[l], ops.KIND_V)
+        own.append((ok, ov))
+    logits = bf16.round_bf16(rng.standard_normal((layers, H)).astype(np.float32))
+    s = bf16.round_bf16(rng.uniform(0.1, 1.3, (layers, H)).astype(np.float32))
+    alpha = bf16.round_bf16(A.sigmoid(logits).astype(np.float32))
+    om = bf16.rsub(alpha, 1.0)
+    ops.blend_chunk(ring_k, ring_v, deep, batch=B, chunk_start=start, chunk_len=chunk,
+                    alpha=torch.from_numpy(alpha.ravel()).to(DEV), one_minus_alpha=torch.from_numpy(om.ravel()).to(DEV),
+                    vscale=torch.from_numpy(s.ravel()).to(DEV))
+    pos = np.arange(start, start + chunk) % R
+    for l in range(layers):
+        gk = ops.cache_unpack(ring_k[l], ops.KIND_K, 0, R).float().cpu().numpy()
+        gv = ops.cache_unpack(ring_v[l], ops.KIND_V, 0, R).float().cpu().numpy()
+        wk = A.blend_chunk_bf16(deep_k[:, :, start:], own[l][0][:, :, pos], logits[l])
+        wv = A.blend_chunk_bf16(deep_v[:, :, start:], own[l][1][:, :, pos], logits[l], s[l])
+        assert np.array_equal(gk[:, :, pos], wk) and np.array_equal(gv[:, :, pos], wv)
+        # every other ring token is untouched
+        rest = np.setdiff1d(np.arange(R), pos)
+        assert np.array_equal(gk[:, :, rest], own[l][0][:, :, rest]) and np.array_equal(gv[:, :, rest], own[l][1][:, :, rest])
