@@ -276,9 +276,8 @@ class Decoder(nn.Module):
         self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size, config.pad_token_id)
         self.layers = nn.ModuleList(DecoderLayer(config, i) for i in range(config.num_hidden_layers))
         self.norm = RMSNorm(config.hidden_size, config.rms_norm_eps)
-        inv, scaling = rope_inv_freq(config)
-        self.register_buffer("inv_freq", inv, persistent=False)
-        self.rope_scaling_factor = scaling
+        # kept out of the module's buffers so that casting the model to bf16 leaves it fp32
+        self.inv_freq, self.rope_scaling_factor = rope_inv_freq(config)
 
     def forward(self, input_ids, cache: Cache | None = None):
         """modeling.py:173-212 (input validation :175-193, chunk loop :196-208)."""
