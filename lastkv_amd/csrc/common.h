@@ -62,17 +62,35 @@ __device__ inline f32x4 mfma_f16(uint4 a, uint4 b, f32x4 c) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Reductions over the four 16-lane rows of a wave (lanes n, n+16, n+32, n+48) with the gfx950
+// VALU lane swaps: permlane16_swap(x, x) yields rows (0,0,2,2) and (1,1,3,3), permlane32_swap(x, x)
+// yields the lower and the upper half on both halves.  No LDS traffic, no bpermute latency.
 __device__ inline float wave_max_across_rows(float x) {
-  // lanes n, n+16, n+32, n+48 hold the same head; reduce over the four 16-lane rows
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ inline float wave_sum_across_rows(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const uint32_t v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Workgroup id -> logical work index such that consecutive logical indices run on the same XCD:
+// the dispatcher hands workgroup i to XCD i % 8, so logical ranges [x * n / 8, (x + 1) * n / 8)
+// land on XCD x and tiles that share K/V share that XCD's L2.
+__device__ inline int xcd_logical_index(int id, int n) {
+  constexpr int kXcds = 8;
+  const int xcd = id % kXcds, k = id / kXcds;
+  const int q = n / kXcds, r = n % kXcds;
+  return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + k;
 }
 
 }  // namespace lkv

@@ -1,17 +1,20 @@
 // Chunked-prefill attention on MFMA for gfx950: several query tokens per sequence attend to
 // [older shared segment (non-causal) | local ring segment (bottom-right causal or bidirectional)].
 //
-// Workgroup = 4 waves = one (sequence, kv head, query tile).  Query rows are (token, head) pairs
-// of the GQA group, row = token * G + head, so every K/V block feeds all heads of the group.
-// Each wave owns 16 * CG rows (CG column groups of the 16-column MFMA tiles).
+// Workgroup = NW waves = one (sequence, kv head, query tile); workgroups are numbered so that the
+// tiles of one (sequence, kv head) run on one XCD and share its L2.  Query rows are (token, head)
+// pairs of the GQA group, row = token * G + head, so every K/V block feeds all heads of the group.
+// Each wave owns 32 rows (two 16-column groups of the 16x16x32 MFMA tiles), few enough registers
+// (< 256 VGPRs, accumulators in VGPRs) for two waves per SIMD.
 // Per 32-token key block:
-//   - the four waves each fetch a quarter of the block from HBM/L2 (16-byte loads, one
-//     contiguous 1 KiB run per load instruction) into registers one block ahead, convert V to
-//     fp16 (applying bf16(V * s) on the older segment) and publish it to an LDS double buffer in
-//     lane order, so every MFMA operand is one conflict-free ds_read_b128;
+//   - the NW waves each fetch 16 / NW of the block's 16 one-KiB fragments from HBM/L2 into
+//     registers two blocks ahead (one contiguous 1 KiB run per load instruction), convert V to
+//     fp16 (applying bf16(V * s) on the older segment) and publish the block to an LDS double
+//     buffer in lane order, so every MFMA operand is one conflict-free ds_read_b128;
 //   - S^T = K * Q^T with 16x16x32 bf16 MFMAs (exact products, fp32 sums);
-//   - online softmax in the exp2 domain (scale and max folded into one FMA), O rescaled only
-//     when some row's running max moved;
+//   - online softmax in the exp2 domain (scale and max folded into one FMA), row max over the
+//     four 16-lane rows with VALU lane swaps, row sums kept per lane and reduced once at the end,
+//     O rescaled only when some row's running max moved;
 //   - O += P * V with 16x16x32 fp16 MFMAs: P in [0, 1] carries 11 mantissa bits (bf16 would
 //     carry 8, a 1.7e-3 relative error the rel-L2 1e-3 bound does not allow), and bf16 V
 //     converts to fp16 exactly for |V| < 65504 (larger values saturate).
@@ -22,7 +25,6 @@
 namespace lkv {
 namespace {
 
-constexpr int kWaves = 4;
 constexpr float kNegInf = -__builtin_inff();
 
 struct PrefillParams {
@@ -49,7 +51,7 @@ struct PrefillParams {
   int32_t l_start_c;
   const int32_t* l_slot;
   int32_t l_nslots;
-  int32_t L, hq, group, causal;
+  int32_t L, hq, hkv, group, causal, tiles;
   float scale_log2;
 };
 
@@ -109,33 +111,109 @@ __device__ inline int visible_local(const PrefillParams& p, const SeqView& sv, i
   return min(max(v, 0), sv.n1);
 }
 
-template <int CG, bool kVScale>
-__global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
-  __shared__ uint4 lds[2][1024];  // per buffer: 8 K fragments x 64 lanes, then 8 V fragments
+// One fragment = one 16-byte-per-lane MFMA operand = 1 KiB; a 32-token block is 16 fragments:
+// K fragments f = u * 4 + kb (u: 16-token half, kb: 32-dim slice) and V fragments 8 + nb (nb:
+// 16-dim slice).  Wave w of NW stages fragments w, w + NW, ... of each block.
+template <int NW>
+struct Stage {
+  uint4 r[16 / NW];
+};
+
+template <int NW>
+__device__ inline void stage_load(Stage<NW>& st, const BlockRef& r, int wave, int n16, int g4) {
+#pragma unroll
+  for (int j = 0; j < 16 / NW; ++j) {
+    const int f = wave + j * NW;
+    const uint16_t* src = f < 8 ? r.k + (f * 16 + n16) * 32 + 8 * g4 : r.v + (16 * (f - 8) + n16) * 32 + 8 * g4;
+    st.r[j] = *reinterpret_cast<const uint4*>(src);
+  }
+}
+
+template <int NW, bool kVScale>
+__device__ inline void stage_store(const Stage<NW>& st, uint4* buf, bool older, float vs, int wave, int lane) {
+#pragma unroll
+  for (int j = 0; j < 16 / NW; ++j) {
+    const int f = wave + j * NW;
+    uint4 x = st.r[j];
+    if (f >= 8) x = (kVScale && older) ? v_to_f16<true>(x, vs) : v_to_f16<false>(x, 1.f);
+    buf[f * 64 + lane] = x;
+  }
+}
+
+// Softmax step of one 16-column group for one block: scores s0 (tokens 8*g4 + 0..3) and s1
+// (8*g4 + 4..7) of column n16 -> fp16 probabilities; m in the scaled exp2 domain, l partial
+// (this lane's 8 tokens only; the four rows are summed once at the end).
+__device__ inline uint4 softmax_step(f32x4 s0, f32x4 s1, const BlockRef& r, bool need_mask, int lim, int g4,
+                                     float c, float& m, float& l, f32x4 (&o)[8]) {
+  float s[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s[i] = s0[i];
+    s[4 + i] = s1[i];
+  }
+  if (need_mask) {  // wave-uniform: partial block or a local block that crosses some row's causal limit
+    const int w0 = 8 * g4;
+    const int hi = r.older ? r.hi : min(r.hi, lim - r.seg_tok + 1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = (w0 + j >= r.lo && w0 + j < hi) ? s[j] : kNegInf;
+  }
+  float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  mx = wave_max_across_rows(mx) * c;
+  const float m_new = fmaxf(m, mx);
+  // with no visible key yet m_new is -inf: subtract 0 instead, so exp2 gives 0 for every -inf
+  const float m_sub = m_new == kNegInf ? 0.f : m_new;
+  const float alpha = fast_exp2(m - m_sub);
+  float pr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(s[j], c, -m_sub));
+  l = l * alpha + (((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7])));
+  m = m_new;
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+    // O rows of this lane are columns 4*g4 + i, whose factors live in lanes 4*g4 + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = __shfl(alpha, 4 * g4 + i);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) o[nb][i] *= a;
+    }
+  }
+  return make_uint4(pack_f16_rne(pr[0], pr[1]), pack_f16_rne(pr[2], pr[3]), pack_f16_rne(pr[4], pr[5]),
+                    pack_f16_rne(pr[6], pr[7]));
+}
+
+// Workgroup = NW waves x 32 query rows (two 16-column groups per wave); K/V of each 32-token
+// block are staged through a three-buffer LDS ring, loaded three blocks ahead.
+template <int NW, bool kVScale>
+__global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p) {
+  __shared__ uint4 lds[3][1024];
+  constexpr int kRowsPerWave = 32;
+  constexpr int kRowsPerWg = NW * kRowsPerWave;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
-  const int tile = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int logical = xcd_logical_index(blockIdx.x, gridDim.x);
+  const int tile = logical % p.tiles;
+  const int kvh = (logical / p.tiles) % p.hkv;
+  const int b = logical / (p.tiles * p.hkv);
   const int G = p.group;
   const int rows_total = p.L * G;
-  constexpr int kRows = 16 * CG;
-  const int wg_row0 = tile * kWaves * kRows;
-  const int row0 = wg_row0 + wave * kRows;
+  const int wg_row0 = tile * kRowsPerWg;
+  const int row0 = wg_row0 + wave * kRowsPerWave;
 
   const SeqView sv = make_view(p, b, kvh);
-  const int wg_last_row = min(rows_total, wg_row0 + kWaves * kRows) - 1;
+  const int wg_last_row = min(rows_total, wg_row0 + kRowsPerWg) - 1;
   const int nbt = sv.nb0 + local_blocks(sv, visible_local(p, sv, wg_last_row / G));
   int w_nbt = 0;
   if (row0 < rows_total) {
-    const int w_last_row = min(rows_total, row0 + kRows) - 1;
+    const int w_last_row = min(rows_total, row0 + kRowsPerWave) - 1;
     w_nbt = sv.nb0 + local_blocks(sv, visible_local(p, sv, w_last_row / G));
   }
 
-  uint4 qf[CG][4];
-  int lim[CG];  // last visible local-segment token of this lane's column
+  uint4 qf[2][4];
+  int lim[2];
 #pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
+  for (int cg = 0; cg < 2; ++cg) {
     const int row = row0 + 16 * cg + n16;
     if (row < rows_total) {
       const int tok = row / G, h = row - tok * G;
@@ -150,120 +228,86 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
     }
   }
   const float vs = kVScale ? p.vscale[kvh] : 1.f;
+  const float c = p.scale_log2;
+  // smallest causal limit among the wave's rows (its first row); blocks past it need masking
+  const int w_min_lim = row0 < rows_total ? visible_local(p, sv, row0 / G) - 1 : -1;
 
-  float m[CG], l[CG];
-  f32x4 o[CG][8];
+  float m[2] = {kNegInf, kNegInf}, l[2] = {0.f, 0.f};
+  f32x4 o[2][8];
 #pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    m[cg] = kNegInf;
-    l[cg] = 0.f;
+  for (int cg = 0; cg < 2; ++cg)
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) o[cg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  // this wave's quarter of a block: K fragments 2w, 2w+1 and V fragments 2w, 2w+1
-  uint4 rk0, rk1, rv0, rv1;
-  auto load_share = [&](int blk) {
-    const BlockRef r = block_ref(sv, blk);
-    const int i = 2 * wave;
-    rk0 = *reinterpret_cast<const uint4*>(r.k + (i * 16 + n16) * 32 + 8 * g4);
-    rk1 = *reinterpret_cast<const uint4*>(r.k + ((i + 1) * 16 + n16) * 32 + 8 * g4);
-    rv0 = *reinterpret_cast<const uint4*>(r.v + (16 * i + n16) * 32 + 8 * g4);
-    rv1 = *reinterpret_cast<const uint4*>(r.v + (16 * (i + 1) + n16) * 32 + 8 * g4);
-  };
-  auto store_share = [&](int blk, int buf) {
-    const int i = 2 * wave;
-    lds[buf][i * 64 + lane] = rk0;
-    lds[buf][(i + 1) * 64 + lane] = rk1;
-    if (kVScale && blk < sv.nb0) {
-      lds[buf][512 + i * 64 + lane] = v_to_f16<true>(rv0, vs);
-      lds[buf][512 + (i + 1) * 64 + lane] = v_to_f16<true>(rv1, vs);
-    } else {
-      lds[buf][512 + i * 64 + lane] = v_to_f16<false>(rv0, 1.f);
-      lds[buf][512 + (i + 1) * 64 + lane] = v_to_f16<false>(rv1, 1.f);
-    }
-  };
 
   if (nbt > 0) {
-    load_share(0);
-    store_share(0, 0);
-  }
-  __syncthreads();
-  const float c = p.scale_log2;
-  for (int blk = 0; blk < nbt; ++blk) {
-    const int buf = blk & 1;
-    const bool has_next = blk + 1 < nbt;
-    if (has_next) load_share(blk + 1);
-    if (blk < w_nbt) {
-      const BlockRef r = block_ref(sv, blk);
-      uint4 kf[8], vf[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) kf[i] = lds[buf][i * 64 + lane];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vf[i] = lds[buf][512 + i * 64 + lane];
-      const bool edge = r.lo > 0 || r.hi < kBlockTokens;
-#pragma unroll
-      for (int cg = 0; cg < CG; ++cg) {
-        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          s0 = mfma_bf16(kf[kb], qf[cg][kb], s0);
-          s1 = mfma_bf16(kf[4 + kb], qf[cg][kb], s1);
-        }
-        float s[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s[i] = s0[i];
-          s[4 + i] = s1[i];
-        }
-        // token w = 8*g4 + j of the block; local tokens past the column's causal limit are hidden
-        if (edge || (!r.older && r.seg_tok + kBlockTokens - 1 > lim[cg])) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int w = 8 * g4 + j;
-            if (w < r.lo || w >= r.hi || (!r.older && r.seg_tok + w > lim[cg])) s[j] = kNegInf;
-          }
-        }
-        float mx = s[0];
-#pragma unroll
-        for (int j = 1; j < 8; ++j) mx = fmaxf(mx, s[j]);
-        mx = wave_max_across_rows(mx) * c;
-        const float m_new = fmaxf(m[cg], mx);
-        float alpha = 1.f, pr[8];
-        if (m_new == kNegInf) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) pr[j] = 0.f;
-        } else {
-          alpha = fast_exp2(m[cg] - m_new);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(s[j], c, -m_new));
-        }
-        float rs = ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
-        rs = wave_sum_across_rows(rs);
-        l[cg] = l[cg] * alpha + rs;
-        m[cg] = m_new;
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float a = __shfl(alpha, 4 * g4 + i);
-#pragma unroll
-            for (int nb = 0; nb < 8; ++nb) o[cg][nb][i] *= a;
-          }
-        }
-        const uint4 ph = make_uint4(pack_f16_rne(pr[0], pr[1]), pack_f16_rne(pr[2], pr[3]),
-                                    pack_f16_rne(pr[4], pr[5]), pack_f16_rne(pr[6], pr[7]));
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) o[cg][nb] = mfma_f16(ph, vf[nb], o[cg][nb]);
-      }
-    }
-    if (has_next) store_share(blk + 1, buf ^ 1);
+    // Software pipeline over blocks j (block j lives in LDS buffer j % 3, in registers set j % 2):
+    //   iteration i: load block i + 3 -> registers; S(i + 1) = K(i + 1) Q^T (MFMA) while the
+    //   softmax of S(i) runs on the VALU; O += P(i) V(i) (MFMA); publish block i + 2 to LDS.
+    // Loads are unconditional (indices past the end re-read the last block, an L2 hit) so the
+    // compiler can count outstanding loads for s_waitcnt.
+    const int last = nbt - 1;
+    Stage<NW> r0, r1;
+    stage_load<NW>(r0, block_ref(sv, 0), wave, n16, g4);
+    stage_load<NW>(r1, block_ref(sv, min(1, last)), wave, n16, g4);
+    stage_store<NW, kVScale>(r0, lds[0], 0 < sv.nb0, vs, wave, lane);
+    stage_store<NW, kVScale>(r1, lds[1], 1 < sv.nb0, vs, wave, lane);
+    stage_load<NW>(r0, block_ref(sv, min(2, last)), wave, n16, g4);
     __syncthreads();
+
+    auto qk = [&](const uint4* buf, f32x4& s00, f32x4& s01, f32x4& s10, f32x4& s11) {
+      s00 = s01 = s10 = s11 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const uint4 k0 = buf[kb * 64 + lane];
+        const uint4 k1 = buf[(4 + kb) * 64 + lane];
+        s00 = mfma_bf16(k0, qf[0][kb], s00);
+        s10 = mfma_bf16(k0, qf[1][kb], s10);
+        s01 = mfma_bf16(k1, qf[0][kb], s01);
+        s11 = mfma_bf16(k1, qf[1][kb], s11);
+      }
+    };
+    f32x4 c00, c01, c10, c11;  // S of the block being softmaxed
+    if (0 < w_nbt) qk(lds[0], c00, c01, c10, c11);
+    // step(i): `ld` receives block i + 3, `st` (holding block i + 2) is published to LDS
+    auto step = [&](int i, Stage<NW>& ld, Stage<NW>& st) {
+      stage_load<NW>(ld, block_ref(sv, min(i + 3, last)), wave, n16, g4);
+      f32x4 n00, n01, n10, n11;
+      const bool next = i + 1 < w_nbt;
+      if (next) qk(lds[(i + 1) % 3], n00, n01, n10, n11);
+      if (i < w_nbt) {
+        const BlockRef r = block_ref(sv, i);
+        const bool need_mask = r.lo > 0 || r.hi < kBlockTokens || (!r.older && r.seg_tok + kBlockTokens - 1 > w_min_lim);
+        const uint4 p0 = softmax_step(c00, c01, r, need_mask, lim[0], g4, c, m[0], l[0], o[0]);
+        const uint4 p1 = softmax_step(c10, c11, r, need_mask, lim[1], g4, c, m[1], l[1], o[1]);
+        const uint4* vb = lds[i % 3] + 512;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const uint4 vf = vb[nb * 64 + lane];
+          o[0][nb] = mfma_f16(p0, vf, o[0][nb]);
+          o[1][nb] = mfma_f16(p1, vf, o[1][nb]);
+        }
+      }
+      if (next) {
+        c00 = n00;
+        c01 = n01;
+        c10 = n10;
+        c11 = n11;
+      }
+      if (i + 2 < nbt) stage_store<NW, kVScale>(st, lds[(i + 2) % 3], i + 2 < sv.nb0, vs, wave, lane);
+      __syncthreads();
+    };
+    for (int i = 0; i < nbt; i += 2) {
+      step(i, r1, r0);
+      if (i + 1 >= nbt) break;
+      step(i + 1, r0, r1);
+    }
   }
 
-  // normalise and write: lane (n16 = dim in group nb, g4) holds rows 4*g4 + i of each column group
+  // normalise and write: lane (n16 = dim in slice nb, g4) holds rows 4*g4 + i of each column group
 #pragma unroll
-  for (int cg = 0; cg < CG; ++cg) {
-    const float linv = l[cg] > 0.f ? 1.f / l[cg] : 0.f;
+  for (int cg = 0; cg < 2; ++cg) {
+    const float lt = wave_sum_across_rows(l[cg]);
+    const float linv = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float f = __shfl(linv, 4 * g4 + i);
@@ -280,7 +324,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillParams p) {
       if (row < rows_total) {
         const int tok = row / G, h = row - tok * G;
         p.lse[(static_cast<int64_t>(b) * p.L + tok) * p.hq + kvh * G + h] =
-            l[cg] > 0.f ? (m[cg] + __log2f(l[cg])) * kLn2 : kNegInf;
+            lt > 0.f ? (m[cg] + __log2f(lt)) * kLn2 : kNegInf;
       }
     }
   }
@@ -357,23 +401,26 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.causal = a->causal;
   p.scale_log2 = a->sm_scale * kLog2e;
   const int64_t rows = static_cast<int64_t>(a->tokens) * group;
-  const bool wide = rows > 4 * 16;
-  const int64_t rows_per_wg = kWaves * 16 * (wide ? 4 : 1);
+  const bool wide = rows > 64;
+  const int64_t rows_per_wg = wide ? 8 * 32 : 2 * 32;
   const int64_t tiles = (rows + rows_per_wg - 1) / rows_per_wg;
-  LKV_REQUIRE(tiles < (1LL << 31), "too many query rows");
-  const dim3 grid(static_cast<unsigned>(tiles), a->num_kv_heads, a->batch);
+  const int64_t wgs = tiles * a->num_kv_heads * a->batch;
+  LKV_REQUIRE(wgs < (1LL << 31), "too many query rows");
+  p.tiles = static_cast<int32_t>(tiles);
+  p.hkv = a->num_kv_heads;
   hipStream_t s = as_stream(stream);
   const bool vsc = a->older_vscale_mode == 1;
+  const dim3 grid(static_cast<unsigned>(wgs));
   if (wide) {
     if (vsc)
-      prefill_kernel<4, true><<<grid, 256, 0, s>>>(p);
+      prefill_kernel<8, true><<<grid, 8 * 64, 0, s>>>(p);
     else
-      prefill_kernel<4, false><<<grid, 256, 0, s>>>(p);
+      prefill_kernel<8, false><<<grid, 8 * 64, 0, s>>>(p);
   } else {
     if (vsc)
-      prefill_kernel<1, true><<<grid, 256, 0, s>>>(p);
+      prefill_kernel<2, true><<<grid, 2 * 64, 0, s>>>(p);
     else
-      prefill_kernel<1, false><<<grid, 256, 0, s>>>(p);
+      prefill_kernel<2, false><<<grid, 2 * 64, 0, s>>>(p);
   }
   return check_launch("lkv_prefill_attn");
 }
