@@ -15,6 +15,11 @@ Printed JSON line (one, from this single process):
   cpu_baseline   the reference path restated with torch ops (torch.cat-free here: config 2 is
                  all shared history; F.scaled_dot_product_attention with enable_gqa) timed on
                  this host's CPU cores for a bounded sample
+  prefill        the metric's "prefill MFMA %": lkv_prefill_attn on the config-3 prefill shape
+                 (B=32, Hq=32, Hkv=8, C=1024, an 8192-token prompt = 8 chunk pieces of 1024
+                 query tokens against [older shared | recent blended | current causal]);
+                 algorithmic FLOPs 4*128*Hq*B*sum(unmasked pairs) over the kernel time, against
+                 the 2.5 PFLOP/s dense bf16 peak
 """
 
 from __future__ import annotations
@@ -35,6 +40,8 @@ B, HQ, HKV, T, D, LAYERS = 32, 32, 8, 8192, 128, 32
 BYTES_PER_CALL = 2 * B * HKV * T * D * 2 + 2 * B * HQ * D * 2  # 1,074,266,112
 FLOPS_PER_CALL = 4 * B * HQ * T * D
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0
+CHUNK = 1024
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "decode_config2_traffic.json")
 
 
@@ -47,7 +54,47 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sweep-splits", action="store_true", help="print the kernel time for several split counts")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA measurement")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one 1 GiB device copy (reference kernel for HBM byte counters)")
     return ap.parse_args()
+
+
+def prefill_measurement(ops, torch, cache, dev, reps: int = 3) -> dict:
+    """lkv_prefill_attn over the 8 chunk pieces of the config-3 prompt, timed with HIP events."""
+
+    R = ops.ring_tokens_for_chunk(CHUNK)
+    g = torch.Generator(device=dev).manual_seed(3)
+    ring = ops.TiledKV(torch.randn((B, HKV, R // 32, 4096), generator=g, device=dev).bfloat16(),
+                       torch.randn((B, HKV, R // 32, 4096), generator=g, device=dev).bfloat16())
+    q = torch.randn((B, CHUNK, HQ, D), generator=g, device=dev).bfloat16()
+    out = torch.empty_like(q)
+    vscale = torch.full((HKV,), 0.5, device=dev)
+    pieces = []
+    for c in range(T // CHUNK):
+        cur = c * CHUNK
+        rec = max(0, cur - CHUNK)
+        pieces.append(dict(older=cache, older_len=rec, vscale=vscale, local=ring, local_len=cur + CHUNK - rec,
+                           local_start=rec % R, causal=True, out=out))
+    pairs = sum(CHUNK * c * CHUNK + CHUNK * (CHUNK + 1) // 2 for c in range(T // CHUNK))
+    flops = 4 * D * HQ * B * pairs
+    for kw in pieces:
+        ops.prefill_attention(q, **kw)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for kw in pieces:
+            ops.prefill_attention(q, **kw)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "workload": "config 3 prefill attention, one layer: 8 x 1024-token chunk pieces, B=32, 8K context",
+        "flops_per_layer": flops, "ms_per_layer": round(ms, 3), "achieved_tflops": round(tflops, 1),
+        "peak_tflops": MFMA_PEAK_TFLOPS, "mfma_pct": round(100 * tflops / MFMA_PEAK_TFLOPS, 2),
+    }
 
 
 def cpu_baseline(seconds: float) -> dict:
@@ -94,7 +141,7 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path runs on one MI355X without sharding or "
-              "collectives (multi-GPU sharding is described in DESIGN.md, not measured).", file=sys.stderr)
+              "collectives; how it would shard across GPUs is a design note, not a measurement.", file=sys.stderr)
         return 2
 
     import torch
@@ -146,6 +193,13 @@ def main() -> int:
     kernel_ms = statistics.mean(e[0].elapsed_time(e[1]) for ev in events for e in ev)
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     achieved = BYTES_PER_CALL / (kernel_ms * 1e-3) / 1e9
+    prefill = None if args.no_prefill else prefill_measurement(ops, torch, cache, dev)
+    if args.calibrate_copy:
+        src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -179,6 +233,7 @@ def main() -> int:
             "traffic": traffic,
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
+        "prefill": prefill,
     }
     print(json.dumps(result), flush=True)
     return 0
