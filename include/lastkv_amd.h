@@ -139,8 +139,8 @@ int32_t lkv_decode_attn(const lkv_decode_args *args, lkv_stream_t stream);
  * Query token i of sequence b (q[b, i, h, :], bf16 [B, L, Hq, 128]) attends to the older
  * segment (all of it) and to local tokens [0, local_len[b] - L + i] (causal = 1) or to all
  * local tokens (causal = 0); the last L local tokens are the queries' own K/V.  Segments,
- * slots, clamping and vscale are as in lkv_decode_args.  out is bf16 [B, L, Hq, 128]; optional
- * lse is fp32 [B, L, Hq] (natural log).  P*V runs in fp16, which represents bf16 V exactly for
+ * slots, clamping and vscale are as in lkv_decode_args.  out is bf16 [B, L, Hq, 128] with
+ * 8-byte-aligned rows (q: 16-byte-aligned rows); optional lse is fp32 [B, L, Hq] (natural log).  P*V runs in fp16, which represents bf16 V exactly for
  * |V| < 65504 (larger magnitudes saturate).
  * ------------------------------------------------------------------------------------- */
 typedef struct lkv_prefill_args {

@@ -28,26 +28,20 @@ struct SeqView {
   int ring_blocks;
 };
 
+// Branch-free (selects only), so it can sit inside straight-line scheduling regions.
 __device__ inline BlockRef block_ref(const SeqView& s, int blk) {
+  const bool older = blk < s.nb0;
+  const int j = blk - s.nb0;
+  int rb = s.lblk0 + j;  // < 2 * ring_blocks: the segment spans at most ring_blocks + 1 blocks
+  rb = rb >= s.ring_blocks ? rb - s.ring_blocks : rb;
+  const int64_t off = static_cast<int64_t>(older ? blk : rb) * kBlockElems;
   BlockRef r;
-  if (blk < s.nb0) {
-    r.k = s.ok + static_cast<int64_t>(blk) * kBlockElems;
-    r.v = s.ov + static_cast<int64_t>(blk) * kBlockElems;
-    r.lo = 0;
-    r.hi = min(kBlockTokens, s.n0 - blk * kBlockTokens);
-    r.seg_tok = -1;
-    r.older = true;
-  } else {
-    const int j = blk - s.nb0;
-    int rb = s.lblk0 + j;
-    while (rb >= s.ring_blocks) rb -= s.ring_blocks;
-    r.k = s.lk + static_cast<int64_t>(rb) * kBlockElems;
-    r.v = s.lv + static_cast<int64_t>(rb) * kBlockElems;
-    r.lo = j == 0 ? s.lead : 0;
-    r.hi = min(kBlockTokens, s.lead + s.n1 - j * kBlockTokens);
-    r.seg_tok = j * kBlockTokens - s.lead;
-    r.older = false;
-  }
+  r.k = (older ? s.ok : s.lk) + off;
+  r.v = (older ? s.ov : s.lv) + off;
+  r.lo = (older || j != 0) ? 0 : s.lead;
+  r.hi = min(kBlockTokens, older ? s.n0 - blk * kBlockTokens : s.lead + s.n1 - j * kBlockTokens);
+  r.seg_tok = older ? -1 : j * kBlockTokens - s.lead;
+  r.older = older;
   return r;
 }
 

@@ -62,16 +62,21 @@ __device__ inline f32x4 mfma_f16(uint4 a, uint4 b, f32x4 c) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// IEEE-754 maximum (NaN-propagating): one v_maximum3_f32 for up to three inputs and no NaN
+// quieting instructions, unlike fmaxf in IEEE mode.
+__device__ inline float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ inline float fmax3_nan(float a, float b, float c) { return fmax_nan(fmax_nan(a, b), c); }
+
 // Reductions over the four 16-lane rows of a wave (lanes n, n+16, n+32, n+48) with the gfx950
 // VALU lane swaps: permlane16_swap(x, x) yields rows (0,0,2,2) and (1,1,3,3), permlane32_swap(x, x)
 // yields the lower and the upper half on both halves.  No LDS traffic, no bpermute latency.
 __device__ inline float wave_max_across_rows(float x) {
   const uint32_t u = __float_as_uint(x);
   const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float y = fmax_nan(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const uint32_t v = __float_as_uint(y);
   const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return fmax_nan(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ inline float wave_sum_across_rows(float x) {

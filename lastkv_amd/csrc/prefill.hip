@@ -8,15 +8,16 @@
 // (< 256 VGPRs, accumulators in VGPRs) for two waves per SIMD.
 // Per 32-token key block:
 //   - the NW waves each fetch 16 / NW of the block's 16 one-KiB fragments from HBM/L2 into
-//     registers two blocks ahead (one contiguous 1 KiB run per load instruction), convert V to
+//     registers one block ahead (one contiguous 1 KiB run per load instruction), convert V to
 //     fp16 (applying bf16(V * s) on the older segment) and publish the block to an LDS double
 //     buffer in lane order, so every MFMA operand is one conflict-free ds_read_b128;
 //   - S^T = K * Q^T with 16x16x32 bf16 MFMAs (exact products, fp32 sums);
-//   - online softmax in the exp2 domain (scale and max folded into one FMA), row max over the
+//   - online softmax in the exp2 domain (scale and offset folded into one FMA), row max over the
 //     four 16-lane rows with VALU lane swaps, row sums kept per lane and reduced once at the end,
-//     O rescaled only when some row's running max moved;
-//   - O += P * V with 16x16x32 fp16 MFMAs: P in [0, 1] carries 11 mantissa bits (bf16 would
-//     carry 8, a 1.7e-3 relative error the rel-L2 1e-3 bound does not allow), and bf16 V
+//     O rescaled (a branch taken only when some row's offset moved) with the factor each lane
+//     already holds;
+//   - O^T += V^T * P^T with 16x16x32 fp16 MFMAs: P in [0, 1] carries 11 mantissa bits (bf16
+//     would carry 8, a 1.7e-3 relative error the rel-L2 1e-3 bound does not allow), and bf16 V
 //     converts to fp16 exactly for |V| < 65504 (larger values saturate).
 #include "attn_common.h"
 #include "common.h"
@@ -26,6 +27,10 @@ namespace lkv {
 namespace {
 
 constexpr float kNegInf = -__builtin_inff();
+// log2 of the largest unnormalised probability.  0 keeps the exact running maximum: a larger
+// slack skips rescales but lets fp16 P round relative to a stale offset, which measurably
+// raises the output error (rel-L2 6e-4 -> 1.1e-3 on random data at slack 8).
+constexpr float kSlack = 0.f;
 
 struct PrefillParams {
   const uint16_t* q;
@@ -62,10 +67,12 @@ __device__ inline uint32_t f16x2_bits(float lo, float hi) {
 // 8 bf16 -> 8 fp16 (exact in range); with kScale the value is bf16(v * s) first.
 template <bool kScale>
 __device__ inline uint4 v_to_f16(uint4 v, float s) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
   auto cv = [s](uint32_t w) -> uint32_t {
     float lo = bf16_lo(w), hi = bf16_hi(w);
-    if (kScale) {
-      const uint32_t packed = pack_bf16x2(lo * s, hi * s);
+    if (kScale) {  // one v_cvt_pk_bf16_f32 rounds both products
+      const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo * s, hi * s}), bf16x2));
       lo = bf16_lo(packed);
       hi = bf16_hi(packed);
     }
@@ -131,61 +138,70 @@ __device__ inline void stage_load(Stage<NW>& st, const BlockRef& r, int wave, in
 
 template <int NW, bool kVScale>
 __device__ inline void stage_store(const Stage<NW>& st, uint4* buf, bool older, float vs, int wave, int lane) {
+  // bf16(v * 1) == v, so local blocks take the same instructions with s = 1 (no branch)
+  const float s = (kVScale && older) ? vs : 1.f;
 #pragma unroll
   for (int j = 0; j < 16 / NW; ++j) {
     const int f = wave + j * NW;
     uint4 x = st.r[j];
-    if (f >= 8) x = (kVScale && older) ? v_to_f16<true>(x, vs) : v_to_f16<false>(x, 1.f);
+    if (f >= 8) x = kVScale ? v_to_f16<true>(x, s) : v_to_f16<false>(x, 1.f);
     buf[f * 64 + lane] = x;
   }
 }
 
-// Softmax step of one 16-column group for one block: scores s0 (tokens 8*g4 + 0..3) and s1
-// (8*g4 + 4..7) of column n16 -> fp16 probabilities; m in the scaled exp2 domain, l partial
-// (this lane's 8 tokens only; the four rows are summed once at the end).
-__device__ inline uint4 softmax_step(f32x4 s0, f32x4 s1, const BlockRef& r, bool need_mask, int lim, int g4,
-                                     float c, float& m, float& l, f32x4 (&o)[8]) {
-  float s[8];
+// Scores of one 16-column group for one block: s0 (tokens 8*g4 + 0..3) and s1 (8*g4 + 4..7) of
+// column n16.
+__device__ inline void gather_scores(f32x4 s0, f32x4 s1, float (&s)[8]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     s[i] = s0[i];
     s[4 + i] = s1[i];
   }
-  if (need_mask) {  // wave-uniform: partial block or a local block that crosses some row's causal limit
-    const int w0 = 8 * g4;
-    const int hi = r.older ? r.hi : min(r.hi, lim - r.seg_tok + 1);
+}
+
+// -inf for tokens outside the block's valid range or past the column's causal limit.
+__device__ inline void mask_scores(float (&s)[8], const BlockRef& r, int lim, int g4) {
+  const int w0 = 8 * g4;
+  const int hi = r.older ? r.hi : min(r.hi, lim - r.seg_tok + 1);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s[j] = (w0 + j >= r.lo && w0 + j < hi) ? s[j] : kNegInf;
-  }
-  float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  for (int j = 0; j < 8; ++j) s[j] = (w0 + j >= r.lo && w0 + j < hi) ? s[j] : kNegInf;
+}
+
+// Online-softmax update of one column group -> fp16 probabilities; m in the scaled exp2 domain,
+// l partial (this lane's 8 tokens only; the four rows are summed once at the end).
+__device__ inline uint4 softmax_core(const float (&s)[8], float c, float& m, float& l, float& alpha) {
+  float mx = fmax3_nan(fmax3_nan(s[0], s[1], s[2]), fmax3_nan(s[3], s[4], s[5]), fmax_nan(s[6], s[7]));
   mx = wave_max_across_rows(mx) * c;
-  const float m_new = fmaxf(m, mx);
+  // The row keeps its exp2 offset m until a block's maximum exceeds it by more than kSlack, so
+  // P <= 2^kSlack; the final O / l ratio does not depend on the offset.
+  const bool raise = mx > m + kSlack;  // m = -inf: true for the first finite maximum
+  const float m_new = raise ? mx : m;
   // with no visible key yet m_new is -inf: subtract 0 instead, so exp2 gives 0 for every -inf
   const float m_sub = m_new == kNegInf ? 0.f : m_new;
-  const float alpha = fast_exp2(m - m_sub);
+  alpha = raise ? fast_exp2(m - m_sub) : 1.f;
   float pr[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(s[j], c, -m_sub));
   l = l * alpha + (((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7])));
   m = m_new;
-  if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-    // O rows of this lane are columns 4*g4 + i, whose factors live in lanes 4*g4 + i
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float a = __shfl(alpha, 4 * g4 + i);
-#pragma unroll
-      for (int nb = 0; nb < 8; ++nb) o[nb][i] *= a;
-    }
-  }
   return make_uint4(pack_f16_rne(pr[0], pr[1]), pack_f16_rne(pr[2], pr[3]), pack_f16_rne(pr[4], pr[5]),
                     pack_f16_rne(pr[6], pr[7]));
 }
 
-// Workgroup = NW waves x 32 query rows (two 16-column groups per wave); K/V of each 32-token
-// block are staged through a three-buffer LDS ring, loaded three blocks ahead.
+// O is accumulated transposed (O^T = V^T * P^T): lane (n16, g4) holds dims 16 * nb + 4 * g4 + i
+// of query row n16, the row whose offset and factor the lane itself holds.
+__device__ inline void rescale_rows(float alpha, f32x4 (&o)[8]) {
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) o[nb] *= alpha;
+  }
+}
+
+// Workgroup = NW waves x 32 query rows (two 16-column groups per wave); K/V of each 32-token block
+// go through a two-buffer LDS ring, fetched two blocks ahead.
 template <int NW, bool kVScale>
 __global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p) {
-  __shared__ uint4 lds[3][1024];
+  __shared__ uint4 lds[2][1024];
   constexpr int kRowsPerWave = 32;
   constexpr int kRowsPerWg = NW * kRowsPerWave;
 
@@ -211,7 +227,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p)
   }
 
   uint4 qf[2][4];
-  int lim[2];
+  int lim[2];  // last visible local-segment token of this lane's column
 #pragma unroll
   for (int cg = 0; cg < 2; ++cg) {
     const int row = row0 + 16 * cg + n16;
@@ -240,92 +256,81 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p)
     for (int nb = 0; nb < 8; ++nb) o[cg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (nbt > 0) {
-    // Software pipeline over blocks j (block j lives in LDS buffer j % 3, in registers set j % 2):
-    //   iteration i: load block i + 3 -> registers; S(i + 1) = K(i + 1) Q^T (MFMA) while the
-    //   softmax of S(i) runs on the VALU; O += P(i) V(i) (MFMA); publish block i + 2 to LDS.
-    // Loads are unconditional (indices past the end re-read the last block, an L2 hit) so the
-    // compiler can count outstanding loads for s_waitcnt.
+    // Loads are unconditional (indices past the end re-read the last block, an L2 hit) so that
+    // the compiler can count outstanding loads for s_waitcnt.
     const int last = nbt - 1;
-    Stage<NW> r0, r1;
-    stage_load<NW>(r0, block_ref(sv, 0), wave, n16, g4);
-    stage_load<NW>(r1, block_ref(sv, min(1, last)), wave, n16, g4);
-    stage_store<NW, kVScale>(r0, lds[0], 0 < sv.nb0, vs, wave, lane);
-    stage_store<NW, kVScale>(r1, lds[1], 1 < sv.nb0, vs, wave, lane);
-    stage_load<NW>(r0, block_ref(sv, min(2, last)), wave, n16, g4);
+    Stage<NW> st;
+    stage_load<NW>(st, block_ref(sv, 0), wave, n16, g4);
+    stage_store<NW, kVScale>(st, lds[0], 0 < sv.nb0, vs, wave, lane);
+    stage_load<NW>(st, block_ref(sv, min(1, last)), wave, n16, g4);
     __syncthreads();
 
-    auto qk = [&](const uint4* buf, f32x4& s00, f32x4& s01, f32x4& s10, f32x4& s11) {
-      s00 = s01 = s10 = s11 = f32x4{0.f, 0.f, 0.f, 0.f};
+    // step(blk): block blk is in `cur`, block blk + 1 is in flight into `st`; at the end it is
+    // published into `nxt` and block blk + 2 is requested.
+    auto step = [&](int blk, const uint4* cur, uint4* nxt) {
+      if (blk < w_nbt) {
+        const BlockRef r = block_ref(sv, blk);
+        f32x4 s00 = {0.f, 0.f, 0.f, 0.f}, s01 = s00, s10 = s00, s11 = s00;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const uint4 k0 = buf[kb * 64 + lane];
-        const uint4 k1 = buf[(4 + kb) * 64 + lane];
-        s00 = mfma_bf16(k0, qf[0][kb], s00);
-        s10 = mfma_bf16(k0, qf[1][kb], s10);
-        s01 = mfma_bf16(k1, qf[0][kb], s01);
-        s11 = mfma_bf16(k1, qf[1][kb], s11);
-      }
-    };
-    f32x4 c00, c01, c10, c11;  // S of the block being softmaxed
-    if (0 < w_nbt) qk(lds[0], c00, c01, c10, c11);
-    // step(i): `ld` receives block i + 3, `st` (holding block i + 2) is published to LDS
-    auto step = [&](int i, Stage<NW>& ld, Stage<NW>& st) {
-      stage_load<NW>(ld, block_ref(sv, min(i + 3, last)), wave, n16, g4);
-      f32x4 n00, n01, n10, n11;
-      const bool next = i + 1 < w_nbt;
-      if (next) qk(lds[(i + 1) % 3], n00, n01, n10, n11);
-      if (i < w_nbt) {
-        const BlockRef r = block_ref(sv, i);
-        const bool need_mask = r.lo > 0 || r.hi < kBlockTokens || (!r.older && r.seg_tok + kBlockTokens - 1 > w_min_lim);
-        const uint4 p0 = softmax_step(c00, c01, r, need_mask, lim[0], g4, c, m[0], l[0], o[0]);
-        const uint4 p1 = softmax_step(c10, c11, r, need_mask, lim[1], g4, c, m[1], l[1], o[1]);
-        const uint4* vb = lds[i % 3] + 512;
+        for (int kb = 0; kb < 4; ++kb) {
+          const uint4 k0 = cur[kb * 64 + lane];
+          const uint4 k1 = cur[(4 + kb) * 64 + lane];
+          s00 = mfma_bf16(k0, qf[0][kb], s00);
+          s10 = mfma_bf16(k0, qf[1][kb], s10);
+          s01 = mfma_bf16(k1, qf[0][kb], s01);
+          s11 = mfma_bf16(k1, qf[1][kb], s11);
+        }
+        float sc0[8], sc1[8];
+        gather_scores(s00, s01, sc0);
+        gather_scores(s10, s11, sc1);
+        // partial block, or a local block crossing the causal limit of some row of this wave
+        if (r.lo > 0 || r.hi < kBlockTokens || (!r.older && r.seg_tok + kBlockTokens - 1 > w_min_lim)) {
+          mask_scores(sc0, r, lim[0], g4);
+          mask_scores(sc1, r, lim[1], g4);
+        }
+        float a0, a1;
+        const uint4 p0 = softmax_core(sc0, c, m[0], l[0], a0);
+        const uint4 p1 = softmax_core(sc1, c, m[1], l[1], a1);
+        rescale_rows(a0, o[0]);
+        rescale_rows(a1, o[1]);
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) {
-          const uint4 vf = vb[nb * 64 + lane];
-          o[0][nb] = mfma_f16(p0, vf, o[0][nb]);
-          o[1][nb] = mfma_f16(p1, vf, o[1][nb]);
+          const uint4 vf = cur[512 + nb * 64 + lane];
+          o[0][nb] = mfma_f16(vf, p0, o[0][nb]);
+          o[1][nb] = mfma_f16(vf, p1, o[1][nb]);
         }
       }
-      if (next) {
-        c00 = n00;
-        c01 = n01;
-        c10 = n10;
-        c11 = n11;
-      }
-      if (i + 2 < nbt) stage_store<NW, kVScale>(st, lds[(i + 2) % 3], i + 2 < sv.nb0, vs, wave, lane);
+      // rows of this wave that see no more keys skip the math but keep the workgroup's staging;
+      // the store is unconditional (after the last block it rewrites a clamped copy nobody reads),
+      // so every path through the loop has the same loads outstanding and the waits stay partial
+      stage_store<NW, kVScale>(st, nxt, blk + 1 < sv.nb0, vs, wave, lane);
+      stage_load<NW>(st, block_ref(sv, min(blk + 2, last)), wave, n16, g4);
       __syncthreads();
     };
-    for (int i = 0; i < nbt; i += 2) {
-      step(i, r1, r0);
-      if (i + 1 >= nbt) break;
-      step(i + 1, r0, r1);
+    for (int blk = 0; blk < nbt; blk += 2) {
+      step(blk, lds[0], lds[1]);
+      if (blk + 1 >= nbt) break;
+      step(blk + 1, lds[1], lds[0]);
     }
   }
 
-  // normalise and write: lane (n16 = dim in slice nb, g4) holds rows 4*g4 + i of each column group
+  // normalise and write: lane (n16, g4) holds dims 16 * nb + 4 * g4 + i of row n16 of each group
 #pragma unroll
   for (int cg = 0; cg < 2; ++cg) {
     const float lt = wave_sum_across_rows(l[cg]);
     const float linv = lt > 0.f ? 1.f / lt : 0.f;
+    const int row = row0 + 16 * cg + n16;
+    if (row < rows_total) {
+      const int tok = row / G, h = row - tok * G;
+      uint16_t* orow = p.out + b * p.out_sb + tok * p.out_st + static_cast<int64_t>(kvh * G + h) * kHeadDim;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float f = __shfl(linv, 4 * g4 + i);
-      const int row = row0 + 16 * cg + 4 * g4 + i;
-      if (row < rows_total) {
-        const int tok = row / G, h = row - tok * G;
-        uint16_t* orow = p.out + b * p.out_sb + tok * p.out_st + static_cast<int64_t>(kvh * G + h) * kHeadDim;
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) orow[16 * nb + n16] = f32_to_bf16_bits(o[cg][nb][i] * f);
+      for (int nb = 0; nb < 8; ++nb) {
+        const f32x4 x = o[cg][nb] * linv;
+        *reinterpret_cast<uint2*>(orow + 16 * nb + 4 * g4) = make_uint2(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]));
       }
-    }
-    if (p.lse != nullptr && g4 == 0) {
-      const int row = row0 + 16 * cg + n16;
-      if (row < rows_total) {
-        const int tok = row / G, h = row - tok * G;
+      if (p.lse != nullptr && g4 == 0)
         p.lse[(static_cast<int64_t>(b) * p.L + tok) * p.hq + kvh * G + h] =
             lt > 0.f ? (m[cg] + __log2f(lt)) * kLn2 : kNegInf;
-      }
     }
   }
 }
@@ -360,6 +365,8 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
               "local_num_slots < batch with identity slots");
   LKV_REQUIRE((a->q_stride_b % 8) == 0 && (a->q_stride_t % 8) == 0 && (reinterpret_cast<uintptr_t>(a->q) & 15) == 0,
               "q rows must be 16-byte aligned");
+  LKV_REQUIRE((a->out_stride_b % 4) == 0 && (a->out_stride_t % 4) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 7) == 0,
+              "out rows must be 8-byte aligned");
   const uintptr_t align_or = reinterpret_cast<uintptr_t>(a->older_k) | reinterpret_cast<uintptr_t>(a->older_v) |
                              reinterpret_cast<uintptr_t>(a->local_k) | reinterpret_cast<uintptr_t>(a->local_v);
   LKV_REQUIRE((align_or & 15) == 0, "caches must be 16-byte aligned");
@@ -401,6 +408,7 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.causal = a->causal;
   p.scale_log2 = a->sm_scale * kLog2e;
   const int64_t rows = static_cast<int64_t>(a->tokens) * group;
+  // wide: 8 waves x 32 rows (two waves per SIMD); narrow: 2 waves x 32 rows
   const bool wide = rows > 64;
   const int64_t rows_per_wg = wide ? 8 * 32 : 2 * 32;
   const int64_t tiles = (rows + rows_per_wg - 1) / rows_per_wg;
