@@ -70,12 +70,14 @@ def prefill_measurement(ops, torch, cache, dev, reps: int = 3) -> dict:
     q = torch.randn((B, CHUNK, HQ, D), generator=g, device=dev).bfloat16()
     out = torch.empty_like(q)
     vscale = torch.full((HKV,), 0.5, device=dev)
+    # the fp16 V workspace of the longest piece, allocated once (a layer's calls share it)
+    workspace = torch.empty(ops.prefill_workspace_bytes(B, HKV, T - 2 * CHUNK, 2 * CHUNK, 0), dtype=torch.uint8, device=dev)
     pieces = []
     for c in range(T // CHUNK):
         cur = c * CHUNK
         rec = max(0, cur - CHUNK)
         pieces.append(dict(older=cache, older_len=rec, vscale=vscale, local=ring, local_len=cur + CHUNK - rec,
-                           local_start=rec % R, causal=True, out=out))
+                           local_start=rec % R, causal=True, out=out, workspace=workspace))
     pairs = sum(CHUNK * c * CHUNK + CHUNK * (CHUNK + 1) // 2 for c in range(T // CHUNK))
     flops = 4 * D * HQ * B * pairs
     for kw in pieces:

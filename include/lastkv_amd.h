@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 1
+#define LKV_ABI_VERSION 2
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -140,8 +140,11 @@ int32_t lkv_decode_attn(const lkv_decode_args *args, lkv_stream_t stream);
  * segment (all of it) and to local tokens [0, local_len[b] - L + i] (causal = 1) or to all
  * local tokens (causal = 0); the last L local tokens are the queries' own K/V.  Segments,
  * slots, clamping and vscale are as in lkv_decode_args.  out is bf16 [B, L, Hq, 128] with
- * 8-byte-aligned rows (q: 16-byte-aligned rows); optional lse is fp32 [B, L, Hq] (natural log).  P*V runs in fp16, which represents bf16 V exactly for
- * |V| < 65504 (larger magnitudes saturate).
+ * 8-byte-aligned rows (q: 16-byte-aligned rows); optional lse is fp32 [B, L, Hq] (natural log).
+ * P*V runs in fp16, which represents bf16 V exactly for |V| < 65504 (larger magnitudes
+ * saturate).  The call first writes the fp16 V (older segment as bf16(V * vscale)) of every key
+ * block into the caller's workspace (lkv_prefill_workspace_bytes), then runs the attention over
+ * it; both launches go on `stream`, and the workspace may be reused once the call has run.
  * ------------------------------------------------------------------------------------- */
 typedef struct lkv_prefill_args {
   int32_t struct_size; /* sizeof(lkv_prefill_args) */
@@ -181,7 +184,14 @@ typedef struct lkv_prefill_args {
   int32_t local_start_const;
   const int32_t *local_slot;
   int32_t local_num_slots;
+  void *workspace; /* >= lkv_prefill_workspace_bytes(args) bytes, 16-byte aligned */
+  int64_t workspace_bytes;
 } lkv_prefill_args;
+
+/* Workspace bytes lkv_prefill_attn needs for these args: the fp16 V of every key block of every
+ * (sequence, kv head), 8 KiB per 32-token block.  Exact when the lengths and the ring start are
+ * host constants, else bounded by the capacities.  Takes the same filled-in struct. */
+int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args *args);
 
 int32_t lkv_prefill_attn(const lkv_prefill_args *args, lkv_stream_t stream);
 

@@ -11,7 +11,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class LastKVNativeError(RuntimeError):
@@ -108,6 +108,8 @@ class PrefillArgs(ctypes.Structure):
         ("local_start_const", c_i32),
         ("local_slot", c_ptr),
         ("local_num_slots", c_i32),
+        ("workspace", c_ptr),
+        ("workspace_bytes", c_i64),
     ]
 
 
@@ -173,6 +175,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "lkv_decode_workspace_bytes": (c_i64, [c_i32, c_i32, c_i32]),
     "lkv_decode_attn": (c_i32, [ctypes.POINTER(DecodeArgs), c_ptr]),
+    "lkv_prefill_workspace_bytes": (c_i64, [ctypes.POINTER(PrefillArgs)]),
     "lkv_prefill_attn": (c_i32, [ctypes.POINTER(PrefillArgs), c_ptr]),
     "lkv_qkv_epilogue": (c_i32, [ctypes.POINTER(QkvArgs), c_ptr]),
     "lkv_blend_chunk": (

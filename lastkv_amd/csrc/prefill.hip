@@ -19,6 +19,8 @@
 //   - O^T += V^T * P^T with 16x16x32 fp16 MFMAs: P in [0, 1] carries 11 mantissa bits (bf16
 //     would carry 8, a 1.7e-3 relative error the rel-L2 1e-3 bound does not allow), and bf16 V
 //     converts to fp16 exactly for |V| < 65504 (larger values saturate).
+#include <algorithm>
+
 #include "attn_common.h"
 #include "common.h"
 #include "runtime.h"
@@ -27,10 +29,6 @@ namespace lkv {
 namespace {
 
 constexpr float kNegInf = -__builtin_inff();
-// log2 of the largest unnormalised probability.  0 keeps the exact running maximum: a larger
-// slack skips rescales but lets fp16 P round relative to a stale offset, which measurably
-// raises the output error (rel-L2 6e-4 -> 1.1e-3 on random data at slack 8).
-constexpr float kSlack = 0.f;
 
 struct PrefillParams {
   const uint16_t* q;
@@ -58,6 +56,9 @@ struct PrefillParams {
   int32_t l_nslots;
   int32_t L, hq, hkv, group, causal, tiles;
   float scale_log2;
+  int32_t vscale_mode;
+  uint16_t* v16;       // fp16 V of every key block, [B, Hkv, v16_blocks, 4096]
+  int32_t v16_blocks;  // blocks per (sequence, kv head) in v16
 };
 
 __device__ inline uint32_t f16x2_bits(float lo, float hi) {
@@ -120,43 +121,62 @@ __device__ inline int visible_local(const PrefillParams& p, const SeqView& sv, i
 
 // One fragment = one 16-byte-per-lane MFMA operand = 1 KiB; a 32-token block is 16 fragments:
 // K fragments f = u * 4 + kb (u: 16-token half, kb: 32-dim slice) and V fragments 8 + nb (nb:
-// 16-dim slice).  Wave w of NW stages fragments w, w + NW, ... of each block.
+// 16-dim slice).  Wave w of NW stages fragments w, w + NW, ... of each block.  Inside a fragment
+// lane (n16, g4) holds the 16 bytes at n16 * 64 + g4 * 16.
 template <int NW>
 struct Stage {
   uint4 r[16 / NW];
 };
 
+// Wave-uniform base pointers and byte ranges of one sequence / kv head: K and V of the older
+// segment and of the ring.  Each load builds its buffer resource from the selected base (scalar
+// instructions only).
+struct SegBase {
+  const uint16_t *ok, *lk, *v16;
+  int32_t o_bytes, l_bytes, v16_bytes;
+};
+
+__device__ inline const uint16_t* uniform_ptr(const uint16_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint16_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base, int32_t bytes) {
+  // word 3 = 0x00020000: raw (untyped) 32-bit data format, the gfx9 setting for byte-addressed loads
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, base ? bytes : 0, 0x00020000);
+}
+
+// Byte offset of block blk inside its segment array, and which segment it is in.
+__device__ inline int block_byte_offset(const SeqView& sv, int blk, bool& older) {
+  older = blk < sv.nb0;
+  int rb = sv.lblk0 + (blk - sv.nb0);
+  rb = rb >= sv.ring_blocks ? rb - sv.ring_blocks : rb;
+  return (older ? blk : rb) * (kBlockElems * 2);
+}
+
 template <int NW>
-__device__ inline void stage_load(Stage<NW>& st, const BlockRef& r, int wave, int n16, int g4) {
+__device__ inline void stage_load(Stage<NW>& st, const SegBase sb, const SeqView& sv, int blk, int wave,
+                                  int lane_off) {
+  bool older;
+  const int boff = __builtin_amdgcn_readfirstlane(block_byte_offset(sv, blk, older));
+  const int32_t kbytes = older ? sb.o_bytes : sb.l_bytes;
+  const uint16_t* kbase = uniform_ptr(older ? sb.ok : sb.lk);
+  const int voff = blk * (kBlockElems * 2);  // the fp16 V workspace is in block order
 #pragma unroll
   for (int j = 0; j < 16 / NW; ++j) {
-    const int f = wave + j * NW;
-    const uint16_t* src = f < 8 ? r.k + (f * 16 + n16) * 32 + 8 * g4 : r.v + (16 * (f - 8) + n16) * 32 + 8 * g4;
-    st.r[j] = *reinterpret_cast<const uint4*>(src);
+    const int f = wave + j * NW;  // wave < NW, so f < 8 exactly when j < 8 / NW
+    const __amdgpu_buffer_rsrc_t r = j < 8 / NW ? make_rsrc(kbase, kbytes) : make_rsrc(sb.v16, sb.v16_bytes);
+    const int off = (j < 8 / NW ? boff : voff) + (f & 7) * 1024;
+    st.r[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, off, 0));
   }
 }
 
-template <int NW, bool kVScale>
-__device__ inline void stage_store(const Stage<NW>& st, uint4* buf, bool older, float vs, int wave, int lane) {
-  // bf16(v * 1) == v, so local blocks take the same instructions with s = 1 (no branch)
-  const float s = (kVScale && older) ? vs : 1.f;
+template <int NW>
+__device__ inline void stage_store(const Stage<NW>& st, uint4* buf, int wave, int lane) {
 #pragma unroll
-  for (int j = 0; j < 16 / NW; ++j) {
-    const int f = wave + j * NW;
-    uint4 x = st.r[j];
-    if (f >= 8) x = kVScale ? v_to_f16<true>(x, s) : v_to_f16<false>(x, 1.f);
-    buf[f * 64 + lane] = x;
-  }
-}
-
-// Scores of one 16-column group for one block: s0 (tokens 8*g4 + 0..3) and s1 (8*g4 + 4..7) of
-// column n16.
-__device__ inline void gather_scores(f32x4 s0, f32x4 s1, float (&s)[8]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    s[i] = s0[i];
-    s[4 + i] = s1[i];
-  }
+  for (int j = 0; j < 16 / NW; ++j) buf[(wave + j * NW) * 64 + lane] = st.r[j];
 }
 
 // -inf for tokens outside the block's valid range or past the column's causal limit.
@@ -167,42 +187,93 @@ __device__ inline void mask_scores(float (&s)[8], const BlockRef& r, int lim, in
   for (int j = 0; j < 8; ++j) s[j] = (w0 + j >= r.lo && w0 + j < hi) ? s[j] : kNegInf;
 }
 
-// Online-softmax update of one column group -> fp16 probabilities; m in the scaled exp2 domain,
-// l partial (this lane's 8 tokens only; the four rows are summed once at the end).
-__device__ inline uint4 softmax_core(const float (&s)[8], float c, float& m, float& l, float& alpha) {
-  float mx = fmax3_nan(fmax3_nan(s[0], s[1], s[2]), fmax3_nan(s[3], s[4], s[5]), fmax_nan(s[6], s[7]));
-  mx = wave_max_across_rows(mx) * c;
-  // The row keeps its exp2 offset m until a block's maximum exceeds it by more than kSlack, so
-  // P <= 2^kSlack; the final O / l ratio does not depend on the offset.
-  const bool raise = mx > m + kSlack;  // m = -inf: true for the first finite maximum
-  const float m_new = raise ? mx : m;
-  // with no visible key yet m_new is -inf: subtract 0 instead, so exp2 gives 0 for every -inf
-  const float m_sub = m_new == kNegInf ? 0.f : m_new;
-  alpha = raise ? fast_exp2(m - m_sub) : 1.f;
-  float pr[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(s[j], c, -m_sub));
-  l = l * alpha + (((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7])));
-  m = m_new;
-  return make_uint4(pack_f16_rne(pr[0], pr[1]), pack_f16_rne(pr[2], pr[3]), pack_f16_rne(pr[4], pr[5]),
-                    pack_f16_rne(pr[6], pr[7]));
+__device__ inline float max8(const float (&s)[8]) {
+  return fmax_nan(fmax3_nan(fmax3_nan(s[0], s[1], s[2]), fmax3_nan(s[3], s[4], s[5]), s[6]), s[7]);
 }
 
-// O is accumulated transposed (O^T = V^T * P^T): lane (n16, g4) holds dims 16 * nb + 4 * g4 + i
-// of query row n16, the row whose offset and factor the lane itself holds.
-__device__ inline void rescale_rows(float alpha, f32x4 (&o)[8]) {
+// Online-softmax state of one 16-row column group: m = the row's score reference (raw scores),
+// mc = m * c, the exp2 offset (0 while m = -inf), l = this lane's part of the row sum.
+// Probabilities are P = 2^(s c - mc).  m is the exact row maximum after the first block; later it
+// is raised only when some P reaches 2 (a new maximum more than 1 / c above m), so P < 2 always
+// and fp16 keeps its full 11-bit precision.  O / l does not depend on the offset.
+struct RowState {
+  float m, mc, l;
+};
+
+// Raises each row's reference to its maximum over this block (lm = lane maxima) and rescales l
+// and O by 2^(mc_old - mc_new).  Runs in a wave-uniform branch taken on the first block and
+// whenever some P reached 2.
+__device__ inline void raise_rows(RowState& rs, float lm, float c, f32x4 (&o)[8]) {
+  const float bm = wave_max_across_rows(lm);
+  const bool up = bm > rs.m;  // m = -inf: true for the first finite maximum
+  const float mc_new = up ? bm * c : rs.mc;
+  const float alpha = up ? fast_exp2(rs.mc - mc_new) : 1.f;  // l and O are 0 while m = -inf
+  rs.m = up ? bm : rs.m;
+  rs.mc = rs.m == kNegInf ? 0.f : mc_new;
+  rs.l *= alpha;
   if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) o[nb] *= alpha;
   }
 }
 
-// Workgroup = NW waves x 32 query rows (two 16-column groups per wave); K/V of each 32-token block
-// go through a two-buffer LDS ring, fetched two blocks ahead.
-template <int NW, bool kVScale>
-__global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p) {
-  __shared__ uint4 lds[2][1024];
-  constexpr int kRowsPerWave = 32;
+// fp32 probabilities of 8 scores and their fp16 packing.
+__device__ inline void probs(const float (&s)[8], float c, float mc, float (&pr)[8], uint32_t (&w)[4]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(s[j], c, -mc));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w[j] = pack_f16_rne(pr[2 * j], pr[2 * j + 1]);
+}
+
+// Nonzero when some packed fp16 probability is >= 2 (exponent field >= 16), infinite or NaN.
+__device__ inline uint32_t probs_overflow(const uint32_t (&w)[4]) {
+  return (w[0] | w[1] | w[2] | w[3]) & 0x40004000u;
+}
+
+__device__ inline float sum8(const float (&pr)[8]) {
+  return ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+}
+
+template <int N>
+struct IC {
+  static constexpr int value = N;
+};
+
+// V pre-pass: every key block of every (sequence, kv head) as fp16 in block order [older |
+// local], with the older segment as bf16(V * s) (the reference's rounded _scale()).  The
+// attention kernel's query tiles then stage V as plain copies instead of each converting it.
+// One workgroup per (block, kv head, sequence); 256 threads x 16 values.
+__global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
+  const int blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const SeqView sv = make_view(p, b, kvh);
+  if (blk >= sv.nb0 + local_blocks(sv, sv.n1)) return;
+  bool older;
+  const int boff = block_byte_offset(sv, blk, older);
+  const uint16_t* src = (older ? sv.ov : sv.lv) + boff / 2;
+  uint16_t* dst = p.v16 + ((static_cast<int64_t>(b) * p.hkv + kvh) * p.v16_blocks + blk) * kBlockElems;
+  const float s = (p.vscale_mode && older) ? p.vscale[kvh] : 1.f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int e = (threadIdx.x + j * 256) * 8;
+    const uint4 x = *reinterpret_cast<const uint4*>(src + e);
+    // bf16(v * 1) == v, so the unscaled blocks take the same instructions
+    *reinterpret_cast<uint4*>(dst + e) = v_to_f16<true>(x, s);
+  }
+}
+
+// Workgroup = NW waves x 16 * CG query rows (CG 16-column groups per wave).  K (bf16, from the caches)
+// and V (fp16, from the pre-pass) blocks go through a ring of kRing LDS buffers; two register
+// stage sets keep the global loads two steps ahead of their LDS store.  Step i (block i in
+// buffer i % 4, block i + 1 in buffer (i + 1) % 4): probabilities of block i from the scores
+// computed in step i - 1, QK^T of block i + 1, P V of block i, store block i + 2 into buffer
+// (i + 2) % 4, load block i + 4, one barrier.
+template <int NW, int CG, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_kernel(
+    const PrefillParams p) {
+  constexpr int kRing = 4;
+  constexpr int kBuf = 1024;  // uint4 per block buffer (16 KiB)
+  __shared__ uint4 lds[kRing * kBuf];
+  constexpr int kRowsPerWave = 16 * CG;
   constexpr int kRowsPerWg = NW * kRowsPerWave;
 
   const int lane = threadIdx.x & 63;
@@ -217,19 +288,20 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p)
   const int wg_row0 = tile * kRowsPerWg;
   const int row0 = wg_row0 + wave * kRowsPerWave;
 
-  const SeqView sv = make_view(p, b, kvh);
+  SeqView sv = make_view(p, b, kvh);
+  // these are wave-uniform; keeping them in scalar registers keeps every block offset scalar
+  sv.n0 = __builtin_amdgcn_readfirstlane(sv.n0);
+  sv.n1 = __builtin_amdgcn_readfirstlane(sv.n1);
+  sv.nb0 = __builtin_amdgcn_readfirstlane(sv.nb0);
+  sv.lblk0 = __builtin_amdgcn_readfirstlane(sv.lblk0);
+  sv.lead = __builtin_amdgcn_readfirstlane(sv.lead);
   const int wg_last_row = min(rows_total, wg_row0 + kRowsPerWg) - 1;
-  const int nbt = sv.nb0 + local_blocks(sv, visible_local(p, sv, wg_last_row / G));
-  int w_nbt = 0;
-  if (row0 < rows_total) {
-    const int w_last_row = min(rows_total, row0 + kRowsPerWave) - 1;
-    w_nbt = sv.nb0 + local_blocks(sv, visible_local(p, sv, w_last_row / G));
-  }
+  const int nbt = __builtin_amdgcn_readfirstlane(sv.nb0 + local_blocks(sv, visible_local(p, sv, wg_last_row / G)));
 
-  uint4 qf[2][4];
-  int lim[2];  // last visible local-segment token of this lane's column
+  uint4 qf[CG][4];
+  int lim[CG];  // last visible local-segment token of this lane's column
 #pragma unroll
-  for (int cg = 0; cg < 2; ++cg) {
+  for (int cg = 0; cg < CG; ++cg) {
     const int row = row0 + 16 * cg + n16;
     if (row < rows_total) {
       const int tok = row / G, h = row - tok * G;
@@ -243,81 +315,162 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p)
       lim[cg] = -1;
     }
   }
-  const float vs = kVScale ? p.vscale[kvh] : 1.f;
   const float c = p.scale_log2;
   // smallest causal limit among the wave's rows (its first row); blocks past it need masking
-  const int w_min_lim = row0 < rows_total ? visible_local(p, sv, row0 / G) - 1 : -1;
+  const int w_min_lim =
+      __builtin_amdgcn_readfirstlane(row0 < rows_total ? visible_local(p, sv, row0 / G) - 1 : -1);
 
-  float m[2] = {kNegInf, kNegInf}, l[2] = {0.f, 0.f};
-  f32x4 o[2][8];
+  RowState rs[CG];
 #pragma unroll
-  for (int cg = 0; cg < 2; ++cg)
+  for (int cg = 0; cg < CG; ++cg) rs[cg] = RowState{kNegInf, 0.f, 0.f};
+  f32x4 o[CG][8];
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg)
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) o[cg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (nbt > 0) {
+    SegBase rsrc;
+    rsrc.ok = uniform_ptr(sv.ok);
+    rsrc.lk = uniform_ptr(sv.lk);
+    rsrc.v16 = uniform_ptr(p.v16 + (static_cast<int64_t>(b) * p.hkv + kvh) * p.v16_blocks * kBlockElems);
+    rsrc.o_bytes = p.o_cap * (kHeadDim * 2);
+    rsrc.l_bytes = p.ring_blocks * (kBlockElems * 2);
+    rsrc.v16_bytes = p.v16_blocks * (kBlockElems * 2);
+    const int lane_off = n16 * 64 + g4 * 16;
     // Loads are unconditional (indices past the end re-read the last block, an L2 hit) so that
     // the compiler can count outstanding loads for s_waitcnt.
     const int last = nbt - 1;
-    Stage<NW> st;
-    stage_load<NW>(st, block_ref(sv, 0), wave, n16, g4);
-    stage_store<NW, kVScale>(st, lds[0], 0 < sv.nb0, vs, wave, lane);
-    stage_load<NW>(st, block_ref(sv, min(1, last)), wave, n16, g4);
+
+    Stage<NW> sa, sb;
+    stage_load<NW>(sa, rsrc, sv, 0, wave, lane_off);
+    stage_load<NW>(sb, rsrc, sv, min(1, last), wave, lane_off);
+    stage_store<NW>(sa, lds, wave, lane);
+    stage_load<NW>(sa, rsrc, sv, min(2, last), wave, lane_off);
+    stage_store<NW>(sb, lds + kBuf, wave, lane);
+    stage_load<NW>(sb, rsrc, sv, min(3, last), wave, lane_off);
     __syncthreads();
 
-    // step(blk): block blk is in `cur`, block blk + 1 is in flight into `st`; at the end it is
-    // published into `nxt` and block blk + 2 is requested.
-    auto step = [&](int blk, const uint4* cur, uint4* nxt) {
-      if (blk < w_nbt) {
-        const BlockRef r = block_ref(sv, blk);
-        f32x4 s00 = {0.f, 0.f, 0.f, 0.f}, s01 = s00, s10 = s00, s11 = s00;
+    // S^T of block 0: sc[cg][u] holds tokens 8 * g4 + 4u .. + 3 of this lane's column n16 of
+    // group cg
+    f32x4 sc[CG][2];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const uint4 k0 = cur[kb * 64 + lane];
-          const uint4 k1 = cur[(4 + kb) * 64 + lane];
-          s00 = mfma_bf16(k0, qf[0][kb], s00);
-          s10 = mfma_bf16(k0, qf[1][kb], s10);
-          s01 = mfma_bf16(k1, qf[0][kb], s01);
-          s11 = mfma_bf16(k1, qf[1][kb], s11);
-        }
-        float sc0[8], sc1[8];
-        gather_scores(s00, s01, sc0);
-        gather_scores(s10, s11, sc1);
-        // partial block, or a local block crossing the causal limit of some row of this wave
-        if (r.lo > 0 || r.hi < kBlockTokens || (!r.older && r.seg_tok + kBlockTokens - 1 > w_min_lim)) {
-          mask_scores(sc0, r, lim[0], g4);
-          mask_scores(sc1, r, lim[1], g4);
-        }
-        float a0, a1;
-        const uint4 p0 = softmax_core(sc0, c, m[0], l[0], a0);
-        const uint4 p1 = softmax_core(sc1, c, m[1], l[1], a1);
-        rescale_rows(a0, o[0]);
-        rescale_rows(a1, o[1]);
+    for (int cg = 0; cg < CG; ++cg)
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) {
-          const uint4 vf = cur[512 + nb * 64 + lane];
-          o[0][nb] = mfma_f16(vf, p0, o[0][nb]);
-          o[1][nb] = mfma_f16(vf, p1, o[1][nb]);
+      for (int u = 0; u < 2; ++u) sc[cg][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const uint4 k0 = lds[kb * 64 + lane];
+      const uint4 k1 = lds[(4 + kb) * 64 + lane];
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        sc[cg][0] = mfma_bf16(k0, qf[cg][kb], sc[cg][0]);
+        sc[cg][1] = mfma_bf16(k1, qf[cg][kb], sc[cg][1]);
+      }
+    }
+
+    // Step i: the 16 LDS reads (K of block i + 1, V of block i) are issued first so their latency
+    // passes under the mask work; then the QK^T MFMAs of block i + 1 are interleaved with the
+    // probabilities of block i (1 MFMA : 2 VALU : 1 exp), and the P V MFMAs of block i with the
+    // row sums and the staging of block i + 2.  A wave whose rows see no keys in a block still
+    // runs it: the mask makes every score -inf, so P = 0 and O, l, m do not change (at most two
+    // blocks per wave at the causal edge).
+    auto step = [&](auto rc, int blk) {
+      constexpr int R = decltype(rc)::value;
+      const uint4* cur = lds + R * kBuf;
+      const uint4* nxt = lds + ((R + 1) % kRing) * kBuf;
+      uint4* wr = lds + ((R + 2) % kRing) * kBuf;
+      Stage<NW>& st = (R % 2 == 0) ? sa : sb;
+      uint4 kf[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) kf[t] = nxt[t * 64 + lane];
+      const BlockRef r = block_ref(sv, blk);
+      float s[CG][8];
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s[cg][i] = sc[cg][0][i];
+          s[cg][4 + i] = sc[cg][1][i];
+        }
+      // partial block, or a local block crossing the causal limit of some row of this wave
+      if (r.lo > 0 || r.hi < kBlockTokens || (!r.older && r.seg_tok + kBlockTokens - 1 > w_min_lim)) {
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) mask_scores(s[cg], r, lim[cg], g4);
+      }
+      // QK^T of block i + 1 (past the last block it multiplies a stale buffer; never used)
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) sc[cg][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) {
+          sc[cg][0] = mfma_bf16(kf[kb], qf[cg][kb], sc[cg][0]);
+          sc[cg][1] = mfma_bf16(kf[4 + kb], qf[cg][kb], sc[cg][1]);
+        }
+      uint32_t pw[CG][4];
+      float lb[CG];  // this block's contribution to l
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) {
+        float pr[8];
+        probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
+        lb[cg] = sum8(pr);
+      }
+      uint4 vf[8];
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) vf[nb] = cur[512 + nb * 64 + lane];
+#pragma unroll
+      for (int i = 0; i < 8 * CG; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (QK^T of block i + 1)
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);  // exp
+      }
+      // first block, or a new row maximum: exact maxima, rescale, recompute this block's P
+      uint32_t ovf = 0;
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) ovf |= probs_overflow(pw[cg]);
+      if (blk == 0 || __builtin_amdgcn_ballot_w64(ovf != 0)) {
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) {
+          raise_rows(rs[cg], max8(s[cg]), c, o[cg]);
+          float pr[8];
+          probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
+          lb[cg] = sum8(pr);
         }
       }
-      // rows of this wave that see no more keys skip the math but keep the workgroup's staging;
-      // the store is unconditional (after the last block it rewrites a clamped copy nobody reads),
-      // so every path through the loop has the same loads outstanding and the waits stay partial
-      stage_store<NW, kVScale>(st, nxt, blk + 1 < sv.nb0, vs, wave, lane);
-      stage_load<NW>(st, block_ref(sv, min(blk + 2, last)), wave, n16, g4);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg)
+          o[cg][nb] = mfma_f16(vf[nb], make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]), o[cg][nb]);
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) rs[cg].l += lb[cg];
+      stage_store<NW>(st, wr, wave, lane);
+      stage_load<NW>(st, rsrc, sv, min(blk + 4, last), wave, lane_off);
+#pragma unroll
+      for (int i = 0; i < 8 * CG; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (P V of block i)
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+      }
       __syncthreads();
     };
-    for (int blk = 0; blk < nbt; blk += 2) {
-      step(blk, lds[0], lds[1]);
+    for (int blk = 0; blk < nbt; blk += kRing) {
+      step(IC<0>{}, blk);
       if (blk + 1 >= nbt) break;
-      step(blk + 1, lds[1], lds[0]);
+      step(IC<1>{}, blk + 1);
+      if (blk + 2 >= nbt) break;
+      step(IC<2>{}, blk + 2);
+      if (blk + 3 >= nbt) break;
+      step(IC<3>{}, blk + 3);
     }
   }
 
   // normalise and write: lane (n16, g4) holds dims 16 * nb + 4 * g4 + i of row n16 of each group
 #pragma unroll
-  for (int cg = 0; cg < 2; ++cg) {
-    const float lt = wave_sum_across_rows(l[cg]);
+  for (int cg = 0; cg < CG; ++cg) {
+    const float lt = wave_sum_across_rows(rs[cg].l);
     const float linv = lt > 0.f ? 1.f / lt : 0.f;
     const int row = row0 + 16 * cg + n16;
     if (row < rows_total) {
@@ -330,13 +483,39 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const PrefillParams p)
       }
       if (p.lse != nullptr && g4 == 0)
         p.lse[(static_cast<int64_t>(b) * p.L + tok) * p.hq + kvh * G + h] =
-            lt > 0.f ? (m[cg] + __log2f(lt)) * kLn2 : kNegInf;
+            lt > 0.f ? (rs[cg].mc + __log2f(lt)) * kLn2 : kNegInf;
     }
   }
 }
 
 }  // namespace
 }  // namespace lkv
+
+namespace {
+
+// Key blocks per (sequence, kv head) the fp16 V workspace must hold: exact when the lengths and
+// the ring start are host constants, else bounded by the capacities.
+int64_t v16_blocks(const lkv_prefill_args* a) {
+  using namespace lkv;
+  int64_t n0 = 0, lblocks = 0;
+  if (a->older_k != nullptr)
+    n0 = a->older_len ? a->older_capacity_tokens
+                      : std::min<int64_t>(std::max(a->older_len_const, 0), a->older_capacity_tokens);
+  if (a->local_k != nullptr) {
+    const int64_t ring = static_cast<int64_t>(a->local_ring_blocks) * kBlockTokens;
+    const int64_t n1 = a->local_len ? ring : std::min<int64_t>(std::max(a->local_len_const, 0), ring);
+    const int64_t lead = a->local_start ? kBlockTokens - 1 : (a->local_start_const & (kBlockTokens - 1));
+    lblocks = n1 > 0 ? (lead + n1 + kBlockTokens - 1) / kBlockTokens : 0;
+  }
+  return (n0 + kBlockTokens - 1) / kBlockTokens + lblocks;
+}
+
+}  // namespace
+
+extern "C" int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args* a) {
+  if (a == nullptr || a->batch <= 0 || a->num_kv_heads <= 0) return 0;
+  return static_cast<int64_t>(a->batch) * a->num_kv_heads * v16_blocks(a) * (lkv::kBlockElems * 2);
+}
 
 extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stream) {
   using namespace lkv;
@@ -360,6 +539,11 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   LKV_REQUIRE(a->older_k == nullptr || a->older_slot != nullptr || a->older_num_slots >= a->batch,
               "older_num_slots < batch with identity slots");
   LKV_REQUIRE(a->local_k == nullptr || a->local_ring_blocks > 0, "local ring needs at least one block");
+  // each (slot, kv head) segment is addressed by a buffer resource with a 31-bit byte range
+  LKV_REQUIRE(a->older_k == nullptr || static_cast<int64_t>(a->older_capacity_tokens) * 256 < (1LL << 31),
+              "older capacity must be below 8M tokens");
+  LKV_REQUIRE(a->local_k == nullptr || static_cast<int64_t>(a->local_ring_blocks) * 8192 < (1LL << 31),
+              "local ring must be below 8M tokens");
   LKV_REQUIRE(a->local_k == nullptr || a->local_num_slots > 0, "local_num_slots must be positive");
   LKV_REQUIRE(a->local_k == nullptr || a->local_slot != nullptr || a->local_num_slots >= a->batch,
               "local_num_slots < batch with identity slots");
@@ -372,7 +556,15 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   LKV_REQUIRE((align_or & 15) == 0, "caches must be 16-byte aligned");
   LKV_REQUIRE((a->older_seq_stride | a->older_head_stride | a->local_seq_stride | a->local_head_stride) % 8 == 0,
               "cache strides must be multiples of 8 elements");
+  LKV_REQUIRE(a->batch <= 65535 && a->num_kv_heads <= 65535, "batch and num_kv_heads must be <= 65535");
   if (a->batch == 0 || a->tokens == 0) return LKV_OK;
+  const int64_t vblocks = v16_blocks(a);
+  const int64_t need = lkv_prefill_workspace_bytes(a);
+  LKV_REQUIRE(vblocks * kBlockElems * 2 < (1LL << 31), "too many key blocks per sequence");
+  LKV_REQUIRE(vblocks == 0 || (a->workspace != nullptr && a->workspace_bytes >= need),
+              "prefill needs a workspace of %lld bytes (lkv_prefill_workspace_bytes), got %lld",
+              static_cast<long long>(need), static_cast<long long>(a->workspace_bytes));
+  LKV_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 15) == 0, "workspace must be 16-byte aligned");
   PrefillParams p;
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_stride_b;
@@ -407,8 +599,11 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.group = group;
   p.causal = a->causal;
   p.scale_log2 = a->sm_scale * kLog2e;
+  p.vscale_mode = a->older_vscale_mode;
+  p.v16 = static_cast<uint16_t*>(a->workspace);
+  p.v16_blocks = static_cast<int32_t>(vblocks);
   const int64_t rows = static_cast<int64_t>(a->tokens) * group;
-  // wide: 8 waves x 32 rows (two waves per SIMD); narrow: 2 waves x 32 rows
+  // wide: 8 waves x 32 rows (two waves per SIMD); narrow: 2 waves x 32 rows for short calls
   const bool wide = rows > 64;
   const int64_t rows_per_wg = wide ? 8 * 32 : 2 * 32;
   const int64_t tiles = (rows + rows_per_wg - 1) / rows_per_wg;
@@ -417,18 +612,16 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.tiles = static_cast<int32_t>(tiles);
   p.hkv = a->num_kv_heads;
   hipStream_t s = as_stream(stream);
-  const bool vsc = a->older_vscale_mode == 1;
-  const dim3 grid(static_cast<unsigned>(wgs));
-  if (wide) {
-    if (vsc)
-      prefill_kernel<8, true><<<grid, 8 * 64, 0, s>>>(p);
-    else
-      prefill_kernel<8, false><<<grid, 8 * 64, 0, s>>>(p);
+  if (vblocks == 0) {
+    // no keys at all: every row's output is zero (the main kernel skips its loop)
   } else {
-    if (vsc)
-      prefill_kernel<2, true><<<grid, 2 * 64, 0, s>>>(p);
-    else
-      prefill_kernel<2, false><<<grid, 2 * 64, 0, s>>>(p);
+    v16_stage_kernel<<<dim3(static_cast<unsigned>(vblocks), a->num_kv_heads, a->batch), 256, 0, s>>>(p);
+    if (const int32_t e = check_launch("lkv_prefill_attn (V pre-pass)")) return e;
   }
+  const dim3 grid(static_cast<unsigned>(wgs));
+  if (wide)
+    prefill_kernel<8, 2, 2><<<grid, 8 * 64, 0, s>>>(p);
+  else
+    prefill_kernel<2, 2, 1><<<grid, 2 * 64, 0, s>>>(p);
   return check_launch("lkv_prefill_attn");
 }

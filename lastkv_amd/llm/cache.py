@@ -38,6 +38,7 @@ class LastKVCache:
         self._store: ops.TiledKV | None = None
         self._ring_k: torch.Tensor | None = None
         self._ring_v: torch.Tensor | None = None
+        self._workspace: torch.Tensor | None = None
 
     # ------------------------------------------------------------------ storage
     @property
@@ -86,6 +87,16 @@ class LastKVCache:
 
     def ring(self, layer: int) -> ops.TiledKV:
         return ops.TiledKV(self._ring_k[layer], self._ring_v[layer])
+
+    def prefill_workspace(self, nbytes: int) -> torch.Tensor:
+        """Scratch for the prefill kernel's fp16 V copy, shared by all layers and grown on demand
+        (each layer's call has finished with it before the next layer's call runs on the stream)."""
+
+        if self._store is None:
+            raise RuntimeError("cache is not allocated yet")
+        if self._workspace is None or self._workspace.numel() < nbytes:
+            self._workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=self._store.device)
+        return self._workspace
 
     @property
     def ring_k(self) -> torch.Tensor:

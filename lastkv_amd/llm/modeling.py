@@ -148,7 +148,8 @@ class LastKVAttention(nn.Module):
         if L == 1:
             out = ops.decode_attention(qn.view(B, H, D), **segments)
         else:
-            out = ops.prefill_attention(qn, causal=True, **segments)
+            ws = cache.prefill_workspace(ops.prefill_workspace_bytes(B, Hkv, rec, p0 + L - rec, rec % ops.BLOCK_TOKENS))
+            out = ops.prefill_attention(qn, causal=True, workspace=ws, **segments)
         return self.o_proj(out.reshape(B, L, H * D))
 
 

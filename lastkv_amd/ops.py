@@ -302,10 +302,14 @@ def prefill_attention(
     sm_scale: float | None = None,
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention of ``q`` ``[B, L, Hq, 128]`` (L query tokens per sequence, the last L tokens of
     the local segment) over ``[older | local]``; the local segment is bottom-right causal
-    (``causal``) or fully visible.  Returns ``out`` ``[B, L, Hq, 128]`` bf16."""
+    (``causal``) or fully visible.  Returns ``out`` ``[B, L, Hq, 128]`` bf16.
+
+    ``workspace`` (uint8, 16-byte aligned, at least ``prefill_workspace_bytes`` of the same
+    arguments) receives the fp16 V of every key block; without it one is allocated per call."""
 
     _require_bf16_cuda("q", q)
     _require(q.dim() == 4 and q.shape[-1] == HEAD_DIM, "q must be [B, L, Hq, 128]")
@@ -331,8 +335,23 @@ def prefill_attention(
     a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
     a.lse = _ptr(lse)
     lib = _lib.load()
+    need = int(lib.lkv_prefill_workspace_bytes(ctypes.byref(a)))
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+    _require(workspace.device == device and workspace.is_contiguous(), "workspace must be a contiguous tensor on the query's device")
+    a.workspace = workspace.data_ptr()
+    a.workspace_bytes = workspace.numel() * workspace.element_size()
+    _require(a.workspace_bytes >= need, f"prefill workspace too small: {a.workspace_bytes} < {need} bytes")
     _lib.check(lib.lkv_prefill_attn(ctypes.byref(a), _stream(device)), "lkv_prefill_attn")
     return out
+
+
+def prefill_workspace_bytes(batch: int, kv_heads: int, older_tokens: int, local_tokens: int, local_lead: int = 31) -> int:
+    """Upper bound of the prefill workspace for segments of at most ``older_tokens`` and
+    ``local_tokens`` keys (``local_lead``: the ring start's offset inside its 32-token block)."""
+
+    blocks = -(-older_tokens // 32) + (-(-(local_lead + local_tokens) // 32) if local_tokens > 0 else 0)
+    return batch * kv_heads * blocks * 8192
 
 
 def _rows(name: str, t: torch.Tensor, heads: int) -> tuple[int, int, int]:

@@ -138,6 +138,60 @@ def test_prefill_agrees_with_decode_for_single_token():
     _close(a[:, 0], d.float().cpu().numpy(), "prefill L=1 vs decode")
 
 
+def _torch_fp32_attention(q, k, v, n_local_visible_last):
+    """fp32 GQA attention on the GPU with a bottom-right causal mask over the last keys.
+    q [Hq, L, D], k/v [Hkv, T, D] float32 tensors; query i sees keys [0, T - L + i]."""
+
+    Hq, L, _ = q.shape
+    Hkv, T, _ = k.shape
+    g = Hq // Hkv
+    kk = k.repeat_interleave(g, 0).contiguous()
+    vv = v.repeat_interleave(g, 0).contiguous()
+    scores = torch.matmul(q, kk.transpose(1, 2).contiguous()) * (128 ** -0.5)
+    i = torch.arange(L, device=q.device)[:, None]
+    j = torch.arange(T, device=q.device)[None, :]
+    scores = scores.masked_fill(j > T - L + i, float("-inf"))
+    return torch.matmul(torch.softmax(scores, -1), vv)
+
+
+def test_prefill_config3_piece_matches_torch_fp32():
+    """The longest config-3 prefill piece at full per-sequence size (C = 1024, chunk 7 of an
+    8192-token prompt: 6144 older + 1024 blended recent + 1024 causal current keys, Hq 32, Hkv 8)
+    against fp32 attention over the same composed keys; B = 2 of the benchmark's 32 sequences."""
+
+    rng = np.random.default_rng(77)
+    B, Hq, Hkv, C, p0, L = 2, 32, 8, 1024, 7 * 1024, 1024
+    r, deep, prev, cur_kv, logits, scale = _history(rng, B, Hkv, C, p0, L)
+    older, ring, start = _caches(r, deep, prev, cur_kv, logits, scale, C, B, Hkv)
+    rec = r.recent[0]
+    q = _bf(rng, (B, L, Hq, 128))
+    ws = torch.empty(ops.prefill_workspace_bytes(B, Hkv, rec, p0 + L - rec, start % 32), dtype=torch.uint8, device=DEV)
+    out = ops.prefill_attention(_t(q), older=older, older_len=rec, vscale=torch.from_numpy(scale).to(DEV), local=ring,
+                                local_len=p0 + L - rec, local_start=start, causal=True, workspace=ws)
+    full_k, full_v = A.compose_history_bf16(deep[0], deep[1], prev[0], prev[1], cur_kv[0], cur_kv[1], logits, scale, C)
+    for b in range(B):
+        want = _torch_fp32_attention(torch.from_numpy(q[b].transpose(1, 0, 2).copy()).to(DEV),
+                                     torch.from_numpy(np.ascontiguousarray(full_k[b], np.float32)).to(DEV),
+                                     torch.from_numpy(np.ascontiguousarray(full_v[b], np.float32)).to(DEV), L)
+        want = want.transpose(0, 1).bfloat16().float().cpu().numpy()
+        _close(out[b], want, f"config-3 piece 7, sequence {b}")
+
+
+def test_prefill_workspace_contract():
+    """The workspace query is exact for host-constant lengths and a short workspace is rejected."""
+
+    B, Hq, Hkv = 2, 8, 2
+    older = ops.TiledKV.zeros(B, Hkv, 256, DEV)
+    ring = ops.TiledKV.zeros(B, Hkv, 128, DEV)
+    q = torch.zeros((B, 40, Hq, 128), dtype=torch.bfloat16, device=DEV)
+    kw = dict(older=older, older_len=100, local=ring, local_len=40, local_start=70)
+    need = ops.prefill_workspace_bytes(B, Hkv, 100, 40, 70 % 32)
+    assert need == B * Hkv * (4 + 2) * 8192
+    ops.prefill_attention(q, workspace=torch.empty(need, dtype=torch.uint8, device=DEV), **kw)
+    with pytest.raises(ValueError, match="workspace"):
+        ops.prefill_attention(q, workspace=torch.empty(need - 8192, dtype=torch.uint8, device=DEV), **kw)
+
+
 # ------------------------------------------------------------------ epilogue
 def _ulp_stats(actual: np.ndarray, expected: np.ndarray):
     diff = actual.view(np.uint32).astype(np.int64) - expected.view(np.uint32).astype(np.int64)
