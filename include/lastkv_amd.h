@@ -279,6 +279,53 @@ int32_t lkv_blend_chunk(int32_t layers, int32_t batch, int32_t kv_heads, int32_t
                         const float *alpha, const float *one_minus_alpha, const float *vscale,
                         lkv_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Exact merge of two attention states over disjoint key sets.
+ *
+ * Replaces the serving path's merge of the older-source pass with the local pass:
+ *   - vllm/src/lastkv/vllm/backends/rmarin_flashinfer/flashinfer_executor.py:185-231
+ *     (merge_attention_states -> flashinfer.cascade.merge_state, LSE [T, H]);
+ *   - fastpath.py:709-719 (two-pass FA3: source_out *= s_l, then vLLM merge_attn_states with
+ *     LSE [H, T]; rows without older history get a source LSE of -inf);
+ *   - batching.py:1835-1861 (source_out * source_out_scale, merge, index_copy into the output).
+ * For token t and head h (strides in elements, so either LSE layout works):
+ *   a = prefix_out[t, h, :], or bf16(prefix_out[t, h, :] * prefix_scale[h]) when prefix_scale is
+ *       set (the reference scales the bf16 source output before merging);
+ *   m = max(la, lb); wa = e^(la - m); wb = e^(lb - m)      (natural-log LSEs; +inf reads as -inf)
+ *   out[t, h, :] = bf16((a * wa + suffix_out[t, h, :] * wb) / (wa + wb))
+ *   out_lse[t, h] = m + ln(wa + wb)                          (optional)
+ * Both LSEs -inf (no keys on either side): out = 0 and out_lse = -inf.  Outputs are bf16 with
+ * 16-byte-aligned rows; head_dim is a multiple of 8.  out may alias suffix_out (each element is
+ * read before it is written by the same thread).
+ * ------------------------------------------------------------------------------------- */
+typedef struct lkv_merge_args {
+  int32_t struct_size; /* sizeof(lkv_merge_args) */
+  int32_t tokens;
+  int32_t num_heads;
+  int32_t head_dim;
+  const void *prefix_out; /* bf16 */
+  int64_t prefix_out_stride_t;
+  int64_t prefix_out_stride_h;
+  const float *prefix_lse;
+  int64_t prefix_lse_stride_t;
+  int64_t prefix_lse_stride_h;
+  const void *suffix_out; /* bf16 */
+  int64_t suffix_out_stride_t;
+  int64_t suffix_out_stride_h;
+  const float *suffix_lse;
+  int64_t suffix_lse_stride_t;
+  int64_t suffix_lse_stride_h;
+  const float *prefix_scale; /* optional fp32 [H] (bf16 values) */
+  void *out;                 /* bf16 */
+  int64_t out_stride_t;
+  int64_t out_stride_h;
+  float *out_lse; /* optional */
+  int64_t out_lse_stride_t;
+  int64_t out_lse_stride_h;
+} lkv_merge_args;
+
+int32_t lkv_merge_states(const lkv_merge_args *args, lkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

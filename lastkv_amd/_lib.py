@@ -113,6 +113,36 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
+class MergeArgs(ctypes.Structure):
+    """Mirror of ``lkv_merge_args``."""
+
+    _fields_ = [
+        ("struct_size", c_i32),
+        ("tokens", c_i32),
+        ("num_heads", c_i32),
+        ("head_dim", c_i32),
+        ("prefix_out", c_ptr),
+        ("prefix_out_stride_t", c_i64),
+        ("prefix_out_stride_h", c_i64),
+        ("prefix_lse", c_ptr),
+        ("prefix_lse_stride_t", c_i64),
+        ("prefix_lse_stride_h", c_i64),
+        ("suffix_out", c_ptr),
+        ("suffix_out_stride_t", c_i64),
+        ("suffix_out_stride_h", c_i64),
+        ("suffix_lse", c_ptr),
+        ("suffix_lse_stride_t", c_i64),
+        ("suffix_lse_stride_h", c_i64),
+        ("prefix_scale", c_ptr),
+        ("out", c_ptr),
+        ("out_stride_t", c_i64),
+        ("out_stride_h", c_i64),
+        ("out_lse", c_ptr),
+        ("out_lse_stride_t", c_i64),
+        ("out_lse_stride_h", c_i64),
+    ]
+
+
 class QkvArgs(ctypes.Structure):
     """Mirror of ``lkv_qkv_args``."""
 
@@ -177,6 +207,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lkv_decode_attn": (c_i32, [ctypes.POINTER(DecodeArgs), c_ptr]),
     "lkv_prefill_workspace_bytes": (c_i64, [ctypes.POINTER(PrefillArgs)]),
     "lkv_prefill_attn": (c_i32, [ctypes.POINTER(PrefillArgs), c_ptr]),
+    "lkv_merge_states": (c_i32, [ctypes.POINTER(MergeArgs), c_ptr]),
     "lkv_qkv_epilogue": (c_i32, [ctypes.POINTER(QkvArgs), c_ptr]),
     "lkv_blend_chunk": (
         c_i32,

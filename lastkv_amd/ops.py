@@ -354,6 +354,70 @@ def prefill_workspace_bytes(batch: int, kv_heads: int, older_tokens: int, local_
     return batch * kv_heads * blocks * 8192
 
 
+def merge_states(
+    prefix_out: torch.Tensor,
+    prefix_lse: torch.Tensor,
+    suffix_out: torch.Tensor,
+    suffix_lse: torch.Tensor,
+    *,
+    prefix_scale: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    out_lse: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Exact merge of two attention states over disjoint key sets (``lkv_merge_states``).
+
+    Outputs are bf16 ``[T, H, D]``; LSEs are fp32 natural-log tensors indexed ``[t, h]`` through
+    their strides (pass ``lse.t()`` for an ``[H, T]`` tensor).  ``prefix_scale`` (fp32 ``[H]``)
+    multiplies the prefix output in bf16 before the merge.  Returns ``(out, out_lse)``."""
+
+    for name, t in (("prefix_out", prefix_out), ("suffix_out", suffix_out)):
+        _require_bf16_cuda(name, t)
+        _require(t.dim() == 3 and t.stride(-1) == 1, f"{name} must be [T, H, D] with contiguous rows")
+    _require(prefix_out.shape == suffix_out.shape, "prefix and suffix outputs differ in shape")
+    T, H, D = prefix_out.shape
+    device = prefix_out.device
+    for name, t in (("prefix_lse", prefix_lse), ("suffix_lse", suffix_lse), ("out_lse", out_lse)):
+        if t is not None:
+            _require(t.dtype == torch.float32 and t.device == device and tuple(t.shape) == (T, H),
+                     f"{name} must be an fp32 [T, H] view on {device}")
+    if prefix_scale is not None:
+        _require(prefix_scale.dtype == torch.float32 and prefix_scale.numel() == H and prefix_scale.is_contiguous()
+                 and prefix_scale.device == device, "prefix_scale must be a contiguous fp32 [H] tensor")
+    if out is None:
+        out = torch.empty_like(suffix_out)
+    _require_bf16_cuda("out", out)
+    _require(tuple(out.shape) == (T, H, D) and out.stride(-1) == 1, "out must be [T, H, D] with contiguous rows")
+    a = _lib.MergeArgs()
+    a.struct_size = ctypes.sizeof(_lib.MergeArgs)
+    a.tokens, a.num_heads, a.head_dim = T, H, D
+    a.prefix_out, a.prefix_out_stride_t, a.prefix_out_stride_h = prefix_out.data_ptr(), prefix_out.stride(0), prefix_out.stride(1)
+    a.prefix_lse, a.prefix_lse_stride_t, a.prefix_lse_stride_h = prefix_lse.data_ptr(), prefix_lse.stride(0), prefix_lse.stride(1)
+    a.suffix_out, a.suffix_out_stride_t, a.suffix_out_stride_h = suffix_out.data_ptr(), suffix_out.stride(0), suffix_out.stride(1)
+    a.suffix_lse, a.suffix_lse_stride_t, a.suffix_lse_stride_h = suffix_lse.data_ptr(), suffix_lse.stride(0), suffix_lse.stride(1)
+    a.prefix_scale = _ptr(prefix_scale)
+    a.out, a.out_stride_t, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    if out_lse is not None:
+        a.out_lse, a.out_lse_stride_t, a.out_lse_stride_h = out_lse.data_ptr(), out_lse.stride(0), out_lse.stride(1)
+    _lib.check(_lib.load().lkv_merge_states(ctypes.byref(a), _stream(device)), "lkv_merge_states")
+    return out, out_lse
+
+
+def merge_attn_states(output, prefix_output, prefix_lse, suffix_output, suffix_lse, output_lse=None) -> None:
+    """vLLM's ``merge_attn_states`` argument order (fastpath.py:709-719): LSEs are ``[H, T]``."""
+
+    merge_states(prefix_output, prefix_lse.t(), suffix_output, suffix_lse.t(), out=output,
+                 out_lse=None if output_lse is None else output_lse.t())
+
+
+def merge_state(v_a, s_a, v_b, s_b):
+    """FlashInfer's ``cascade.merge_state`` argument order (flashinfer_executor.py:185-231): LSEs
+    ``[T, H]`` (natural log here); returns ``(v, s)``."""
+
+    s = torch.empty_like(s_a)
+    v, _ = merge_states(v_a, s_a, v_b, s_b, out_lse=s)
+    return v, s
+
+
 def _rows(name: str, t: torch.Tensor, heads: int) -> tuple[int, int, int]:
     """(ptr, stride_b, stride_t) of a [B, L, heads * 128] (or [B, L, heads, 128]) bf16 tensor."""
 
