@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 2
+#define LKV_ABI_VERSION 3
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -122,6 +122,21 @@ typedef struct lkv_decode_args {
   int32_t local_num_slots;          /* slots addressable through local_slot */
   void *workspace;
   int64_t workspace_bytes;
+  /* Optional paging (NULL tables: contiguous segments as above).  With older_block_table, block j
+   * (tokens 32j..32j+31) of sequence b's older segment is page older_block_table[b *
+   * older_table_stride + j] of the pool at older_k / older_v: page p of kv head h starts at element
+   * p * older_page_stride + h * older_head_stride; older_slot and older_seq_stride are unused and
+   * older_capacity_tokens <= 32 * older_table_stride.  With local_block_table, ring block rb of
+   * sequence b is page local_block_table[b * local_table_stride + rb] (rb < local_ring_blocks <=
+   * local_table_stride).  Page ids are clamped into [0, num_pages). */
+  const int32_t *older_block_table;
+  int64_t older_table_stride;
+  int64_t older_page_stride;
+  int32_t older_num_pages;
+  const int32_t *local_block_table;
+  int64_t local_table_stride;
+  int64_t local_page_stride;
+  int32_t local_num_pages;
 } lkv_decode_args;
 
 int64_t lkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_splits);
@@ -186,6 +201,15 @@ typedef struct lkv_prefill_args {
   int32_t local_num_slots;
   void *workspace; /* >= lkv_prefill_workspace_bytes(args) bytes, 16-byte aligned */
   int64_t workspace_bytes;
+  /* Optional paging, with the same meaning as in lkv_decode_args. */
+  const int32_t *older_block_table;
+  int64_t older_table_stride;
+  int64_t older_page_stride;
+  int32_t older_num_pages;
+  const int32_t *local_block_table;
+  int64_t local_table_stride;
+  int64_t local_page_stride;
+  int32_t local_num_pages;
 } lkv_prefill_args;
 
 /* Workspace bytes lkv_prefill_attn needs for these args: the fp16 V of every key block of every

@@ -11,7 +11,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class LastKVNativeError(RuntimeError):
@@ -64,6 +64,14 @@ class DecodeArgs(ctypes.Structure):
         ("local_num_slots", c_i32),
         ("workspace", c_ptr),
         ("workspace_bytes", c_i64),
+        ("older_block_table", c_ptr),
+        ("older_table_stride", c_i64),
+        ("older_page_stride", c_i64),
+        ("older_num_pages", c_i32),
+        ("local_block_table", c_ptr),
+        ("local_table_stride", c_i64),
+        ("local_page_stride", c_i64),
+        ("local_num_pages", c_i32),
     ]
 
 
@@ -110,6 +118,14 @@ class PrefillArgs(ctypes.Structure):
         ("local_num_slots", c_i32),
         ("workspace", c_ptr),
         ("workspace_bytes", c_i64),
+        ("older_block_table", c_ptr),
+        ("older_table_stride", c_i64),
+        ("older_page_stride", c_i64),
+        ("older_num_pages", c_i32),
+        ("local_block_table", c_ptr),
+        ("local_table_stride", c_i64),
+        ("local_page_stride", c_i64),
+        ("local_num_pages", c_i32),
     ]
 
 

@@ -28,24 +28,8 @@ struct DecodeParams {
   uint16_t* out;
   int64_t out_sb;
   float* lse;
-  const uint16_t* ok;
-  const uint16_t* ov;
-  int64_t o_ss, o_hs;
-  const int32_t* o_len;
-  int32_t o_len_c, o_cap;
-  const int32_t* o_slot;
-  int32_t o_nslots;
+  SegParams seg;
   const float* vscale;
-  const uint16_t* lk;
-  const uint16_t* lv;
-  int64_t l_ss, l_hs;
-  int32_t ring_blocks;
-  const int32_t* l_len;
-  int32_t l_len_c;
-  const int32_t* l_start;
-  int32_t l_start_c;
-  const int32_t* l_slot;
-  int32_t l_nslots;
   float* ws_o;
   float* ws_ml;
   int32_t hq, group, splits;
@@ -158,27 +142,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = p.group;
 
-  SeqView sv;
-  {
-    const int oslot = p.o_slot ? p.o_slot[b] : b;
-    const int lslot = p.l_slot ? p.l_slot[b] : b;
-    int n0 = p.o_len ? p.o_len[b] : p.o_len_c;
-    int n1 = p.lk ? (p.l_len ? p.l_len[b] : p.l_len_c) : 0;
-    n0 = (oslot < 0 || oslot >= p.o_nslots || p.ok == nullptr) ? 0 : min(max(n0, 0), p.o_cap);
-    n1 = (lslot < 0 || lslot >= p.l_nslots) ? 0 : min(max(n1, 0), p.ring_blocks * kBlockTokens);
-    int ls = p.l_start ? p.l_start[b] : p.l_start_c;
-    ls = (ls < 0 || ls >= p.ring_blocks * kBlockTokens) ? 0 : ls;
-    sv.ok = p.ok ? p.ok + static_cast<int64_t>(oslot) * p.o_ss + kvh * p.o_hs : nullptr;
-    sv.ov = p.ov ? p.ov + static_cast<int64_t>(oslot) * p.o_ss + kvh * p.o_hs : nullptr;
-    sv.lk = p.lk ? p.lk + static_cast<int64_t>(lslot) * p.l_ss + kvh * p.l_hs : nullptr;
-    sv.lv = p.lv ? p.lv + static_cast<int64_t>(lslot) * p.l_ss + kvh * p.l_hs : nullptr;
-    sv.n0 = n0;
-    sv.n1 = n1;
-    sv.nb0 = (n0 + kBlockTokens - 1) / kBlockTokens;
-    sv.lblk0 = ls >> 5;
-    sv.lead = ls & (kBlockTokens - 1);
-    sv.ring_blocks = p.ring_blocks;
-  }
+  const SeqView sv = make_seq_view(p.seg, b, kvh);
   const int nbt = sv.nb0 + (sv.n1 > 0 ? (sv.lead + sv.n1 + kBlockTokens - 1) / kBlockTokens : 0);
   const int bps = (nbt + p.splits - 1) / p.splits;
   const int blk_begin = split * bps;
@@ -305,24 +269,10 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->older_vscale_mode == 1, "older_vscale_mode must be 0 or 1");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->vscale != nullptr, "older_vscale_mode 1 needs vscale");
   LKV_REQUIRE(a->q != nullptr && a->out != nullptr, "null q/out");
-  LKV_REQUIRE((a->older_k == nullptr) == (a->older_v == nullptr), "older_k and older_v must both be set");
-  LKV_REQUIRE((a->local_k == nullptr) == (a->local_v == nullptr), "local_k and local_v must both be set");
-  LKV_REQUIRE(a->older_k == nullptr || a->older_capacity_tokens % kBlockTokens == 0,
-              "older capacity must be a multiple of 32 tokens");
-  LKV_REQUIRE(a->older_k == nullptr || a->older_num_slots > 0, "older_num_slots must be positive");
-  LKV_REQUIRE(a->older_k == nullptr || a->older_slot != nullptr || a->older_num_slots >= a->batch,
-              "older_num_slots < batch with identity slots");
-  LKV_REQUIRE(a->local_k == nullptr || a->local_ring_blocks > 0, "local ring needs at least one block");
-  LKV_REQUIRE(a->local_k == nullptr || a->local_num_slots > 0, "local_num_slots must be positive");
-  LKV_REQUIRE(a->local_k == nullptr || a->local_slot != nullptr || a->local_num_slots >= a->batch,
-              "local_num_slots < batch with identity slots");
   LKV_REQUIRE((a->q_stride_b % 8) == 0 && (reinterpret_cast<uintptr_t>(a->q) & 15) == 0,
               "q rows must be 16-byte aligned");
-  const uintptr_t align_or = reinterpret_cast<uintptr_t>(a->older_k) | reinterpret_cast<uintptr_t>(a->older_v) |
-                             reinterpret_cast<uintptr_t>(a->local_k) | reinterpret_cast<uintptr_t>(a->local_v);
-  LKV_REQUIRE((align_or & 15) == 0, "caches must be 16-byte aligned");
-  LKV_REQUIRE((a->older_seq_stride | a->older_head_stride | a->local_seq_stride | a->local_head_stride) % 8 == 0,
-              "cache strides must be multiples of 8 elements");
+  DecodeParams p;
+  if (const int32_t st = fill_segments(a, p.seg)) return st;
   if (a->batch == 0) return LKV_OK;
   const int64_t need = lkv_decode_workspace_bytes(a->batch, a->num_q_heads, a->num_splits);
   if (need > 0) {
@@ -332,33 +282,12 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
     if ((reinterpret_cast<uintptr_t>(a->workspace) & 15) != 0)
       return fail(LKV_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   }
-  DecodeParams p;
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_stride_b;
   p.out = static_cast<uint16_t*>(a->out);
   p.out_sb = a->out_stride_b;
   p.lse = a->lse;
-  p.ok = static_cast<const uint16_t*>(a->older_k);
-  p.ov = static_cast<const uint16_t*>(a->older_v);
-  p.o_ss = a->older_seq_stride;
-  p.o_hs = a->older_head_stride;
-  p.o_len = a->older_len;
-  p.o_len_c = a->older_len_const;
-  p.o_cap = a->older_capacity_tokens;
-  p.o_slot = a->older_slot;
-  p.o_nslots = a->older_num_slots;
   p.vscale = a->vscale;
-  p.lk = static_cast<const uint16_t*>(a->local_k);
-  p.lv = static_cast<const uint16_t*>(a->local_v);
-  p.l_ss = a->local_seq_stride;
-  p.l_hs = a->local_head_stride;
-  p.ring_blocks = a->local_k ? a->local_ring_blocks : 1;
-  p.l_len = a->local_len;
-  p.l_len_c = a->local_len_const;
-  p.l_start = a->local_start;
-  p.l_start_c = a->local_start_const;
-  p.l_slot = a->local_slot;
-  p.l_nslots = a->local_num_slots;
   p.ws_o = static_cast<float*>(a->workspace);
   p.ws_ml = need > 0 ? p.ws_o + static_cast<int64_t>(a->batch) * a->num_q_heads * a->num_splits * kHeadDim : nullptr;
   p.hq = a->num_q_heads;

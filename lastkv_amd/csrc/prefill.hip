@@ -36,24 +36,8 @@ struct PrefillParams {
   uint16_t* out;
   int64_t out_sb, out_st;
   float* lse;
-  const uint16_t* ok;
-  const uint16_t* ov;
-  int64_t o_ss, o_hs;
-  const int32_t* o_len;
-  int32_t o_len_c, o_cap;
-  const int32_t* o_slot;
-  int32_t o_nslots;
+  SegParams seg;
   const float* vscale;
-  const uint16_t* lk;
-  const uint16_t* lv;
-  int64_t l_ss, l_hs;
-  int32_t ring_blocks;
-  const int32_t* l_len;
-  int32_t l_len_c;
-  const int32_t* l_start;
-  int32_t l_start_c;
-  const int32_t* l_slot;
-  int32_t l_nslots;
   int32_t L, hq, hkv, group, causal, tiles;
   float scale_log2;
   int32_t vscale_mode;
@@ -90,29 +74,6 @@ __device__ inline uint32_t pack_f16_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-__device__ inline SeqView make_view(const PrefillParams& p, int b, int kvh) {
-  SeqView sv;
-  const int oslot = p.o_slot ? p.o_slot[b] : b;
-  const int lslot = p.l_slot ? p.l_slot[b] : b;
-  int n0 = p.o_len ? p.o_len[b] : p.o_len_c;
-  int n1 = p.lk ? (p.l_len ? p.l_len[b] : p.l_len_c) : 0;
-  n0 = (oslot < 0 || oslot >= p.o_nslots || p.ok == nullptr) ? 0 : min(max(n0, 0), p.o_cap);
-  n1 = (lslot < 0 || lslot >= p.l_nslots) ? 0 : min(max(n1, 0), p.ring_blocks * kBlockTokens);
-  int ls = p.l_start ? p.l_start[b] : p.l_start_c;
-  ls = (ls < 0 || ls >= p.ring_blocks * kBlockTokens) ? 0 : ls;
-  sv.ok = p.ok ? p.ok + static_cast<int64_t>(oslot) * p.o_ss + kvh * p.o_hs : nullptr;
-  sv.ov = p.ov ? p.ov + static_cast<int64_t>(oslot) * p.o_ss + kvh * p.o_hs : nullptr;
-  sv.lk = p.lk ? p.lk + static_cast<int64_t>(lslot) * p.l_ss + kvh * p.l_hs : nullptr;
-  sv.lv = p.lv ? p.lv + static_cast<int64_t>(lslot) * p.l_ss + kvh * p.l_hs : nullptr;
-  sv.n0 = n0;
-  sv.n1 = n1;
-  sv.nb0 = (n0 + kBlockTokens - 1) / kBlockTokens;
-  sv.lblk0 = ls >> 5;
-  sv.lead = ls & (kBlockTokens - 1);
-  sv.ring_blocks = p.ring_blocks;
-  return sv;
-}
-
 // Local-segment tokens visible to a query token (causal: bottom-right aligned).
 __device__ inline int visible_local(const PrefillParams& p, const SeqView& sv, int token) {
   const int v = p.causal ? sv.n1 - p.L + token + 1 : sv.n1;
@@ -128,12 +89,10 @@ struct Stage {
   uint4 r[16 / NW];
 };
 
-// Wave-uniform base pointers and byte ranges of one sequence / kv head: K and V of the older
-// segment and of the ring.  Each load builds its buffer resource from the selected base (scalar
-// instructions only).
+// Wave-uniform base of the fp16 V workspace of one (sequence, kv head) and its byte range.
 struct SegBase {
-  const uint16_t *ok, *lk, *v16;
-  int32_t o_bytes, l_bytes, v16_bytes;
+  const uint16_t* v16;
+  int32_t v16_bytes;
 };
 
 __device__ inline const uint16_t* uniform_ptr(const uint16_t* p) {
@@ -148,27 +107,26 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base, int32_t
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, base ? bytes : 0, 0x00020000);
 }
 
-// Byte offset of block blk inside its segment array, and which segment it is in.
-__device__ inline int block_byte_offset(const SeqView& sv, int blk, bool& older) {
-  older = blk < sv.nb0;
-  int rb = sv.lblk0 + (blk - sv.nb0);
-  rb = rb >= sv.ring_blocks ? rb - sv.ring_blocks : rb;
-  return (older ? blk : rb) * (kBlockElems * 2);
+// Wave w of NW loads fragments w, w + NW, ... of block blk: K (bf16) from the block's cache or
+// pool page (a buffer resource over that one 8 KiB block, built with scalar instructions) and V
+// (fp16) from the workspace, which holds the blocks in order.
+// Wave-uniform address of block blk's K (cache block or pool page).
+template <bool kPaged>
+__device__ inline const uint16_t* k_block(const SeqView& sv, int blk) {
+  return uniform_ptr((blk < sv.nb0 ? sv.ok : sv.lk) + block_offset<kPaged>(sv, blk));
 }
 
+// kblk = k_block<kPaged>(sv, blk), computed by the caller outside the scheduled region (the page-table
+// lookup branches).
 template <int NW>
-__device__ inline void stage_load(Stage<NW>& st, const SegBase sb, const SeqView& sv, int blk, int wave,
+__device__ inline void stage_load(Stage<NW>& st, const SegBase sb, const uint16_t* kblk, int blk, int wave,
                                   int lane_off) {
-  bool older;
-  const int boff = __builtin_amdgcn_readfirstlane(block_byte_offset(sv, blk, older));
-  const int32_t kbytes = older ? sb.o_bytes : sb.l_bytes;
-  const uint16_t* kbase = uniform_ptr(older ? sb.ok : sb.lk);
-  const int voff = blk * (kBlockElems * 2);  // the fp16 V workspace is in block order
+  const int voff = blk * (kBlockElems * 2);
 #pragma unroll
   for (int j = 0; j < 16 / NW; ++j) {
     const int f = wave + j * NW;  // wave < NW, so f < 8 exactly when j < 8 / NW
-    const __amdgpu_buffer_rsrc_t r = j < 8 / NW ? make_rsrc(kbase, kbytes) : make_rsrc(sb.v16, sb.v16_bytes);
-    const int off = (j < 8 / NW ? boff : voff) + (f & 7) * 1024;
+    const __amdgpu_buffer_rsrc_t r = j < 8 / NW ? make_rsrc(kblk, kBlockElems * 2) : make_rsrc(sb.v16, sb.v16_bytes);
+    const int off = (j < 8 / NW ? 0 : voff) + (f & 7) * 1024;
     st.r[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, off, 0));
   }
 }
@@ -243,13 +201,13 @@ struct IC {
 // local], with the older segment as bf16(V * s) (the reference's rounded _scale()).  The
 // attention kernel's query tiles then stage V as plain copies instead of each converting it.
 // One workgroup per (block, kv head, sequence); 256 threads x 16 values.
+template <bool kPaged>
 __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
   const int blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const SeqView sv = make_view(p, b, kvh);
+  const SeqView sv = make_seq_view(p.seg, b, kvh);
   if (blk >= sv.nb0 + local_blocks(sv, sv.n1)) return;
-  bool older;
-  const int boff = block_byte_offset(sv, blk, older);
-  const uint16_t* src = (older ? sv.ov : sv.lv) + boff / 2;
+  const bool older = blk < sv.nb0;
+  const uint16_t* src = (older ? sv.ov : sv.lv) + block_offset<kPaged>(sv, blk);
   uint16_t* dst = p.v16 + ((static_cast<int64_t>(b) * p.hkv + kvh) * p.v16_blocks + blk) * kBlockElems;
   const float s = (p.vscale_mode && older) ? p.vscale[kvh] : 1.f;
 #pragma unroll
@@ -267,7 +225,7 @@ __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
 // buffer i % 4, block i + 1 in buffer (i + 1) % 4): probabilities of block i from the scores
 // computed in step i - 1, QK^T of block i + 1, P V of block i, store block i + 2 into buffer
 // (i + 2) % 4, load block i + 4, one barrier.
-template <int NW, int CG, int WPE>
+template <int NW, int CG, int WPE, bool kPaged>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_kernel(
     const PrefillParams p) {
   constexpr int kRing = 4;
@@ -288,7 +246,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   const int wg_row0 = tile * kRowsPerWg;
   const int row0 = wg_row0 + wave * kRowsPerWave;
 
-  SeqView sv = make_view(p, b, kvh);
+  SeqView sv = make_seq_view(p.seg, b, kvh);
   // these are wave-uniform; keeping them in scalar registers keeps every block offset scalar
   sv.n0 = __builtin_amdgcn_readfirstlane(sv.n0);
   sv.n1 = __builtin_amdgcn_readfirstlane(sv.n1);
@@ -331,11 +289,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
 
   if (nbt > 0) {
     SegBase rsrc;
-    rsrc.ok = uniform_ptr(sv.ok);
-    rsrc.lk = uniform_ptr(sv.lk);
     rsrc.v16 = uniform_ptr(p.v16 + (static_cast<int64_t>(b) * p.hkv + kvh) * p.v16_blocks * kBlockElems);
-    rsrc.o_bytes = p.o_cap * (kHeadDim * 2);
-    rsrc.l_bytes = p.ring_blocks * (kBlockElems * 2);
     rsrc.v16_bytes = p.v16_blocks * (kBlockElems * 2);
     const int lane_off = n16 * 64 + g4 * 16;
     // Loads are unconditional (indices past the end re-read the last block, an L2 hit) so that
@@ -343,12 +297,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
     const int last = nbt - 1;
 
     Stage<NW> sa, sb;
-    stage_load<NW>(sa, rsrc, sv, 0, wave, lane_off);
-    stage_load<NW>(sb, rsrc, sv, min(1, last), wave, lane_off);
+    stage_load<NW>(sa, rsrc, k_block<kPaged>(sv, 0), 0, wave, lane_off);
+    stage_load<NW>(sb, rsrc, k_block<kPaged>(sv, min(1, last)), min(1, last), wave, lane_off);
     stage_store<NW>(sa, lds, wave, lane);
-    stage_load<NW>(sa, rsrc, sv, min(2, last), wave, lane_off);
+    stage_load<NW>(sa, rsrc, k_block<kPaged>(sv, min(2, last)), min(2, last), wave, lane_off);
     stage_store<NW>(sb, lds + kBuf, wave, lane);
-    stage_load<NW>(sb, rsrc, sv, min(3, last), wave, lane_off);
+    stage_load<NW>(sb, rsrc, k_block<kPaged>(sv, min(3, last)), min(3, last), wave, lane_off);
     __syncthreads();
 
     // S^T of block 0: sc[cg][u] holds tokens 8 * g4 + 4u .. + 3 of this lane's column n16 of
@@ -381,10 +335,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
       const uint4* nxt = lds + ((R + 1) % kRing) * kBuf;
       uint4* wr = lds + ((R + 2) % kRing) * kBuf;
       Stage<NW>& st = (R % 2 == 0) ? sa : sb;
+      const int ld_blk = min(blk + 4, last);
+      const uint16_t* ld_k = k_block<kPaged>(sv, ld_blk);
       uint4 kf[8];
 #pragma unroll
       for (int t = 0; t < 8; ++t) kf[t] = nxt[t * 64 + lane];
-      const BlockRef r = block_ref(sv, blk);
+      const BlockRef r = block_range(sv, blk);
       float s[CG][8];
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg)
@@ -448,7 +404,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) rs[cg].l += lb[cg];
       stage_store<NW>(st, wr, wave, lane);
-      stage_load<NW>(st, rsrc, sv, min(blk + 4, last), wave, lane_off);
+      stage_load<NW>(st, rsrc, ld_k, ld_blk, wave, lane_off);
 #pragma unroll
       for (int i = 0; i < 8 * CG; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (P V of block i)
@@ -531,31 +487,12 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->older_vscale_mode == 1, "older_vscale_mode must be 0 or 1");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->vscale != nullptr, "older_vscale_mode 1 needs vscale");
   LKV_REQUIRE(a->q != nullptr && a->out != nullptr, "null q/out");
-  LKV_REQUIRE((a->older_k == nullptr) == (a->older_v == nullptr), "older_k and older_v must both be set");
-  LKV_REQUIRE((a->local_k == nullptr) == (a->local_v == nullptr), "local_k and local_v must both be set");
-  LKV_REQUIRE(a->older_k == nullptr || a->older_capacity_tokens % kBlockTokens == 0,
-              "older capacity must be a multiple of 32 tokens");
-  LKV_REQUIRE(a->older_k == nullptr || a->older_num_slots > 0, "older_num_slots must be positive");
-  LKV_REQUIRE(a->older_k == nullptr || a->older_slot != nullptr || a->older_num_slots >= a->batch,
-              "older_num_slots < batch with identity slots");
-  LKV_REQUIRE(a->local_k == nullptr || a->local_ring_blocks > 0, "local ring needs at least one block");
-  // each (slot, kv head) segment is addressed by a buffer resource with a 31-bit byte range
-  LKV_REQUIRE(a->older_k == nullptr || static_cast<int64_t>(a->older_capacity_tokens) * 256 < (1LL << 31),
-              "older capacity must be below 8M tokens");
-  LKV_REQUIRE(a->local_k == nullptr || static_cast<int64_t>(a->local_ring_blocks) * 8192 < (1LL << 31),
-              "local ring must be below 8M tokens");
-  LKV_REQUIRE(a->local_k == nullptr || a->local_num_slots > 0, "local_num_slots must be positive");
-  LKV_REQUIRE(a->local_k == nullptr || a->local_slot != nullptr || a->local_num_slots >= a->batch,
-              "local_num_slots < batch with identity slots");
   LKV_REQUIRE((a->q_stride_b % 8) == 0 && (a->q_stride_t % 8) == 0 && (reinterpret_cast<uintptr_t>(a->q) & 15) == 0,
               "q rows must be 16-byte aligned");
   LKV_REQUIRE((a->out_stride_b % 4) == 0 && (a->out_stride_t % 4) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 7) == 0,
               "out rows must be 8-byte aligned");
-  const uintptr_t align_or = reinterpret_cast<uintptr_t>(a->older_k) | reinterpret_cast<uintptr_t>(a->older_v) |
-                             reinterpret_cast<uintptr_t>(a->local_k) | reinterpret_cast<uintptr_t>(a->local_v);
-  LKV_REQUIRE((align_or & 15) == 0, "caches must be 16-byte aligned");
-  LKV_REQUIRE((a->older_seq_stride | a->older_head_stride | a->local_seq_stride | a->local_head_stride) % 8 == 0,
-              "cache strides must be multiples of 8 elements");
+  PrefillParams p;
+  if (const int32_t st = fill_segments(a, p.seg)) return st;
   LKV_REQUIRE(a->batch <= 65535 && a->num_kv_heads <= 65535, "batch and num_kv_heads must be <= 65535");
   if (a->batch == 0 || a->tokens == 0) return LKV_OK;
   const int64_t vblocks = v16_blocks(a);
@@ -565,7 +502,6 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
               "prefill needs a workspace of %lld bytes (lkv_prefill_workspace_bytes), got %lld",
               static_cast<long long>(need), static_cast<long long>(a->workspace_bytes));
   LKV_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 15) == 0, "workspace must be 16-byte aligned");
-  PrefillParams p;
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_stride_b;
   p.q_st = a->q_stride_t;
@@ -573,27 +509,7 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.out_sb = a->out_stride_b;
   p.out_st = a->out_stride_t;
   p.lse = a->lse;
-  p.ok = static_cast<const uint16_t*>(a->older_k);
-  p.ov = static_cast<const uint16_t*>(a->older_v);
-  p.o_ss = a->older_seq_stride;
-  p.o_hs = a->older_head_stride;
-  p.o_len = a->older_len;
-  p.o_len_c = a->older_len_const;
-  p.o_cap = a->older_capacity_tokens;
-  p.o_slot = a->older_slot;
-  p.o_nslots = a->older_num_slots;
   p.vscale = a->vscale;
-  p.lk = static_cast<const uint16_t*>(a->local_k);
-  p.lv = static_cast<const uint16_t*>(a->local_v);
-  p.l_ss = a->local_seq_stride;
-  p.l_hs = a->local_head_stride;
-  p.ring_blocks = a->local_k ? a->local_ring_blocks : 1;
-  p.l_len = a->local_len;
-  p.l_len_c = a->local_len_const;
-  p.l_start = a->local_start;
-  p.l_start_c = a->local_start_const;
-  p.l_slot = a->local_slot;
-  p.l_nslots = a->local_num_slots;
   p.L = a->tokens;
   p.hq = a->num_q_heads;
   p.group = group;
@@ -612,16 +528,23 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.tiles = static_cast<int32_t>(tiles);
   p.hkv = a->num_kv_heads;
   hipStream_t s = as_stream(stream);
-  if (vblocks == 0) {
-    // no keys at all: every row's output is zero (the main kernel skips its loop)
-  } else {
-    v16_stage_kernel<<<dim3(static_cast<unsigned>(vblocks), a->num_kv_heads, a->batch), 256, 0, s>>>(p);
+  const bool paged = a->older_block_table != nullptr || a->local_block_table != nullptr;
+  if (vblocks > 0) {  // (no keys at all: every row's output is zero; the main kernel skips its loop)
+    const dim3 vgrid(static_cast<unsigned>(vblocks), a->num_kv_heads, a->batch);
+    if (paged)
+      v16_stage_kernel<true><<<vgrid, 256, 0, s>>>(p);
+    else
+      v16_stage_kernel<false><<<vgrid, 256, 0, s>>>(p);
     if (const int32_t e = check_launch("lkv_prefill_attn (V pre-pass)")) return e;
   }
   const dim3 grid(static_cast<unsigned>(wgs));
-  if (wide)
-    prefill_kernel<8, 2, 2><<<grid, 8 * 64, 0, s>>>(p);
+  if (wide && paged)
+    prefill_kernel<8, 2, 2, true><<<grid, 8 * 64, 0, s>>>(p);
+  else if (wide)
+    prefill_kernel<8, 2, 2, false><<<grid, 8 * 64, 0, s>>>(p);
+  else if (paged)
+    prefill_kernel<2, 2, 1, true><<<grid, 2 * 64, 0, s>>>(p);
   else
-    prefill_kernel<2, 2, 1><<<grid, 2 * 64, 0, s>>>(p);
+    prefill_kernel<2, 2, 1, false><<<grid, 2 * 64, 0, s>>>(p);
   return check_launch("lkv_prefill_attn");
 }

@@ -93,6 +93,49 @@ class TiledKV:
         return self.k.device
 
 
+@dataclass
+class PagedKV:
+    """K and V page pools in the tiled block layout: ``[pages, heads, 4096]`` bf16 each.
+
+    A page holds 32 tokens of every kv head; which pages form a sequence's segment is given per
+    call by an int32 block table ``[B, W]`` (block j of sequence b is page ``table[b, j]``)."""
+
+    k: torch.Tensor
+    v: torch.Tensor
+
+    def __post_init__(self) -> None:
+        for name, t in (("k", self.k), ("v", self.v)):
+            _require_bf16_cuda(f"PagedKV.{name}", t)
+            _require(t.dim() == 3 and t.shape[-1] == BLOCK_ELEMS, f"PagedKV.{name} must be [pages, heads, 4096]")
+            _require(t.is_contiguous(), f"PagedKV.{name} must be contiguous")
+        _require(self.k.shape == self.v.shape, "PagedKV k and v shapes differ")
+
+    @classmethod
+    def zeros(cls, pages: int, heads: int, device: torch.device | str) -> "PagedKV":
+        shape = (pages, heads, BLOCK_ELEMS)
+        return cls(torch.zeros(shape, dtype=torch.bfloat16, device=device), torch.zeros(shape, dtype=torch.bfloat16, device=device))
+
+    @property
+    def pages(self) -> int:
+        return int(self.k.shape[0])
+
+    @property
+    def heads(self) -> int:
+        return int(self.k.shape[1])
+
+    @property
+    def page_stride(self) -> int:
+        return self.heads * BLOCK_ELEMS
+
+    @property
+    def head_stride(self) -> int:
+        return BLOCK_ELEMS
+
+    @property
+    def device(self) -> torch.device:
+        return self.k.device
+
+
 def cache_pack(src: torch.Tensor, cache: torch.Tensor, kind: int, token0: int = 0, *, capacity_tokens: int | None = None) -> None:
     """Write ``src`` ``[B, H, T, 128]`` into cache tokens ``[token0, token0 + T)`` of slots ``0..B-1``."""
 
@@ -170,9 +213,19 @@ def _len_arg(value: int | torch.Tensor | None, batch: int, name: str, device: to
     return None, int(value)
 
 
+def _table_arg(table: torch.Tensor, B: int, name: str, device: torch.device) -> None:
+    _require(table is not None, f"a paged {name} segment needs a block table")
+    _require(table.dtype == torch.int32 and table.device == device and table.dim() == 2 and table.shape[0] == B
+             and table.stride(1) == 1, f"{name}_table must be an int32 [B, W] tensor with contiguous rows on {device}")
+
+
 def _fill_segments(a, B: int, device: torch.device, older, older_len, older_slot, vscale, local, local_len,
-                   local_start, local_slot) -> int:
-    """Fill the older/local segment fields shared by DecodeArgs and PrefillArgs; returns Hkv."""
+                   local_start, local_slot, older_table=None, local_table=None, local_ring_blocks=None) -> int:
+    """Fill the older/local segment fields shared by DecodeArgs and PrefillArgs; returns Hkv.
+
+    ``older`` / ``local`` are a TiledKV (contiguous per slot) or a PagedKV with a block table
+    (``older_table`` [B, W]: older block j of sequence b is page ``older_table[b, j]``;
+    ``local_table`` [B, >= ring blocks]: ring block rb is page ``local_table[b, rb]``)."""
 
     _require(older is not None or local is not None, "at least one key segment is required")
     Hkv = (older if older is not None else local).heads
@@ -190,44 +243,67 @@ def _fill_segments(a, B: int, device: torch.device, older, older_len, older_slot
     if older is not None:
         _require(older.device == device, "older cache on another device")
         a.older_k, a.older_v = older.k.data_ptr(), older.v.data_ptr()
-        a.older_seq_stride, a.older_head_stride = older.seq_stride, older.head_stride
+        a.older_head_stride = older.head_stride
         a.older_len, a.older_len_const = _len_arg(older_len, B, "older_len", device)
-        a.older_capacity_tokens = older.capacity_tokens
-        a.older_slot = _ptr(older_slot)
-        a.older_num_slots = older.slots
-        if older_slot is None:
-            _require(older.slots >= B, "older cache has fewer slots than sequences")
+        if isinstance(older, PagedKV):
+            _table_arg(older_table, B, "older", device)
+            _require(older_slot is None, "older_slot does not apply to a paged segment")
+            a.older_block_table, a.older_table_stride = older_table.data_ptr(), older_table.stride(0)
+            a.older_page_stride, a.older_num_pages = older.page_stride, older.pages
+            a.older_capacity_tokens = older_table.shape[1] * BLOCK_TOKENS
+        else:
+            _require(older_table is None, "older_table needs a PagedKV older segment")
+            a.older_seq_stride = older.seq_stride
+            a.older_capacity_tokens = older.capacity_tokens
+            a.older_slot = _ptr(older_slot)
+            a.older_num_slots = older.slots
+            if older_slot is None:
+                _require(older.slots >= B, "older cache has fewer slots than sequences")
         if not isinstance(older_len, torch.Tensor):
-            _require(0 <= older_len <= older.capacity_tokens, "older_len exceeds the cache capacity")
+            _require(0 <= older_len <= a.older_capacity_tokens, "older_len exceeds the cache capacity")
     if local is not None:
         _require(local.device == device, "local cache on another device")
         a.local_k, a.local_v = local.k.data_ptr(), local.v.data_ptr()
-        a.local_seq_stride, a.local_head_stride = local.seq_stride, local.head_stride
-        a.local_ring_blocks = local.blocks
+        a.local_head_stride = local.head_stride
+        if isinstance(local, PagedKV):
+            _table_arg(local_table, B, "local", device)
+            _require(local_slot is None, "local_slot does not apply to a paged segment")
+            a.local_ring_blocks = int(local_ring_blocks if local_ring_blocks is not None else local_table.shape[1])
+            _require(0 < a.local_ring_blocks <= local_table.shape[1], "local_ring_blocks exceeds the table width")
+            a.local_block_table, a.local_table_stride = local_table.data_ptr(), local_table.stride(0)
+            a.local_page_stride, a.local_num_pages = local.page_stride, local.pages
+        else:
+            _require(local_table is None, "local_table needs a PagedKV local segment")
+            a.local_seq_stride = local.seq_stride
+            a.local_ring_blocks = local.blocks
+            a.local_slot = _ptr(local_slot)
+            a.local_num_slots = local.slots
+            if local_slot is None:
+                _require(local.slots >= B, "local cache has fewer slots than sequences")
+        ring_tokens = a.local_ring_blocks * BLOCK_TOKENS
         a.local_len, a.local_len_const = _len_arg(local_len, B, "local_len", device)
         a.local_start, a.local_start_const = _len_arg(local_start, B, "local_start", device)
-        a.local_slot = _ptr(local_slot)
-        a.local_num_slots = local.slots
-        if local_slot is None:
-            _require(local.slots >= B, "local cache has fewer slots than sequences")
         if not isinstance(local_len, torch.Tensor):
-            _require(0 <= local_len <= local.capacity_tokens, "local_len exceeds the ring capacity")
+            _require(0 <= local_len <= ring_tokens, "local_len exceeds the ring capacity")
         if not isinstance(local_start, torch.Tensor):
-            _require(0 <= local_start < local.capacity_tokens, "local_start outside the ring")
+            _require(0 <= local_start < ring_tokens, "local_start outside the ring")
     return Hkv
 
 
 def decode_attention(
     q: torch.Tensor,
     *,
-    older: TiledKV | None = None,
+    older: TiledKV | PagedKV | None = None,
     older_len: int | torch.Tensor = 0,
     older_slot: torch.Tensor | None = None,
     vscale: torch.Tensor | None = None,
-    local: TiledKV | None = None,
+    local: TiledKV | PagedKV | None = None,
     local_len: int | torch.Tensor = 0,
     local_start: int | torch.Tensor = 0,
     local_slot: torch.Tensor | None = None,
+    older_table: torch.Tensor | None = None,
+    local_table: torch.Tensor | None = None,
+    local_ring_blocks: int | None = None,
     sm_scale: float | None = None,
     num_splits: int | None = None,
     out: torch.Tensor | None = None,
@@ -250,7 +326,8 @@ def decode_attention(
     device = q.device
     a = _lib.DecodeArgs()
     a.struct_size = ctypes.sizeof(_lib.DecodeArgs)
-    Hkv = _fill_segments(a, B, device, older, older_len, older_slot, vscale, local, local_len, local_start, local_slot)
+    Hkv = _fill_segments(a, B, device, older, older_len, older_slot, vscale, local, local_len, local_start, local_slot,
+                         older_table, local_table, local_ring_blocks)
     _require(Hq % Hkv == 0 and Hq // Hkv <= 16, "Hq must be a multiple of Hkv with group <= 16")
     if out is None:
         out = torch.empty((B, Hq, HEAD_DIM), dtype=torch.bfloat16, device=device)
@@ -290,14 +367,17 @@ def decode_attention(
 def prefill_attention(
     q: torch.Tensor,
     *,
-    older: TiledKV | None = None,
+    older: TiledKV | PagedKV | None = None,
     older_len: int | torch.Tensor = 0,
     older_slot: torch.Tensor | None = None,
     vscale: torch.Tensor | None = None,
-    local: TiledKV | None = None,
+    local: TiledKV | PagedKV | None = None,
     local_len: int | torch.Tensor = 0,
     local_start: int | torch.Tensor = 0,
     local_slot: torch.Tensor | None = None,
+    older_table: torch.Tensor | None = None,
+    local_table: torch.Tensor | None = None,
+    local_ring_blocks: int | None = None,
     causal: bool = True,
     sm_scale: float | None = None,
     out: torch.Tensor | None = None,
@@ -318,7 +398,8 @@ def prefill_attention(
     device = q.device
     a = _lib.PrefillArgs()
     a.struct_size = ctypes.sizeof(_lib.PrefillArgs)
-    Hkv = _fill_segments(a, B, device, older, older_len, older_slot, vscale, local, local_len, local_start, local_slot)
+    Hkv = _fill_segments(a, B, device, older, older_len, older_slot, vscale, local, local_len, local_start, local_slot,
+                         older_table, local_table, local_ring_blocks)
     _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
     if out is None:
         out = torch.empty((B, L, Hq, HEAD_DIM), dtype=torch.bfloat16, device=device)
