@@ -279,6 +279,19 @@ typedef struct lkv_qkv_args {
   int32_t deep_capacity_tokens;
   int32_t deep_num_slots;
   const int32_t *deep_slot; /* device [B] or NULL -> slot b */
+  /* Optional paging (the serving path's page pool): with ring_block_table, ring block rb of
+   * sequence b is page ring_block_table[b * ring_table_stride + rb] of the pool at ring_k /
+   * ring_v (page p of kv head g at p * ring_page_stride + g * ring_head_stride; ring slots and
+   * ring_seq_stride unused); deep_block_table likewise maps deep block j of sequence b.  Page ids
+   * are clamped into [0, num_pages). */
+  const int32_t *ring_block_table;
+  int64_t ring_table_stride;
+  int64_t ring_page_stride;
+  int32_t ring_num_pages;
+  const int32_t *deep_block_table;
+  int64_t deep_table_stride;
+  int64_t deep_page_stride;
+  int32_t deep_num_pages;
 } lkv_qkv_args;
 
 int32_t lkv_qkv_epilogue(const lkv_qkv_args *args, lkv_stream_t stream);
@@ -296,12 +309,43 @@ int32_t lkv_qkv_epilogue(const lkv_qkv_args *args, lkv_stream_t stream);
  * which is the reference's bf16 expression evaluated op by op.  Both caches are tiled; R =
  * ring_tokens (a multiple of 32).  Layer l's ring is ring + l * ring_layer_stride.
  * ------------------------------------------------------------------------------------- */
-int32_t lkv_blend_chunk(int32_t layers, int32_t batch, int32_t kv_heads, int32_t chunk_start, int32_t chunk_len,
-                        void *ring_k, void *ring_v, int64_t ring_layer_stride, int64_t ring_seq_stride,
-                        int64_t ring_head_stride, int32_t ring_tokens, const void *deep_k, const void *deep_v,
-                        int64_t deep_seq_stride, int64_t deep_head_stride, int32_t deep_capacity_tokens,
-                        const float *alpha, const float *one_minus_alpha, const float *vscale,
-                        lkv_stream_t stream);
+typedef struct lkv_blend_args {
+  int32_t struct_size; /* sizeof(lkv_blend_args) */
+  int32_t layers;
+  int32_t batch;
+  int32_t kv_heads;
+  int32_t chunk_start;
+  int32_t chunk_len;
+  void *ring_k; /* tiled rings, layer l at ring + l * ring_layer_stride (or a page pool, below) */
+  void *ring_v;
+  int64_t ring_layer_stride;
+  int64_t ring_seq_stride;
+  int64_t ring_head_stride;
+  int32_t ring_tokens;
+  const void *deep_k; /* tiled shared store (or a page pool, below) */
+  const void *deep_v;
+  int64_t deep_seq_stride;
+  int64_t deep_head_stride;
+  int32_t deep_capacity_tokens;
+  const float *alpha;           /* [layers * kv_heads] */
+  const float *one_minus_alpha; /* [layers * kv_heads] */
+  const float *vscale;          /* [layers * kv_heads] or NULL (s = 1) */
+  /* Optional paging: ring block rb of (layer l, sequence b) is page ring_block_table[l *
+   * ring_table_layer_stride + b * ring_table_stride + rb] of the ring pool (page stride
+   * ring_page_stride; ring_layer_stride / ring_seq_stride unused); deep block j of sequence b is
+   * page deep_block_table[b * deep_table_stride + j] of the deep pool.  Ids are clamped. */
+  const int32_t *ring_block_table;
+  int64_t ring_table_layer_stride;
+  int64_t ring_table_stride;
+  int64_t ring_page_stride;
+  int32_t ring_num_pages;
+  const int32_t *deep_block_table;
+  int64_t deep_table_stride;
+  int64_t deep_page_stride;
+  int32_t deep_num_pages;
+} lkv_blend_args;
+
+int32_t lkv_blend_chunk(const lkv_blend_args *args, lkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
  * Exact merge of two attention states over disjoint key sets.

@@ -204,6 +204,50 @@ class QkvArgs(ctypes.Structure):
         ("deep_capacity_tokens", c_i32),
         ("deep_num_slots", c_i32),
         ("deep_slot", c_ptr),
+        ("ring_block_table", c_ptr),
+        ("ring_table_stride", c_i64),
+        ("ring_page_stride", c_i64),
+        ("ring_num_pages", c_i32),
+        ("deep_block_table", c_ptr),
+        ("deep_table_stride", c_i64),
+        ("deep_page_stride", c_i64),
+        ("deep_num_pages", c_i32),
+    ]
+
+
+class BlendArgs(ctypes.Structure):
+    """Mirror of ``lkv_blend_args``."""
+
+    _fields_ = [
+        ("struct_size", c_i32),
+        ("layers", c_i32),
+        ("batch", c_i32),
+        ("kv_heads", c_i32),
+        ("chunk_start", c_i32),
+        ("chunk_len", c_i32),
+        ("ring_k", c_ptr),
+        ("ring_v", c_ptr),
+        ("ring_layer_stride", c_i64),
+        ("ring_seq_stride", c_i64),
+        ("ring_head_stride", c_i64),
+        ("ring_tokens", c_i32),
+        ("deep_k", c_ptr),
+        ("deep_v", c_ptr),
+        ("deep_seq_stride", c_i64),
+        ("deep_head_stride", c_i64),
+        ("deep_capacity_tokens", c_i32),
+        ("alpha", c_ptr),
+        ("one_minus_alpha", c_ptr),
+        ("vscale", c_ptr),
+        ("ring_block_table", c_ptr),
+        ("ring_table_layer_stride", c_i64),
+        ("ring_table_stride", c_i64),
+        ("ring_page_stride", c_i64),
+        ("ring_num_pages", c_i32),
+        ("deep_block_table", c_ptr),
+        ("deep_table_stride", c_i64),
+        ("deep_page_stride", c_i64),
+        ("deep_num_pages", c_i32),
     ]
 
 
@@ -225,11 +269,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lkv_prefill_attn": (c_i32, [ctypes.POINTER(PrefillArgs), c_ptr]),
     "lkv_merge_states": (c_i32, [ctypes.POINTER(MergeArgs), c_ptr]),
     "lkv_qkv_epilogue": (c_i32, [ctypes.POINTER(QkvArgs), c_ptr]),
-    "lkv_blend_chunk": (
-        c_i32,
-        [c_i32, c_i32, c_i32, c_i32, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_i64, c_i64,
-         c_i32, c_ptr, c_ptr, c_ptr, c_ptr],
-    ),
+    "lkv_blend_chunk": (c_i32, [ctypes.POINTER(BlendArgs), c_ptr]),
 }
 
 _lock = threading.Lock()

@@ -38,7 +38,21 @@ struct QkvParams {
   int64_t d_ss, d_hs;
   int32_t deep_cap, deep_slots;
   const int32_t* deep_slot;
+  // optional page tables: block j of sequence b is page tab[b * tab_stride + j] of the pool
+  const int32_t* r_tab;
+  int64_t r_tab_stride, r_page;
+  int32_t r_npages;
+  const int32_t* d_tab;
+  int64_t d_tab_stride, d_page;
+  int32_t d_npages;
 };
+
+// Element offset of block blk of sequence b: contiguous per slot, or a clamped page of a pool.
+__device__ inline int64_t write_block(const int32_t* tab, int64_t tab_stride, int64_t page, int32_t npages, int b,
+                                      int blk) {
+  if (tab == nullptr) return static_cast<int64_t>(blk) * kBlockElems;
+  return static_cast<int64_t>(min(max(tab[b * tab_stride + blk], 0), npages - 1)) * page;
+}
 
 __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
   const int lane = threadIdx.x & 63;
@@ -81,11 +95,12 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
   const uint16_t* vrow = p.v + b * p.v_sb + i * p.v_st + static_cast<int64_t>(g) * kHeadDim;
   const uint16_t v0 = vrow[lane], v1 = vrow[lane + 64];
   {
-    const int slot = p.ring_slot ? p.ring_slot[b] : b;
+    const int slot = p.r_tab ? 0 : (p.ring_slot ? p.ring_slot[b] : b);
     if (slot >= 0 && slot < p.ring_slots) {
       const int rt = position % p.ring_tokens;
-      uint16_t* kb = p.rk + slot * p.r_ss + g * p.r_hs + static_cast<int64_t>(rt >> 5) * kBlockElems;
-      uint16_t* vb = p.rv + slot * p.r_ss + g * p.r_hs + static_cast<int64_t>(rt >> 5) * kBlockElems;
+      const int64_t off = slot * p.r_ss + g * p.r_hs + write_block(p.r_tab, p.r_tab_stride, p.r_page, p.r_npages, b, rt >> 5);
+      uint16_t* kb = p.rk + off;
+      uint16_t* vb = p.rv + off;
       const int wt = rt & 31;
       kb[k_tile_offset(wt, lane)] = o0;
       kb[k_tile_offset(wt, lane + 64)] = o1;
@@ -94,10 +109,11 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
     }
   }
   if (p.dk != nullptr && position < p.deep_cap) {
-    const int slot = p.deep_slot ? p.deep_slot[b] : b;
+    const int slot = p.d_tab ? 0 : (p.deep_slot ? p.deep_slot[b] : b);
     if (slot >= 0 && slot < p.deep_slots) {
-      uint16_t* kb = p.dk + slot * p.d_ss + g * p.d_hs + static_cast<int64_t>(position >> 5) * kBlockElems;
-      uint16_t* vb = p.dv + slot * p.d_ss + g * p.d_hs + static_cast<int64_t>(position >> 5) * kBlockElems;
+      const int64_t off = slot * p.d_ss + g * p.d_hs + write_block(p.d_tab, p.d_tab_stride, p.d_page, p.d_npages, b, position >> 5);
+      uint16_t* kb = p.dk + off;
+      uint16_t* vb = p.dv + off;
       const int wt = position & 31;
       kb[k_tile_offset(wt, lane)] = o0;
       kb[k_tile_offset(wt, lane + 64)] = o1;
@@ -117,6 +133,12 @@ struct BlendParams {
   const uint16_t *dk, *dv;
   int64_t d_ss, d_hs;
   const float *alpha, *om, *vs;
+  const int32_t* r_tab;  // [layers, batch, .] ring pages, or nullptr
+  int64_t r_tab_ls, r_tab_stride, r_page;
+  int32_t r_npages;
+  const int32_t* d_tab;  // [batch, .] shared-store pages, or nullptr
+  int64_t d_tab_stride, d_page;
+  int32_t d_npages;
 };
 
 // One thread per 8-element (16-byte) run of one block of one (layer, sequence, head).  K and
@@ -142,10 +164,13 @@ __global__ __launch_bounds__(256) void blend_kernel(const BlendParams p) {
     const int lh = l * p.heads + g;
     const float a = p.alpha[lh], om = p.om[lh];
     const float s = (kind == 1 && p.vs != nullptr) ? p.vs[lh] : 1.f;
-    const uint16_t* dsrc = (kind == 0 ? p.dk : p.dv) + b * p.d_ss + g * p.d_hs +
-                           static_cast<int64_t>(blk) * kBlockElems + off;
-    uint16_t* rdst = (kind == 0 ? p.rk : p.rv) + l * p.r_ls + b * p.r_ss + g * p.r_hs +
-                     static_cast<int64_t>(ring_blk) * kBlockElems + off;
+    const int64_t doff = (p.d_tab ? 0 : b * p.d_ss) + g * p.d_hs +
+                         write_block(p.d_tab, p.d_tab_stride, p.d_page, p.d_npages, b, blk);
+    const int64_t roff = p.r_tab ? g * p.r_hs + write_block(p.r_tab + l * p.r_tab_ls, p.r_tab_stride, p.r_page,
+                                                            p.r_npages, b, ring_blk)
+                                 : l * p.r_ls + b * p.r_ss + g * p.r_hs + static_cast<int64_t>(ring_blk) * kBlockElems;
+    const uint16_t* dsrc = (kind == 0 ? p.dk : p.dv) + doff + off;
+    uint16_t* rdst = (kind == 0 ? p.rk : p.rv) + roff + off;
     const uint4 dv4 = *reinterpret_cast<const uint4*>(dsrc);
     uint4 rv4 = *reinterpret_cast<const uint4*>(rdst);
     const uint16_t* de = reinterpret_cast<const uint16_t*>(&dv4);
@@ -181,12 +206,22 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
   LKV_REQUIRE(a->q && a->k && a->v && a->cos && a->sin && a->q_out, "null tensor pointer");
   LKV_REQUIRE(a->ring_k && a->ring_v, "ring cache required");
   LKV_REQUIRE(a->ring_tokens > 0 && a->ring_tokens % kBlockTokens == 0, "ring_tokens must be a positive multiple of 32");
-  LKV_REQUIRE(a->ring_num_slots > 0, "ring_num_slots must be positive");
-  LKV_REQUIRE(a->ring_slot != nullptr || a->ring_num_slots >= a->batch, "ring has fewer slots than sequences");
+  const bool rpaged = a->ring_block_table != nullptr, dpaged = a->deep_block_table != nullptr;
+  if (rpaged) {
+    LKV_REQUIRE(a->ring_num_pages > 0 && a->ring_table_stride * kBlockTokens >= a->ring_tokens,
+                "ring page table must hold ring_tokens / 32 pages of a non-empty pool");
+  } else {
+    LKV_REQUIRE(a->ring_num_slots > 0, "ring_num_slots must be positive");
+    LKV_REQUIRE(a->ring_slot != nullptr || a->ring_num_slots >= a->batch, "ring has fewer slots than sequences");
+  }
   LKV_REQUIRE((a->deep_k == nullptr) == (a->deep_v == nullptr), "deep_k and deep_v must both be set");
   LKV_REQUIRE(a->deep_k == nullptr || a->deep_capacity_tokens % kBlockTokens == 0, "deep capacity must be a multiple of 32");
-  LKV_REQUIRE(a->deep_k == nullptr || a->deep_slot != nullptr || a->deep_num_slots >= a->batch,
-              "deep cache has fewer slots than sequences");
+  if (a->deep_k != nullptr && dpaged) {
+    LKV_REQUIRE(a->deep_num_pages > 0 && a->deep_table_stride * kBlockTokens >= a->deep_capacity_tokens,
+                "deep page table must hold deep_capacity_tokens / 32 pages of a non-empty pool");
+  } else if (a->deep_k != nullptr) {
+    LKV_REQUIRE(a->deep_slot != nullptr || a->deep_num_slots >= a->batch, "deep cache has fewer slots than sequences");
+  }
   LKV_REQUIRE(a->positions != nullptr || a->position_const >= 0, "negative position");
   const int64_t items = static_cast<int64_t>(a->batch) * a->tokens * (a->num_q_heads + a->num_kv_heads);
   if (items == 0) return LKV_OK;
@@ -229,55 +264,76 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
   p.d_ss = a->deep_seq_stride;
   p.d_hs = a->deep_head_stride;
   p.deep_cap = a->deep_k ? a->deep_capacity_tokens : 0;
-  p.deep_slots = a->deep_num_slots;
+  p.deep_slots = dpaged ? 1 : a->deep_num_slots;
   p.deep_slot = a->deep_slot;
+  p.ring_slots = rpaged ? 1 : a->ring_num_slots;
+  p.r_tab = a->ring_block_table;
+  p.r_tab_stride = a->ring_table_stride;
+  p.r_page = a->ring_page_stride;
+  p.r_npages = a->ring_num_pages;
+  p.d_tab = a->deep_block_table;
+  p.d_tab_stride = a->deep_table_stride;
+  p.d_page = a->deep_page_stride;
+  p.d_npages = a->deep_num_pages;
   const int blocks = static_cast<int>((items + 3) / 4);
   qkv_epilogue_kernel<<<blocks, 256, 0, as_stream(stream)>>>(p);
   return check_launch("lkv_qkv_epilogue");
 }
 
-extern "C" int32_t lkv_blend_chunk(int32_t layers, int32_t batch, int32_t kv_heads, int32_t chunk_start,
-                                   int32_t chunk_len, void* ring_k, void* ring_v, int64_t ring_layer_stride,
-                                   int64_t ring_seq_stride, int64_t ring_head_stride, int32_t ring_tokens,
-                                   const void* deep_k, const void* deep_v, int64_t deep_seq_stride,
-                                   int64_t deep_head_stride, int32_t deep_capacity_tokens, const float* alpha,
-                                   const float* one_minus_alpha, const float* vscale, lkv_stream_t stream) {
+extern "C" int32_t lkv_blend_chunk(const lkv_blend_args* a, lkv_stream_t stream) {
   using namespace lkv;
-  LKV_REQUIRE(layers >= 0 && batch >= 0 && kv_heads > 0, "bad sizes");
-  LKV_REQUIRE(chunk_start >= 0 && chunk_len >= 0, "bad chunk range");
-  LKV_REQUIRE(ring_tokens > 0 && ring_tokens % kBlockTokens == 0, "ring_tokens must be a positive multiple of 32");
-  LKV_REQUIRE(chunk_len <= ring_tokens, "chunk longer than the ring");
-  LKV_REQUIRE(static_cast<int64_t>(chunk_start) + chunk_len <= deep_capacity_tokens, "chunk beyond the deep capacity");
-  LKV_REQUIRE(ring_k && ring_v && deep_k && deep_v && alpha && one_minus_alpha, "null pointer");
-  if (layers == 0 || batch == 0 || chunk_len == 0) return LKV_OK;
+  LKV_REQUIRE(a != nullptr, "null args");
+  LKV_REQUIRE(a->struct_size == static_cast<int32_t>(sizeof(lkv_blend_args)), "lkv_blend_args size mismatch");
+  LKV_REQUIRE(a->layers >= 0 && a->batch >= 0 && a->kv_heads > 0, "bad sizes");
+  LKV_REQUIRE(a->chunk_start >= 0 && a->chunk_len >= 0, "bad chunk range");
+  LKV_REQUIRE(a->ring_tokens > 0 && a->ring_tokens % kBlockTokens == 0, "ring_tokens must be a positive multiple of 32");
+  LKV_REQUIRE(a->chunk_len <= a->ring_tokens, "chunk longer than the ring");
+  LKV_REQUIRE(static_cast<int64_t>(a->chunk_start) + a->chunk_len <= a->deep_capacity_tokens, "chunk beyond the deep capacity");
+  LKV_REQUIRE(a->ring_k && a->ring_v && a->deep_k && a->deep_v && a->alpha && a->one_minus_alpha, "null pointer");
+  LKV_REQUIRE(a->ring_block_table == nullptr ||
+                  (a->ring_num_pages > 0 && a->ring_table_stride * kBlockTokens >= a->ring_tokens),
+              "ring page table must hold ring_tokens / 32 pages of a non-empty pool");
+  LKV_REQUIRE(a->deep_block_table == nullptr ||
+                  (a->deep_num_pages > 0 && a->deep_table_stride * kBlockTokens >= a->deep_capacity_tokens),
+              "deep page table must hold deep_capacity_tokens / 32 pages of a non-empty pool");
+  if (a->layers == 0 || a->batch == 0 || a->chunk_len == 0) return LKV_OK;
   // two blocks of the chunk must not share a ring block, or their threads would race on it
-  const int first_blk = chunk_start / kBlockTokens;
-  const int last_blk = (chunk_start + chunk_len - 1) / kBlockTokens;
-  LKV_REQUIRE(last_blk - first_blk + 1 <= ring_tokens / kBlockTokens,
-              "chunk [%d, %d) spans more 32-token blocks than the ring holds (%d tokens)", chunk_start,
-              chunk_start + chunk_len, ring_tokens);
+  const int first_blk = a->chunk_start / kBlockTokens;
+  const int last_blk = (a->chunk_start + a->chunk_len - 1) / kBlockTokens;
+  LKV_REQUIRE(last_blk - first_blk + 1 <= a->ring_tokens / kBlockTokens,
+              "chunk [%d, %d) spans more 32-token blocks than the ring holds (%d tokens)", a->chunk_start,
+              a->chunk_start + a->chunk_len, a->ring_tokens);
   BlendParams p;
-  p.layers = layers;
-  p.batch = batch;
-  p.heads = kv_heads;
-  p.start = chunk_start;
-  p.end = chunk_start + chunk_len;
+  p.layers = a->layers;
+  p.batch = a->batch;
+  p.heads = a->kv_heads;
+  p.start = a->chunk_start;
+  p.end = a->chunk_start + a->chunk_len;
   p.blk0 = first_blk;
   p.nblk = last_blk - first_blk + 1;
-  p.rk = static_cast<uint16_t*>(ring_k);
-  p.rv = static_cast<uint16_t*>(ring_v);
-  p.r_ls = ring_layer_stride;
-  p.r_ss = ring_seq_stride;
-  p.r_hs = ring_head_stride;
-  p.ring_tokens = ring_tokens;
-  p.dk = static_cast<const uint16_t*>(deep_k);
-  p.dv = static_cast<const uint16_t*>(deep_v);
-  p.d_ss = deep_seq_stride;
-  p.d_hs = deep_head_stride;
-  p.alpha = alpha;
-  p.om = one_minus_alpha;
-  p.vs = vscale;
-  const int64_t total = static_cast<int64_t>(layers) * batch * kv_heads * p.nblk * (kBlockElems / 8) * 2;
+  p.rk = static_cast<uint16_t*>(a->ring_k);
+  p.rv = static_cast<uint16_t*>(a->ring_v);
+  p.r_ls = a->ring_layer_stride;
+  p.r_ss = a->ring_seq_stride;
+  p.r_hs = a->ring_head_stride;
+  p.ring_tokens = a->ring_tokens;
+  p.dk = static_cast<const uint16_t*>(a->deep_k);
+  p.dv = static_cast<const uint16_t*>(a->deep_v);
+  p.d_ss = a->deep_seq_stride;
+  p.d_hs = a->deep_head_stride;
+  p.alpha = a->alpha;
+  p.om = a->one_minus_alpha;
+  p.vs = a->vscale;
+  p.r_tab = a->ring_block_table;
+  p.r_tab_ls = a->ring_table_layer_stride;
+  p.r_tab_stride = a->ring_table_stride;
+  p.r_page = a->ring_page_stride;
+  p.r_npages = a->ring_num_pages;
+  p.d_tab = a->deep_block_table;
+  p.d_tab_stride = a->deep_table_stride;
+  p.d_page = a->deep_page_stride;
+  p.d_npages = a->deep_num_pages;
+  const int64_t total = static_cast<int64_t>(a->layers) * a->batch * a->kv_heads * p.nblk * (kBlockElems / 8) * 2;
   const int64_t want = (total + 255) / 256;
   const int grid = static_cast<int>(want < 65536 ? want : 65536);
   blend_kernel<<<grid, 256, 0, as_stream(stream)>>>(p);

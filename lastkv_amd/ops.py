@@ -525,15 +525,19 @@ def qkv_epilogue(
     k_norm_weight: torch.Tensor | None,
     eps: float,
     positions: int | torch.Tensor,
-    ring: TiledKV,
+    ring: TiledKV | PagedKV,
     ring_slot: torch.Tensor | None = None,
-    deep: TiledKV | None = None,
+    deep: TiledKV | PagedKV | None = None,
     deep_slot: torch.Tensor | None = None,
     q_out: torch.Tensor | None = None,
+    ring_table: torch.Tensor | None = None,
+    ring_tokens: int | None = None,
+    deep_table: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """RoPE + q/k RMSNorm of the projections and the append of K/V to the layer ring (and, for
     the final layer, the shared cache) at positions ``positions + i``; returns the normalised
-    queries ``[B, L, Hq, 128]``."""
+    queries ``[B, L, Hq, 128]``.  A PagedKV ring / deep store takes an int32 page table ``[B, W]``
+    (``ring_tokens``: the ring length, default ``32 * W``)."""
 
     B, L = int(q.shape[0]), int(q.shape[1])
     qp, qsb, qst = _rows("q", q, num_q_heads)
@@ -568,15 +572,31 @@ def qkv_epilogue(
     a.q_norm_w, a.k_norm_w = _ptr(q_norm_weight), _ptr(k_norm_weight)
     a.q_out, a.q_out_stride_b, a.q_out_stride_t = q_out.data_ptr(), q_out.stride(0), q_out.stride(1)
     a.ring_k, a.ring_v = ring.k.data_ptr(), ring.v.data_ptr()
-    a.ring_seq_stride, a.ring_head_stride = ring.seq_stride, ring.head_stride
-    a.ring_tokens, a.ring_num_slots, a.ring_slot = ring.capacity_tokens, ring.slots, _ptr(ring_slot)
+    a.ring_head_stride = ring.head_stride
+    if isinstance(ring, PagedKV):
+        _table_arg(ring_table, B, "ring", device)
+        a.ring_block_table, a.ring_table_stride = ring_table.data_ptr(), ring_table.stride(0)
+        a.ring_page_stride, a.ring_num_pages = ring.page_stride, ring.pages
+        a.ring_tokens = int(ring_tokens if ring_tokens is not None else ring_table.shape[1] * BLOCK_TOKENS)
+        _require(0 < a.ring_tokens <= ring_table.shape[1] * BLOCK_TOKENS and a.ring_tokens % BLOCK_TOKENS == 0,
+                 "ring_tokens must be a multiple of 32 within the ring table")
+    else:
+        a.ring_seq_stride = ring.seq_stride
+        a.ring_tokens, a.ring_num_slots, a.ring_slot = ring.capacity_tokens, ring.slots, _ptr(ring_slot)
     if deep is not None:
         _require(deep.heads == num_kv_heads, "deep kv heads mismatch")
         a.deep_k, a.deep_v = deep.k.data_ptr(), deep.v.data_ptr()
-        a.deep_seq_stride, a.deep_head_stride = deep.seq_stride, deep.head_stride
-        a.deep_capacity_tokens, a.deep_num_slots, a.deep_slot = deep.capacity_tokens, deep.slots, _ptr(deep_slot)
+        a.deep_head_stride = deep.head_stride
+        if isinstance(deep, PagedKV):
+            _table_arg(deep_table, B, "deep", device)
+            a.deep_block_table, a.deep_table_stride = deep_table.data_ptr(), deep_table.stride(0)
+            a.deep_page_stride, a.deep_num_pages = deep.page_stride, deep.pages
+            a.deep_capacity_tokens = deep_table.shape[1] * BLOCK_TOKENS
+        else:
+            a.deep_seq_stride = deep.seq_stride
+            a.deep_capacity_tokens, a.deep_num_slots, a.deep_slot = deep.capacity_tokens, deep.slots, _ptr(deep_slot)
         if not isinstance(positions, torch.Tensor):
-            _require(positions + L <= deep.capacity_tokens, "positions exceed the shared cache capacity")
+            _require(positions + L <= a.deep_capacity_tokens, "positions exceed the shared cache capacity")
     lib = _lib.load()
     _lib.check(lib.lkv_qkv_epilogue(ctypes.byref(a), _stream(device)), "lkv_qkv_epilogue")
     return q_out
@@ -585,7 +605,7 @@ def qkv_epilogue(
 def blend_chunk(
     ring_k: torch.Tensor,
     ring_v: torch.Tensor,
-    deep: TiledKV,
+    deep: TiledKV | PagedKV,
     *,
     batch: int,
     chunk_start: int,
@@ -593,31 +613,60 @@ def blend_chunk(
     alpha: torch.Tensor,
     one_minus_alpha: torch.Tensor,
     vscale: torch.Tensor | None,
+    ring_table: torch.Tensor | None = None,
+    ring_tokens: int | None = None,
+    deep_table: torch.Tensor | None = None,
 ) -> None:
-    """Boundary commit: for every layer's ring (``ring_k``/``ring_v`` ``[layers, slots, H,
-    blocks, 4096]``) blend tokens ``[chunk_start, chunk_start + chunk_len)`` with the shared cache
-    in place.  ``alpha``, ``one_minus_alpha``, ``vscale``: fp32 ``[layers * H]`` bf16 values."""
+    """Boundary commit: for every layer's ring blend tokens ``[chunk_start, chunk_start +
+    chunk_len)`` with the shared cache in place.  ``alpha``, ``one_minus_alpha``, ``vscale``: fp32
+    ``[layers * H]`` bf16 values.
+
+    Contiguous rings: ``ring_k``/``ring_v`` ``[layers, slots, H, blocks, 4096]``.  Paged rings: the
+    pool ``[pages, H, 4096]`` and ``ring_table`` int32 ``[layers, batch, W]`` (ring block rb of
+    layer l, sequence b is page ``ring_table[l, b, rb]``; ``ring_tokens`` defaults to ``32 * W``).
+    A PagedKV ``deep`` takes ``deep_table`` ``[batch, W']``."""
 
     for name, t in (("ring_k", ring_k), ("ring_v", ring_v)):
         _require_bf16_cuda(name, t)
-        _require(t.dim() == 5 and t.shape[-1] == BLOCK_ELEMS and t.is_contiguous(), f"{name} must be contiguous [layers, slots, H, blocks, 4096]")
-    _require(ring_k.shape == ring_v.shape, "ring k/v shapes differ")
-    layers, slots, H, blocks, _ = ring_k.shape
-    _require(H == deep.heads and batch <= slots and batch <= deep.slots, "ring/deep geometry mismatch")
+    _require(ring_k.shape == ring_v.shape and ring_k.is_contiguous() and ring_v.is_contiguous(), "ring k/v must be contiguous and alike")
+    device = deep.device
+    a = _lib.BlendArgs()
+    a.struct_size = ctypes.sizeof(_lib.BlendArgs)
+    if ring_table is None:
+        _require(ring_k.dim() == 5 and ring_k.shape[-1] == BLOCK_ELEMS, "ring_k must be [layers, slots, H, blocks, 4096]")
+        layers, slots, H, blocks, _ = ring_k.shape
+        _require(batch <= slots, "ring has fewer slots than sequences")
+        a.ring_layer_stride, a.ring_seq_stride, a.ring_head_stride = ring_k.stride(0), ring_k.stride(1), ring_k.stride(2)
+        a.ring_tokens = blocks * BLOCK_TOKENS
+    else:
+        _require(ring_k.dim() == 3 and ring_k.shape[-1] == BLOCK_ELEMS, "a paged ring pool must be [pages, H, 4096]")
+        _require(ring_table.dtype == torch.int32 and ring_table.dim() == 3 and ring_table.shape[1] == batch
+                 and ring_table.stride(2) == 1 and ring_table.device == device, "ring_table must be int32 [layers, batch, W]")
+        layers, H = int(ring_table.shape[0]), int(ring_k.shape[1])
+        a.ring_head_stride = BLOCK_ELEMS
+        a.ring_block_table = ring_table.data_ptr()
+        a.ring_table_layer_stride, a.ring_table_stride = ring_table.stride(0), ring_table.stride(1)
+        a.ring_page_stride, a.ring_num_pages = H * BLOCK_ELEMS, int(ring_k.shape[0])
+        a.ring_tokens = int(ring_tokens if ring_tokens is not None else ring_table.shape[2] * BLOCK_TOKENS)
+    _require(H == deep.heads, "ring/deep head counts differ")
     for name, t in (("alpha", alpha), ("one_minus_alpha", one_minus_alpha), ("vscale", vscale)):
         if t is not None:
-            _require(t.dtype == torch.float32 and t.is_contiguous() and t.numel() == layers * H and t.device == deep.device,
+            _require(t.dtype == torch.float32 and t.is_contiguous() and t.numel() == layers * H and t.device == device,
                      f"{name} must be a contiguous fp32 [layers * H] tensor")
-    lib = _lib.load()
-    _lib.check(
-        lib.lkv_blend_chunk(
-            layers, batch, H, chunk_start, chunk_len, ring_k.data_ptr(), ring_v.data_ptr(), ring_k.stride(0),
-            ring_k.stride(1), ring_k.stride(2), blocks * BLOCK_TOKENS, deep.k.data_ptr(), deep.v.data_ptr(),
-            deep.seq_stride, deep.head_stride, deep.capacity_tokens, alpha.data_ptr(), one_minus_alpha.data_ptr(),
-            _ptr(vscale), _stream(deep.device),
-        ),
-        "lkv_blend_chunk",
-    )
+    a.layers, a.batch, a.kv_heads, a.chunk_start, a.chunk_len = layers, batch, H, chunk_start, chunk_len
+    a.ring_k, a.ring_v = ring_k.data_ptr(), ring_v.data_ptr()
+    a.deep_k, a.deep_v = deep.k.data_ptr(), deep.v.data_ptr()
+    a.deep_head_stride = deep.head_stride
+    if isinstance(deep, PagedKV):
+        _table_arg(deep_table, batch, "deep", device)
+        a.deep_block_table, a.deep_table_stride = deep_table.data_ptr(), deep_table.stride(0)
+        a.deep_page_stride, a.deep_num_pages = deep.page_stride, deep.pages
+        a.deep_capacity_tokens = deep_table.shape[1] * BLOCK_TOKENS
+    else:
+        _require(batch <= deep.slots, "shared cache has fewer slots than sequences")
+        a.deep_seq_stride, a.deep_capacity_tokens = deep.seq_stride, deep.capacity_tokens
+    a.alpha, a.one_minus_alpha, a.vscale = alpha.data_ptr(), one_minus_alpha.data_ptr(), _ptr(vscale)
+    _lib.check(_lib.load().lkv_blend_chunk(ctypes.byref(a), _stream(device)), "lkv_blend_chunk")
 
 
 def ring_tokens_for_chunk(chunk: int) -> int:

@@ -104,3 +104,63 @@ def test_corrupt_page_ids_stay_inside_the_pool():
     out2 = ops.prefill_attention(ql, older=pool, older_table=table, older_len=128)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all() and torch.isfinite(out2.float()).all()
+
+
+def _gather(pool: ops.PagedKV, table: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Pool pages listed in ``table`` [S, nb] back into contiguous [S, H, nb, 4096] caches."""
+
+    S, nb = table.shape
+    idx = table.reshape(-1).long()
+    k = pool.k[idx].view(S, nb, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
+    v = pool.v[idx].view(S, nb, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
+    return k, v
+
+
+def test_epilogue_paged_equals_contiguous():
+    g = torch.Generator(device=DEV).manual_seed(9)
+    B, L, Hq, Hkv, p0 = 3, 20, 8, 2, 50
+    ring = _rand_cache(g, B, Hkv, 128)
+    deep = _rand_cache(g, B, Hkv, 256)
+    perm = torch.randperm(B * 12 + 5, generator=torch.Generator().manual_seed(1)).to(DEV)
+    pool = ops.PagedKV.zeros(B * 12 + 5, Hkv, DEV)
+    rtab = _scatter(ring, pool, perm[: B * 4].view(B, 4))
+    dtab = _scatter(deep, pool, perm[B * 4 : B * 12].view(B, 8))
+    q = torch.randn((B, L, Hq * 128), generator=g, device=DEV).bfloat16()
+    k = torch.randn((B, L, Hkv * 128), generator=g, device=DEV).bfloat16()
+    v = torch.randn((B, L, Hkv * 128), generator=g, device=DEV).bfloat16()
+    cos = torch.rand((1, L, 128), generator=g, device=DEV).bfloat16()
+    sin = torch.rand((1, L, 128), generator=g, device=DEV).bfloat16()
+    w = (torch.rand(128, generator=g, device=DEV) + 0.5).bfloat16()
+    pos = torch.tensor([p0, p0 + 37, p0 + 90], dtype=torch.int32, device=DEV)
+    kw = dict(num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=w, k_norm_weight=w, eps=1e-5, positions=pos)
+    qa = ops.qkv_epilogue(q, k, v, cos, sin, ring=ring, deep=deep, **kw)
+    qb = ops.qkv_epilogue(q, k, v, cos, sin, ring=pool, ring_table=rtab, deep=pool, deep_table=dtab, **kw)
+    assert torch.equal(qa, qb)
+    rk, rv = _gather(pool, rtab)
+    dk, dv = _gather(pool, dtab)
+    assert torch.equal(rk, ring.k) and torch.equal(rv, ring.v)
+    assert torch.equal(dk, deep.k) and torch.equal(dv, deep.v)
+
+
+def test_blend_paged_equals_contiguous():
+    g = torch.Generator(device=DEV).manual_seed(4)
+    layers, B, H, C = 3, 2, 2, 64
+    R = ops.ring_tokens_for_chunk(C)
+    deep = _rand_cache(g, B, H, 256)
+    ring_k = torch.randn((layers, B, H, R // 32, 4096), generator=g, device=DEV).bfloat16()
+    ring_v = torch.randn_like(ring_k)
+    pages = layers * B * (R // 32) + B * 8 + 3
+    perm = torch.randperm(pages, generator=torch.Generator().manual_seed(2)).to(DEV)
+    pool = ops.PagedKV.zeros(pages, H, DEV)
+    rtab = torch.stack([_scatter(ops.TiledKV(ring_k[l].contiguous(), ring_v[l].contiguous()), pool,
+                                 perm[l * B * (R // 32) : (l + 1) * B * (R // 32)].view(B, R // 32)) for l in range(layers)])
+    dtab = _scatter(deep, pool, perm[layers * B * (R // 32) : layers * B * (R // 32) + B * 8].view(B, 8))
+    alpha = torch.rand(layers * H, generator=g, device=DEV).bfloat16().float()
+    om = (1 - alpha).bfloat16().float()
+    vs = (torch.rand(layers * H, generator=g, device=DEV) + 0.5).bfloat16().float()
+    kw = dict(batch=B, chunk_start=2 * C, chunk_len=C, alpha=alpha, one_minus_alpha=om, vscale=vs)
+    ops.blend_chunk(ring_k, ring_v, deep, **kw)
+    ops.blend_chunk(pool.k, pool.v, pool, ring_table=rtab.contiguous(), deep_table=dtab, **kw)
+    for l in range(layers):
+        k, v = _gather(pool, rtab[l])
+        assert torch.equal(k, ring_k[l]) and torch.equal(v, ring_v[l])
