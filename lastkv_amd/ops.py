@@ -341,9 +341,9 @@ def decode_attention(
                  "lse must be a contiguous fp32 [B, Hq] tensor")
     max_tokens = 0
     if older is not None:
-        max_tokens += older.capacity_tokens if isinstance(older_len, torch.Tensor) else int(older_len)
+        max_tokens += a.older_capacity_tokens if isinstance(older_len, torch.Tensor) else int(older_len)
     if local is not None:
-        max_tokens += local.capacity_tokens if isinstance(local_len, torch.Tensor) else int(local_len)
+        max_tokens += a.local_ring_blocks * BLOCK_TOKENS if isinstance(local_len, torch.Tensor) else int(local_len)
     if num_splits is None:
         num_splits = default_decode_splits(B, Hkv, max_tokens, _cu_count(device))
     lib = _lib.load()
@@ -425,6 +425,12 @@ def prefill_attention(
     _require(a.workspace_bytes >= need, f"prefill workspace too small: {a.workspace_bytes} < {need} bytes")
     _lib.check(lib.lkv_prefill_attn(ctypes.byref(a), _stream(device)), "lkv_prefill_attn")
     return out
+
+
+def decode_workspace_bytes(batch: int, num_q_heads: int, num_splits: int) -> int:
+    """Bytes of the split-K workspace ``decode_attention`` needs (0 for one split)."""
+
+    return int(_lib.load().lkv_decode_workspace_bytes(batch, num_q_heads, num_splits))
 
 
 def prefill_workspace_bytes(batch: int, kv_heads: int, older_tokens: int, local_tokens: int, local_lead: int = 31) -> int:

@@ -1,0 +1,475 @@
+"""Serving fast path over one paged K/V pool: the MI355X counterpart of the reference's vLLM
+decode fast path (``vllm/src/lastkv/vllm/backends/rmarin_flashinfer/fastpath.py``), its fused
+slab pool (``batching.py:1971-2122``) and the model runner that calls it per layer
+(``vllm_model.py``, ``vllm_backend.py:637-664``).
+
+``LastKVPagePool`` holds every sequence's K/V in 32-token pages of one ``[pages, Hkv, 4096]`` pool
+(K and V): per slot, the shared last-layer pages of its positions (handed out as the sequence
+grows, like vLLM blocks) and, per layer, a fixed ring of ``ring_tokens_for_chunk(C)`` tokens (the
+recent + current chunk, the reference's per-layer ring pages).  ``LastKVFastPath.prepare`` is the
+host prologue of one step (``fastpath.py:455-575``, row plan ``:427-453``): boundary commits of
+sequences that completed a chunk, and the per-row positions, key lengths, ring starts and page
+table rows staged in device memory.  ``run_layer`` is the per-layer op sequence
+(``fastpath.py:619-651``): the fused QKV epilogue (RoPE + q/k RMSNorm + ring append, plus the
+shared append on the final layer) and one attention pass over [shared older pages | ring pages]
+written into ``output``.  For a decode step every per-layer call reads only device-resident
+metadata and preallocated buffers.
+
+Rounding contract: the HF bf16 one (older V used as bf16(V * s_l) inside the attention kernel,
+the recent chunk blended once per boundary in bf16), i.e. the numbers of ``lastkv_amd.llm``.  The
+reference's vLLM path instead keeps V / s_l in the rings and rescales the output
+(``fastpath.py:652-690``); that variant's extra roundings are not reproduced.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import ops
+
+BLOCK = ops.BLOCK_TOKENS
+
+
+def plan_row(position: int, tokens: int, chunk: int, ring_tokens: int) -> tuple[int, int, int]:
+    """Key segments of a row whose ``tokens`` new tokens start at ``position`` and stay inside one
+    chunk: (older keys = rec, local keys = position + tokens - rec, ring start = rec mod R), with
+    cur = floor(last / C) * C and rec = max(0, cur - C) (``access_plan.py:237-253``,
+    ``fastpath.py:427-453``)."""
+
+    if position < 0 or tokens < 1 or chunk < 1:
+        raise ValueError("position >= 0, tokens >= 1 and chunk >= 1 are required")
+    if position % chunk + tokens > chunk:
+        raise ValueError(f"tokens [{position}, {position + tokens}) cross a chunk boundary of C={chunk}")
+    rec = max(0, (position + tokens - 1) // chunk * chunk - chunk)
+    local = position + tokens - rec
+    if local > ring_tokens:
+        raise ValueError("the ring cannot hold the local window")
+    return rec, local, rec % ring_tokens
+
+
+class PageAllocator:
+    """Host bookkeeping of sequence slots and shared-cache pages: per slot a table row of page ids
+    (unused entries name ``scratch``), pages handed out in order as a sequence grows and returned
+    when its slot closes."""
+
+    def __init__(self, *, max_slots: int, pages: int, width: int, scratch: int):
+        self.width, self.scratch = width, scratch
+        self.table = np.full((max_slots, width), scratch, dtype=np.int32)
+        self.used = np.zeros(max_slots, dtype=np.int64)
+        self._free_pages = list(range(pages - 1, -1, -1))
+        self._free_slots = list(range(max_slots - 1, -1, -1))
+
+    @property
+    def free_pages(self) -> int:
+        return len(self._free_pages)
+
+    def open_slot(self) -> int:
+        if not self._free_slots:
+            raise RuntimeError("no free sequence slot in the pool")
+        return self._free_slots.pop()
+
+    def close_slot(self, slot: int) -> None:
+        n = int(self.used[slot])
+        self._free_pages.extend(int(p) for p in self.table[slot, :n][::-1])
+        self.table[slot, :] = self.scratch
+        self.used[slot] = 0
+        self._free_slots.append(slot)
+
+    def reserve(self, slot: int, tokens: int) -> tuple[int, int]:
+        """Pages for positions ``[0, tokens)`` of ``slot``; returns the table columns it filled."""
+
+        need = -(-tokens // BLOCK)
+        if need > self.width:
+            raise ValueError(f"sequence of {tokens} tokens exceeds the pool's {self.width * BLOCK} tokens per slot")
+        have = int(self.used[slot])
+        if need <= have:
+            return have, have
+        if need - have > len(self._free_pages):
+            raise RuntimeError("the page pool is out of shared-cache pages")
+        for j in range(have, need):
+            self.table[slot, j] = self._free_pages.pop()
+        self.used[slot] = need
+        return have, need
+
+
+class LastKVPagePool:
+    """One ``[pages, Hkv, 4096]`` K/V pool: shared last-layer pages (handed out per slot on demand)
+    and per-layer ring pages (fixed per slot), plus one scratch page that padded rows and unused
+    table entries name.  Device copies of the page tables sit beside the host bookkeeping."""
+
+    def __init__(self, *, num_layers: int, kv_heads: int, chunk_size: int, max_slots: int, source_pages: int,
+                 max_tokens_per_slot: int, device: torch.device | str):
+        if min(num_layers, kv_heads, chunk_size, max_slots, source_pages, max_tokens_per_slot) < 1:
+            raise ValueError("pool sizes must be positive")
+        self.num_layers, self.kv_heads, self.chunk_size, self.max_slots = num_layers, kv_heads, chunk_size, max_slots
+        self.device = torch.device(device)
+        self.ring_tokens = ops.ring_tokens_for_chunk(chunk_size)
+        self.ring_blocks = self.ring_tokens // BLOCK
+        self.src_width = -(-max_tokens_per_slot // BLOCK)
+        self.source_pages = source_pages
+        ring_pages = num_layers * max_slots * self.ring_blocks
+        self.scratch_page = source_pages + ring_pages
+        self.pool = ops.PagedKV.zeros(self.scratch_page + 1, kv_heads, self.device)
+        # ring pages: static table [L, slots, ring_blocks] behind the shared pages
+        ring = source_pages + np.arange(ring_pages, dtype=np.int64).reshape(num_layers, max_slots, self.ring_blocks)
+        self.ring_table = torch.from_numpy(ring.astype(np.int32)).to(self.device)
+        self.pages = PageAllocator(max_slots=max_slots, pages=source_pages, width=self.src_width, scratch=self.scratch_page)
+        self.src_table = torch.from_numpy(self.pages.table.copy()).to(self.device)
+
+    @property
+    def free_pages(self) -> int:
+        return self.pages.free_pages
+
+    def open_slot(self) -> int:
+        return self.pages.open_slot()
+
+    def close_slot(self, slot: int) -> None:
+        self.pages.close_slot(slot)
+        self.src_table[slot].fill_(self.scratch_page)
+
+    def reserve(self, slot: int, tokens: int) -> None:
+        """Give ``slot`` shared pages for positions ``[0, tokens)``."""
+
+        lo, hi = self.pages.reserve(slot, tokens)
+        if hi > lo:
+            self.src_table[slot, lo:hi].copy_(torch.from_numpy(self.pages.table[slot, lo:hi]))
+
+
+@dataclass
+class _Row:
+    slot: int
+    position: int  # first position of this step's tokens
+    tokens: int
+    older: int = 0  # older (shared) keys: rec = max(0, cur - C)
+    local: int = 0  # ring keys: positions [rec, position + tokens)
+
+
+class LastKVFastPath:
+    """Per-step prologue and per-layer op sequence of the serving path over a LastKVPagePool.
+
+    ``layer_params[l]`` = (q_norm_weight bf16 [128] or None, k_norm_weight or None, eps, vscale
+    fp32 [Hkv] or None); ``blend`` = (alpha, one_minus_alpha, vscale-or-None), fp32 ``[L * Hkv]``
+    as ``blend_chunk`` takes them; ``rotary(positions [B, n]) -> (cos, sin)`` bf16 ``[B, n, 128]``.
+    ``from_model`` takes all three from a ``lastkv_amd.llm`` model.  ``num_splits`` fixes the
+    decode split count (default: chosen per step from the longest row)."""
+
+    def __init__(self, pool: LastKVPagePool, *, num_q_heads: int, layer_params, blend, rotary, max_batch: int,
+                 num_splits: int | None = None):
+        self.pool = pool
+        self.num_q_heads = num_q_heads
+        self.layer_params = list(layer_params)
+        if len(self.layer_params) != pool.num_layers:
+            raise ValueError("one parameter tuple per layer is required")
+        if num_q_heads % pool.kv_heads:
+            raise ValueError("num_q_heads must be a multiple of the pool's kv heads")
+        self.blend = blend
+        self.rotary = rotary
+        self.max_batch = max_batch
+        self.num_splits = num_splits
+        dev = pool.device
+        self._seen = np.zeros(pool.max_slots, dtype=np.int64)
+        self._committed = np.zeros(pool.max_slots, dtype=np.int64)  # boundary blended through
+        self._open = np.zeros(pool.max_slots, dtype=bool)
+        i32 = dict(dtype=torch.int32, device=dev)
+        self._meta = torch.zeros((4, max_batch), **i32)  # positions, older_len, local_len, local_start
+        self._older_table = torch.full((max_batch, pool.src_width), pool.scratch_page, **i32)
+        self._ring_table = torch.full((pool.num_layers, max_batch, pool.ring_blocks), pool.scratch_page, **i32)
+        self._cos1 = torch.zeros((max_batch, 1, ops.HEAD_DIM), dtype=torch.bfloat16, device=dev)
+        self._sin1 = torch.zeros_like(self._cos1)
+        self._q_out = torch.empty((max_batch, num_q_heads, ops.HEAD_DIM), dtype=torch.bfloat16, device=dev)
+        self._decode_ws = torch.empty(16, dtype=torch.uint8, device=dev)
+        self._prefill_ws = torch.empty(16, dtype=torch.uint8, device=dev)
+        self.rows: list[_Row] = []
+        self.batch = 0  # rows of this step, padding included
+        self.tokens = 0  # query tokens of this step, padding included
+        self.splits = 1
+        self.uniform = True  # every row of this step has the same token count
+        self._row_rope: list[tuple[torch.Tensor, torch.Tensor]] = []
+        self._row_splits: list[int] = []
+
+    @classmethod
+    def from_model(cls, model, pool: LastKVPagePool, *, max_batch: int, num_splits: int | None = None) -> "LastKVFastPath":
+        """Parameters of a ``lastkv_amd.llm`` decoder: its layers' q/k norms, V scales and blend gates."""
+
+        inner = getattr(model, "model", model)
+        cfg = inner.config
+        params = []
+        for layer in inner.layers:
+            att = layer.self_attn
+            qn = att.q_norm.weight if cfg.use_qk_norm else None
+            kn = att.k_norm.weight if cfg.use_qk_norm else None
+            params.append((qn, kn, cfg.rms_norm_eps, att._older_vscale()))
+
+        def rotary(positions):
+            cos, sin = inner.rotary(positions, torch.bfloat16)
+            if cfg.use_nope:
+                return torch.ones_like(cos), torch.zeros_like(sin)
+            return cos, sin
+
+        return cls(pool, num_q_heads=cfg.num_attention_heads, layer_params=params, blend=inner._blend_params(),
+                   rotary=rotary, max_batch=max_batch, num_splits=num_splits)
+
+    # -------------------------------------------------------------- sequences
+    def add_sequence(self) -> int:
+        slot = self.pool.open_slot()
+        self._seen[slot] = self._committed[slot] = 0
+        self._open[slot] = True
+        return slot
+
+    def free_sequence(self, slot: int) -> None:
+        if not self._open[slot]:
+            raise ValueError(f"slot {slot} is not in use")
+        self._open[slot] = False
+        self.pool.close_slot(slot)
+
+    def seen(self, slot: int) -> int:
+        return int(self._seen[slot])
+
+    # -------------------------------------------------------------- host prologue
+    def prepare(self, rows: list[tuple[int, int]], pad_to: int | None = None) -> None:
+        """Stage one step: ``rows`` = (slot, new tokens) per sequence, in the order their tokens
+        appear in the step's q/k/v rows; each row continues its sequence at ``seen(slot)``.
+
+        Commits the previous chunk of every row that starts on a chunk boundary (blend of every
+        layer's ring with the shared pages, ``batching.py:1099-1155``; as in the reference it runs
+        at the first step after the boundary), hands out shared pages, and copies positions,
+        lengths, ring starts and table rows to device memory.  A row must not cross a chunk
+        boundary (split prompts at multiples of C).  ``pad_to`` pads a decode step with empty rows
+        that read and write only the scratch page."""
+
+        P = self.pool
+        C = P.chunk_size
+        if not rows:
+            raise ValueError("a step needs at least one row")
+        if len({r[0] for r in rows}) != len(rows):
+            raise ValueError("a slot appears twice in one step")
+        parsed = []
+        for slot, n in rows:
+            if not (0 <= slot < P.max_slots) or not self._open[slot]:
+                raise ValueError(f"slot {slot} is not in use")
+            p = int(self._seen[slot])
+            rec, local, _ = plan_row(p, n, C, P.ring_tokens)
+            parsed.append(_Row(slot, p, n, rec, local))
+        uniform = all(r.tokens == parsed[0].tokens for r in parsed)
+        B = len(parsed)
+        Bp = B if pad_to is None else max(B, int(pad_to))
+        if pad_to is not None and not (uniform and parsed[0].tokens == 1):
+            raise ValueError("pad_to applies to decode steps (one token per row)")
+        if Bp > self.max_batch:
+            raise ValueError(f"{Bp} rows exceed max_batch {self.max_batch}")
+        for r in parsed:
+            P.reserve(r.slot, r.position + r.tokens)
+        for r in parsed:
+            if r.position > 0 and r.position % C == 0 and self._committed[r.slot] < r.position:
+                self._commit(r.slot, r.position)
+        meta = np.zeros((4, Bp), dtype=np.int32)  # padded rows: position 0, no keys
+        for b, r in enumerate(parsed):
+            meta[:, b] = (r.position, r.older, r.local, r.older % P.ring_tokens)
+        # pageable host memory: the copy has read it when the call returns
+        self._meta[:, :Bp].copy_(torch.from_numpy(meta))
+        slots = torch.tensor([r.slot for r in parsed], dtype=torch.long).to(P.device)
+        self._older_table[:B].copy_(P.src_table.index_select(0, slots))
+        self._ring_table[:, :B].copy_(P.ring_table.index_select(1, slots))
+        if Bp > B:
+            self._older_table[B:Bp].fill_(P.scratch_page)
+            self._ring_table[:, B:Bp].fill_(P.scratch_page)
+        Hq = self.num_q_heads
+        self.tokens = sum(r.tokens for r in parsed) + (Bp - B)
+        if uniform and parsed[0].tokens == 1:
+            cos, sin = self.rotary(self._meta[0, :Bp].long()[:, None])
+            self._cos1[:Bp].copy_(cos)
+            self._sin1[:Bp].copy_(sin)
+            keys = max(r.older + r.local for r in parsed)
+            self.splits = self.num_splits or ops.default_decode_splits(Bp, P.kv_heads, keys, ops._cu_count(P.device))
+            need = ops.decode_workspace_bytes(Bp, Hq, self.splits)
+            if self._decode_ws.numel() < need:
+                self._decode_ws = torch.empty(need, dtype=torch.uint8, device=P.device)
+        else:
+            self._row_rope = []
+            if uniform:
+                n = parsed[0].tokens
+                pos = self._meta[0, :B].long()[:, None] + torch.arange(n, device=P.device)[None, :]
+                self._row_rope = [self.rotary(pos)]
+                # device-resident lengths: the kernel sizes its fp16 V copy by the older table's
+                # width and the whole ring
+                width = max(1, -(-max(r.older for r in parsed) // BLOCK))
+                need = ops.prefill_workspace_bytes(B, P.kv_heads, width * BLOCK, P.ring_tokens)
+            else:
+                cu = ops._cu_count(P.device)
+                self._row_splits = [self.num_splits or ops.default_decode_splits(1, P.kv_heads, r.older + r.local, cu)
+                                    for r in parsed]
+                for r in parsed:
+                    self._row_rope.append(self.rotary(torch.arange(r.position, r.position + r.tokens,
+                                                                   device=P.device)[None, :]))
+                need = max(ops.prefill_workspace_bytes(1, P.kv_heads, r.older, r.local) for r in parsed)
+                dneed = max(ops.decode_workspace_bytes(1, Hq, sp) for sp in self._row_splits)
+                if self._decode_ws.numel() < dneed:
+                    self._decode_ws = torch.empty(dneed, dtype=torch.uint8, device=P.device)
+            if self._prefill_ws.numel() < need:
+                self._prefill_ws = torch.empty(need, dtype=torch.uint8, device=P.device)
+        if self._q_out.shape[0] < self.tokens:
+            self._q_out = torch.empty((self.tokens, Hq, ops.HEAD_DIM), dtype=torch.bfloat16, device=P.device)
+        for r in parsed:
+            self._seen[r.slot] = r.position + r.tokens
+        self.rows, self.batch, self.uniform = parsed, Bp, uniform
+
+    def _commit(self, slot: int, boundary: int) -> None:
+        """Blend chunk [boundary - C, boundary) of every layer's ring of ``slot`` with its shared pages."""
+
+        P = self.pool
+        alpha, om, s = self.blend
+        ops.blend_chunk(P.pool.k, P.pool.v, P.pool, batch=1, chunk_start=boundary - P.chunk_size, chunk_len=P.chunk_size,
+                        alpha=alpha, one_minus_alpha=om, vscale=s, ring_table=P.ring_table[:, slot:slot + 1],
+                        ring_tokens=P.ring_tokens, deep_table=P.src_table[slot:slot + 1])
+        self._committed[slot] = boundary
+
+    # -------------------------------------------------------------- per-layer op sequence
+    def run_layer(self, layer_index: int, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                  output: torch.Tensor) -> torch.Tensor:
+        """``query`` ``[T, Hq * 128]`` (or ``[T, Hq, 128]``), ``key``/``value`` ``[T, Hkv * 128]``
+        (row views of a fused projection are fine): this step's projections, rows in ``prepare``
+        order.  Writes the attention output ``[T, Hq, 128]`` (contiguous) and returns it."""
+
+        P = self.pool
+        B, T = self.batch, self.tokens
+        Hq, Hkv = self.num_q_heads, P.kv_heads
+        if min(query.shape[0], key.shape[0], value.shape[0], output.shape[0]) < T:
+            raise ValueError(f"this step has {T} query tokens")
+        qn_w, kn_w, eps, vs = self.layer_params[layer_index]
+        top = layer_index == P.num_layers - 1
+        ring_tab = self._ring_table[layer_index]
+        pos, older_len, local_len, local_start = self._meta
+        n = self.rows[0].tokens
+        if self.uniform:  # every row has n tokens (padding only for n == 1)
+            cos, sin = (self._cos1[:B], self._sin1[:B]) if n == 1 else self._row_rope[0]
+            q_out = ops.qkv_epilogue(
+                query[:T].reshape(B, n, Hq * 128), key[:T].reshape(B, n, Hkv * 128), value[:T].reshape(B, n, Hkv * 128),
+                cos, sin, num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=qn_w, k_norm_weight=kn_w, eps=eps,
+                positions=pos[:B], ring=P.pool, ring_table=ring_tab[:B], ring_tokens=P.ring_tokens,
+                deep=P.pool if top else None, deep_table=self._older_table[:B] if top else None,
+                q_out=self._q_out[:T].view(B, n, Hq, 128))
+            seg = dict(older=P.pool, older_table=self._older_table[:B], older_len=older_len[:B], vscale=vs, local=P.pool,
+                       local_table=ring_tab[:B], local_ring_blocks=P.ring_blocks, local_len=local_len[:B],
+                       local_start=local_start[:B])
+            if n == 1:
+                ops.decode_attention(q_out.view(B, Hq, 128), out=output[:T].view(B, Hq, 128), num_splits=self.splits,
+                                     workspace=self._decode_ws, **seg)
+            else:
+                width = max(1, -(-max(r.older for r in self.rows) // BLOCK))
+                seg["older_table"] = self._older_table[:B, :width]
+                ops.prefill_attention(q_out, causal=True, out=output[:T].view(B, n, Hq, 128),
+                                      workspace=self._prefill_ws, **seg)
+            return output
+        start = 0
+        for b, r in enumerate(self.rows):
+            n = r.tokens
+            sl = slice(start, start + n)
+            cos, sin = self._row_rope[b]
+            q_out = ops.qkv_epilogue(
+                query[sl].reshape(1, n, Hq * 128), key[sl].reshape(1, n, Hkv * 128), value[sl].reshape(1, n, Hkv * 128),
+                cos, sin, num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=qn_w, k_norm_weight=kn_w, eps=eps,
+                positions=r.position, ring=P.pool, ring_table=ring_tab[b:b + 1], ring_tokens=P.ring_tokens,
+                deep=P.pool if top else None, deep_table=self._older_table[b:b + 1] if top else None,
+                q_out=self._q_out[sl].view(1, n, Hq, 128))
+            width = max(1, -(-r.older // BLOCK))
+            seg = dict(older=P.pool, older_table=self._older_table[b:b + 1, :width], older_len=r.older, vscale=vs,
+                       local=P.pool, local_table=ring_tab[b:b + 1], local_ring_blocks=P.ring_blocks, local_len=r.local,
+                       local_start=r.older % P.ring_tokens)
+            if n == 1:
+                ops.decode_attention(q_out.view(1, Hq, 128), out=output[sl].view(1, Hq, 128), num_splits=self._row_splits[b],
+                                     workspace=self._decode_ws, **seg)
+            else:
+                ops.prefill_attention(q_out, causal=True, out=output[sl].view(1, n, Hq, 128), workspace=self._prefill_ws,
+                                      **seg)
+            start += n
+        return output
+
+
+class LastKVServingModel:
+    """Continuous-batching runner of a ``lastkv_amd.llm`` causal LM over a LastKVFastPath: one
+    ``step`` runs the decoder over ragged rows (prefill pieces and decode tokens of different
+    sequences in one batch), the role of the reference's vLLM model class + backend forward
+    (``vllm_model.py``, ``vllm_backend.py:637-664``).  Projections, norms and MLP are the model's
+    own torch modules applied to the step's ``[T, hidden]`` rows."""
+
+    def __init__(self, model, *, max_batch: int, max_tokens_per_slot: int, source_pages: int | None = None,
+                 num_splits: int | None = None, device=None):
+        self.model = model
+        inner = model.model
+        cfg = inner.config
+        if cfg.head_dim != ops.HEAD_DIM:
+            raise ValueError(f"the MI355X kernels support head_dim {ops.HEAD_DIM}")
+        device = device or next(model.parameters()).device
+        per_slot = -(-max_tokens_per_slot // BLOCK)
+        self.pool = LastKVPagePool(num_layers=cfg.num_hidden_layers, kv_heads=cfg.num_key_value_heads,
+                                   chunk_size=cfg.chunk_size, max_slots=max_batch,
+                                   source_pages=source_pages or max_batch * per_slot,
+                                   max_tokens_per_slot=max_tokens_per_slot, device=device)
+        self.fast = LastKVFastPath.from_model(model, self.pool, max_batch=max_batch, num_splits=num_splits)
+        self.config = cfg
+
+    def add_sequence(self) -> int:
+        return self.fast.add_sequence()
+
+    def free_sequence(self, slot: int) -> None:
+        self.fast.free_sequence(slot)
+
+    @torch.no_grad()
+    def step(self, rows: list[tuple[int, torch.Tensor]], pad_to: int | None = None) -> torch.Tensor:
+        """``rows`` = (slot, new token ids [n]); returns the logits of each row's last token ``[B, vocab]``."""
+
+        cfg, inner = self.config, self.model.model
+        self.fast.prepare([(slot, int(ids.numel())) for slot, ids in rows], pad_to=pad_to)
+        T = self.fast.tokens
+        ids = torch.cat([ids.reshape(-1).to(self.pool.device) for _, ids in rows])
+        if T > ids.numel():
+            ids = torch.cat([ids, ids.new_zeros(T - ids.numel())])
+        hidden = inner.embed_tokens(ids)
+        Hq = cfg.num_attention_heads
+        out = torch.empty((T, Hq, ops.HEAD_DIM), dtype=hidden.dtype, device=hidden.device)
+        for i, layer in enumerate(inner.layers):
+            att = layer.self_attn
+            h = layer.input_layernorm(hidden)
+            self.fast.run_layer(i, att.q_proj(h), att.k_proj(h), att.v_proj(h), out)
+            hidden = hidden + att.o_proj(out.view(T, Hq * ops.HEAD_DIM))
+            hidden = hidden + layer.mlp(layer.post_attention_layernorm(hidden))
+        last = torch.tensor(np.cumsum([int(ids.numel()) for _, ids in rows]) - 1, device=hidden.device)
+        return self.model.lm_head(inner.norm(hidden.index_select(0, last)))
+
+    @torch.no_grad()
+    def generate(self, prompts: list[torch.Tensor], max_new_tokens: int, *, prefill_chunk: int | None = None
+                 ) -> list[torch.Tensor]:
+        """Greedy continuous batching: every step carries each unfinished sequence's next prompt
+        piece (cut at chunk boundaries and at ``prefill_chunk``) or its last generated token.
+        Returns each prompt followed by its ``max_new_tokens`` generated ids."""
+
+        C = self.config.chunk_size
+        slots = [self.add_sequence() for _ in prompts]
+        fed = [0] * len(prompts)  # prompt tokens fed so far
+        gen: list[list[int]] = [[] for _ in prompts]
+        try:
+            while any(len(g) < max_new_tokens for g in gen):
+                rows, owners = [], []
+                for i, (slot, prompt) in enumerate(zip(slots, prompts)):
+                    if len(gen[i]) >= max_new_tokens:
+                        continue
+                    flat = prompt.reshape(-1)
+                    if fed[i] < flat.numel():
+                        p = self.fast.seen(slot)
+                        take = min(flat.numel() - fed[i], C - p % C, prefill_chunk or flat.numel())
+                        rows.append((slot, flat[fed[i]:fed[i] + take]))
+                        fed[i] += take
+                    else:
+                        rows.append((slot, torch.tensor([gen[i][-1]], dtype=flat.dtype)))
+                    owners.append(i)
+                tokens = self.step(rows).argmax(-1).tolist()
+                for i, tok in zip(owners, tokens):
+                    if fed[i] >= prompts[i].numel():
+                        gen[i].append(int(tok))
+        finally:
+            for slot in slots:
+                self.free_sequence(slot)
+        return [torch.cat([p.reshape(-1).cpu(), torch.tensor(g, dtype=p.dtype)]) for p, g in zip(prompts, gen)]

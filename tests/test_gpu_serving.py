@@ -1,0 +1,164 @@
+"""GPU parity of the serving fast path (lastkv_amd.serving) over one paged pool.
+
+1. ``run_layer`` against a contiguous twin: per sequence a LastKVCache driven by the same C-ABI
+   calls the drop-in attention makes (contiguous ring + shared store, boundary blend right at the
+   boundary).  The same arithmetic runs in the same order on both sides, so with one decode split
+   the outputs of every layer at every step are bit-identical, over ragged steps (prompt pieces of
+   different lengths in one step, uniform prefill steps, padded decode steps) that cross several
+   chunk boundaries with a chunk size that straddles page boundaries.
+2. ``LastKVServingModel`` (ragged continuous batching through the tiny model) against the oracle
+   model run per sequence, with the noise-floor criterion of the drop-in model's tests: no further
+   from the fp32-attention oracle than the reference's own bf16 path is.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from lastkv_amd import ops
+from lastkv_amd.llm import LastKVCache
+from lastkv_amd.serving import LastKVFastPath, LastKVPagePool, LastKVServingModel
+
+from test_gpu_llm import _no_worse_than_reference_bf16, _o16, _o32, _tiny
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rotary(positions: torch.Tensor):
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 128, 2, device=positions.device).float() / 128))
+    f = positions[..., None].float() * inv
+    emb = torch.cat((f, f), -1)
+    return emb.cos().bfloat16(), emb.sin().bfloat16()
+
+
+class _Twin:
+    """One sequence on contiguous buffers, called exactly as LastKVAttention.forward calls the kernels."""
+
+    def __init__(self, layers, Hkv, C, cap, params, blend):
+        self.cache = LastKVCache(layers, C, capacity_tokens=cap)
+        self.cache.reserve(1, Hkv, torch.device(DEV), cap)
+        self.params, self.blend, self.C, self.layers = params, blend, C, layers
+
+    def layer(self, l, q, k, v, Hq, Hkv):
+        c, C = self.cache, self.C
+        n = q.shape[0]
+        p0 = c.seen_tokens
+        qn_w, kn_w, eps, vs = self.params[l]
+        cos, sin = _rotary(torch.arange(p0, p0 + n, device=DEV)[None, :])
+        ring = c.ring(l)
+        qn = ops.qkv_epilogue(q.reshape(1, n, -1), k.reshape(1, n, -1), v.reshape(1, n, -1), cos, sin, num_q_heads=Hq,
+                              num_kv_heads=Hkv, q_norm_weight=qn_w, k_norm_weight=kn_w, eps=eps, positions=p0,
+                              ring=ring, deep=c.store if l == self.layers - 1 else None)
+        rec = max(0, (p0 + n - 1) // C * C - C)
+        seg = dict(older=c.store, older_len=rec, vscale=vs, local=ring, local_len=p0 + n - rec,
+                   local_start=rec % c.ring_tokens)
+        if n == 1:
+            return ops.decode_attention(qn.view(1, Hq, 128), num_splits=1, **seg).view(1, Hq, 128)
+        return ops.prefill_attention(qn, causal=True, **seg).view(n, Hq, 128)
+
+    def advance(self, n):
+        c = self.cache
+        c.seen_tokens += n
+        if c.seen_tokens % self.C == 0:
+            alpha, om, s = self.blend
+            ops.blend_chunk(c.ring_k, c.ring_v, c.store, batch=1, chunk_start=c.seen_tokens - self.C, chunk_len=self.C,
+                            alpha=alpha, one_minus_alpha=om, vscale=s)
+
+
+def test_run_layer_bit_exact_vs_contiguous_twin():
+    g = torch.Generator(device=DEV).manual_seed(5)
+    layers, Hq, Hkv, C, cap = 3, 8, 2, 48, 640
+    params = []
+    for l in range(layers):
+        w = (torch.rand(128, generator=g, device=DEV) + 0.5).bfloat16()
+        vs = (torch.rand(Hkv, generator=g, device=DEV) + 0.4).bfloat16().float()
+        params.append((w, w.flip(0).contiguous(), 1e-5, vs))
+    alpha = torch.rand(layers * Hkv, generator=g, device=DEV).bfloat16().float()
+    blend = (alpha, (1 - alpha).bfloat16().float(), torch.cat([p[3] for p in params]))
+    pool = LastKVPagePool(num_layers=layers, kv_heads=Hkv, chunk_size=C, max_slots=4, source_pages=64,
+                          max_tokens_per_slot=cap, device=DEV)
+    fast = LastKVFastPath(pool, num_q_heads=Hq, layer_params=params, blend=blend, rotary=_rotary, max_batch=6,
+                          num_splits=1)
+    slots = [fast.add_sequence() for _ in range(3)]
+    twins = [_Twin(layers, Hkv, C, cap, params, blend) for _ in slots]
+    # (rows of (sequence, tokens), pad_to)
+    schedule = [([(0, 48), (1, 20), (2, 5)], None), ([(1, 28), (0, 48), (2, 43)], None),
+                ([(0, 48), (1, 48), (2, 48)], None), ([(2, 30), (0, 1)], None)]
+    schedule += [([(0, 1), (1, 1)], 4)] * 3 + [([(0, 1), (1, 1), (2, 1)], None)] * 2
+    schedule += [([(2, 16)], None), ([(0, 2), (1, 1), (2, 3)], None)] + [([(1, 1), (2, 1), (0, 1)], 5 if i % 2 else None) for i in range(60)]
+    for step, (rows, pad) in enumerate(schedule):
+        fast.prepare([(slots[i], n) for i, n in rows], pad_to=pad)
+        T = fast.tokens
+        q = torch.randn((T, Hq * 128), generator=g, device=DEV).bfloat16()
+        k = torch.randn((T, Hkv * 128), generator=g, device=DEV).bfloat16()
+        v = torch.randn((T, Hkv * 128), generator=g, device=DEV).bfloat16()
+        for l in range(layers):
+            out = torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=DEV)
+            fast.run_layer(l, q, k, v, out)
+            start = 0
+            for i, n in rows:
+                sl = slice(start, start + n)
+                want = twins[i].layer(l, q[sl], k[sl], v[sl], Hq, Hkv)
+                assert torch.equal(out[sl], want), f"step {step} layer {l} sequence {i}"
+                start += n
+        for i, n in rows:
+            twins[i].advance(n)
+            assert fast.seen(slots[i]) == twins[i].cache.seen_tokens
+    print(f"{len(schedule)} steps, final lengths {[fast.seen(s) for s in slots]}", flush=True)
+    for s in slots:
+        fast.free_sequence(s)
+    assert pool.free_pages == 64
+
+
+def test_serving_model_ragged_batches_match_oracle():
+    oracle, ours = _tiny(chunk=8)
+    lengths = [37, 22, 50]
+    gen = torch.Generator().manual_seed(8)
+    seqs = [torch.randint(3, 97, (n,), generator=gen).to(DEV) for n in lengths]
+    runner = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=64)
+    slots = [runner.add_sequence() for _ in seqs]
+    fed = [0] * len(seqs)
+    got = [[] for _ in seqs]  # (position of the row's last token, logits)
+    pieces = [5, 3, 8, 1, 8, 2, 7]
+    step = 0
+    with torch.inference_mode():
+        while any(f < len(s) for f, s in zip(fed, seqs)):
+            rows, owners = [], []
+            for i, s in enumerate(seqs):
+                if fed[i] >= len(s):
+                    continue
+                p = runner.fast.seen(slots[i])
+                take = min(len(s) - fed[i], 8 - p % 8, pieces[(step + i) % len(pieces)] if fed[i] < 24 else 1)
+                rows.append((slots[i], s[fed[i]:fed[i] + take]))
+                owners.append((i, fed[i] + take - 1))
+                fed[i] += take
+            logits = runner.step(rows)
+            for (i, pos), row in zip(owners, logits):
+                got[i].append((pos, row.float()))
+            step += 1
+        for i, s in enumerate(seqs):
+            want, _ = _o32(oracle)(s[None])
+            ref16, _ = _o16(oracle)(s[None])
+            pos = [p for p, _ in got[i]]
+            mine = torch.stack([r for _, r in got[i]])[None]
+            _no_worse_than_reference_bf16(mine, want[:, pos].float(), ref16[:, pos].float(),
+                                          f"serving sequence {i} ({len(pos)} steps)")
+    print(f"{step} ragged steps", flush=True)
+
+
+def test_serving_generate_runs_and_frees_pages():
+    _, ours = _tiny(chunk=8)
+    runner = LastKVServingModel(ours, max_batch=3, max_tokens_per_slot=96)
+    total = runner.pool.free_pages
+    prompts = [torch.tensor([1, 5, 17, 33, 2, 9], device=DEV), torch.arange(3, 30, device=DEV)]
+    with torch.inference_mode():
+        out = runner.generate(prompts, 12, prefill_chunk=5)
+        again = runner.generate(prompts, 12, prefill_chunk=5)  # reused slots and pages, same ids
+    for a, b, p in zip(out, again, prompts):
+        assert a.shape[0] == p.numel() + 12
+        assert torch.equal(a[: p.numel()], p.cpu())
+        assert torch.equal(a, b)
+    assert runner.pool.free_pages == total
