@@ -394,6 +394,49 @@ typedef struct lkv_merge_args {
 
 int32_t lkv_merge_states(const lkv_merge_args *args, lkv_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Append K and V rows into pages of a tiled pool.
+ *
+ * Replaces the cache writes of:
+ *   - the Wan model's cache append (videogen/src/lastkv/videogen/cache.py:33-50 append_shared,
+ *     model.py:621-645 _append_current_history, model.py:67-84 append_to_cache);
+ *   - vLLM's reshape_and_cache_flash into the fast path's ring / source pages
+ *     (vllm/src/lastkv/vllm/backends/rmarin_flashinfer/fastpath.py:659-663).
+ * Token t of sequence b (k / v rows at b * stride_b + t * stride_t + h * stride_h, 128 bf16
+ * each, 16-byte aligned) goes to absolute position p = token0 + t; with wrap_tokens > 0 (a ring,
+ * a multiple of 32) the cache position is p mod wrap_tokens, else p.  Cache position c of
+ * sequence b lives in page block_table[b * table_stride + c / 32] (ids clamped to the pool)
+ * at offset c mod 32 of the tiled block of head h.  Requires token0 + tokens <= 32 * table_width
+ * without wrap, tokens <= wrap_tokens <= 32 * table_width with it.
+ * ------------------------------------------------------------------------------------- */
+typedef struct lkv_append_args {
+  int32_t struct_size; /* sizeof(lkv_append_args) */
+  int32_t batch;
+  int32_t tokens;
+  int32_t heads;
+  int32_t head_dim; /* 128 */
+  int32_t token0;
+  int32_t wrap_tokens;
+  const void *k; /* bf16 */
+  int64_t k_stride_b;
+  int64_t k_stride_t;
+  int64_t k_stride_h;
+  const void *v; /* bf16 */
+  int64_t v_stride_b;
+  int64_t v_stride_t;
+  int64_t v_stride_h;
+  void *pool_k; /* [pages, heads, 4096] bf16 */
+  void *pool_v;
+  int64_t page_stride;
+  int64_t head_stride;
+  int32_t num_pages;
+  const int32_t *block_table;
+  int64_t table_stride;
+  int32_t table_width;
+} lkv_append_args;
+
+int32_t lkv_append_paged(const lkv_append_args *args, lkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

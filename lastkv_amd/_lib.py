@@ -129,6 +129,36 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
+class AppendArgs(ctypes.Structure):
+    """Mirror of ``lkv_append_args``."""
+
+    _fields_ = [
+        ("struct_size", c_i32),
+        ("batch", c_i32),
+        ("tokens", c_i32),
+        ("heads", c_i32),
+        ("head_dim", c_i32),
+        ("token0", c_i32),
+        ("wrap_tokens", c_i32),
+        ("k", c_ptr),
+        ("k_stride_b", c_i64),
+        ("k_stride_t", c_i64),
+        ("k_stride_h", c_i64),
+        ("v", c_ptr),
+        ("v_stride_b", c_i64),
+        ("v_stride_t", c_i64),
+        ("v_stride_h", c_i64),
+        ("pool_k", c_ptr),
+        ("pool_v", c_ptr),
+        ("page_stride", c_i64),
+        ("head_stride", c_i64),
+        ("num_pages", c_i32),
+        ("block_table", c_ptr),
+        ("table_stride", c_i64),
+        ("table_width", c_i32),
+    ]
+
+
 class MergeArgs(ctypes.Structure):
     """Mirror of ``lkv_merge_args``."""
 
@@ -268,6 +298,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lkv_prefill_workspace_bytes": (c_i64, [ctypes.POINTER(PrefillArgs)]),
     "lkv_prefill_attn": (c_i32, [ctypes.POINTER(PrefillArgs), c_ptr]),
     "lkv_merge_states": (c_i32, [ctypes.POINTER(MergeArgs), c_ptr]),
+    "lkv_append_paged": (c_i32, [ctypes.POINTER(AppendArgs), c_ptr]),
     "lkv_qkv_epilogue": (c_i32, [ctypes.POINTER(QkvArgs), c_ptr]),
     "lkv_blend_chunk": (c_i32, [ctypes.POINTER(BlendArgs), c_ptr]),
 }

@@ -107,3 +107,137 @@ extern "C" int32_t lkv_cache_unpack(const void* src, int64_t src_seq_stride, int
       heads, tokens, kind);
   return check_launch("lkv_cache_unpack");
 }
+
+// ---------------------------------------------------------------------------------------------
+// Paged append: K/V rows -> pool pages.  One thread moves one (sequence, head, 8-token group,
+// 8-dim group): eight 16-byte K stores, and for V an 8x8 register transpose so that each of the
+// eight dims is one 16-byte store of 8 consecutive tokens (V tiles are dim-major).  Groups are
+// 8-aligned in absolute positions; a ring wrap (a multiple of 32 tokens) keeps that alignment.
+namespace lkv {
+namespace {
+
+struct AppendParams {
+  const uint16_t* k;
+  int64_t ksb, kst, ksh;
+  const uint16_t* v;
+  int64_t vsb, vst, vsh;
+  uint16_t* pk;
+  uint16_t* pv;
+  int64_t page_stride, head_stride;
+  const int32_t* table;
+  int64_t table_stride;
+  int32_t num_pages, token0, tokens, wrap, heads, groups;
+};
+
+__global__ __launch_bounds__(256) void append_paged_kernel(const AppendParams p, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int d8 = static_cast<int>(i & 15);
+  int64_t rest = i >> 4;
+  const int g = static_cast<int>(rest % p.groups);
+  rest /= p.groups;
+  const int h = static_cast<int>(rest % p.heads);
+  const int b = static_cast<int>(rest / p.heads);
+  const int a0 = ((p.token0 >> 3) + g) * 8;  // absolute position of the group's first token
+  const int c0 = p.wrap > 0 ? a0 % p.wrap : a0;
+  int page = p.table[b * p.table_stride + (c0 >> 5)];
+  page = page < 0 ? 0 : (page >= p.num_pages ? p.num_pages - 1 : page);
+  const int64_t base = page * p.page_stride + h * p.head_stride;
+  const int w0 = c0 & 31;
+  uint16_t vt[8][8];  // [token j][dim e]
+  bool all = true;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int t = a0 + j - p.token0;
+    const bool ok = t >= 0 && t < p.tokens;
+    all = all && ok;
+    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+    if (ok) {
+      kv = *reinterpret_cast<const uint4*>(p.k + b * p.ksb + t * p.kst + h * p.ksh + d8 * 8);
+      vv = *reinterpret_cast<const uint4*>(p.v + b * p.vsb + t * p.vst + h * p.vsh + d8 * 8);
+      *reinterpret_cast<uint4*>(p.pk + base + k_tile_offset(w0 + j, d8 * 8)) = kv;
+    }
+    const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vt[j][2 * e] = static_cast<uint16_t>(w[e] & 0xffffu);
+      vt[j][2 * e + 1] = static_cast<uint16_t>(w[e] >> 16);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    uint16_t* dst = p.pv + base + v_tile_offset(w0, d8 * 8 + e);
+    if (all) {
+      uint4 o;
+      o.x = vt[0][e] | (static_cast<uint32_t>(vt[1][e]) << 16);
+      o.y = vt[2][e] | (static_cast<uint32_t>(vt[3][e]) << 16);
+      o.z = vt[4][e] | (static_cast<uint32_t>(vt[5][e]) << 16);
+      o.w = vt[6][e] | (static_cast<uint32_t>(vt[7][e]) << 16);
+      *reinterpret_cast<uint4*>(dst) = o;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = a0 + j - p.token0;
+        if (t >= 0 && t < p.tokens) dst[j] = vt[j][e];
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace lkv
+
+extern "C" int32_t lkv_append_paged(const lkv_append_args* a, lkv_stream_t stream) {
+  using namespace lkv;
+  LKV_REQUIRE(a != nullptr, "null args");
+  LKV_REQUIRE(a->struct_size == static_cast<int32_t>(sizeof(lkv_append_args)),
+              "lkv_append_args size mismatch (caller %d, library %d)", a->struct_size,
+              static_cast<int32_t>(sizeof(lkv_append_args)));
+  LKV_REQUIRE(a->head_dim == kHeadDim, "head_dim must be 128, got %d", a->head_dim);
+  LKV_REQUIRE(a->batch >= 0 && a->heads > 0 && a->tokens >= 0 && a->token0 >= 0, "bad sizes");
+  LKV_REQUIRE(a->k && a->v && a->pool_k && a->pool_v && a->block_table, "null tensor");
+  LKV_REQUIRE(a->num_pages > 0 && a->table_width > 0, "empty pool or table");
+  LKV_REQUIRE(a->wrap_tokens >= 0 && a->wrap_tokens % kBlockTokens == 0, "wrap_tokens must be a multiple of 32");
+  const int64_t cap = static_cast<int64_t>(a->table_width) * kBlockTokens;
+  if (a->wrap_tokens > 0) {
+    LKV_REQUIRE(a->tokens <= a->wrap_tokens && a->wrap_tokens <= cap,
+                "a ring append needs tokens (%d) <= wrap_tokens (%d) <= 32 * table_width (%lld)", a->tokens,
+                a->wrap_tokens, static_cast<long long>(cap));
+  } else {
+    LKV_REQUIRE(static_cast<int64_t>(a->token0) + a->tokens <= cap, "positions [%d, %d) exceed the table (%lld tokens)",
+                a->token0, a->token0 + a->tokens, static_cast<long long>(cap));
+  }
+  const uintptr_t align = reinterpret_cast<uintptr_t>(a->k) | reinterpret_cast<uintptr_t>(a->v) |
+                          reinterpret_cast<uintptr_t>(a->pool_k) | reinterpret_cast<uintptr_t>(a->pool_v);
+  LKV_REQUIRE((align & 15) == 0, "tensors must be 16-byte aligned");
+  LKV_REQUIRE(((a->k_stride_b | a->k_stride_t | a->k_stride_h | a->v_stride_b | a->v_stride_t | a->v_stride_h |
+                a->page_stride | a->head_stride) & 7) == 0,
+              "strides must be multiples of 8 elements");
+  if (a->batch == 0 || a->tokens == 0) return LKV_OK;
+  AppendParams p;
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.ksb = a->k_stride_b;
+  p.kst = a->k_stride_t;
+  p.ksh = a->k_stride_h;
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.vsb = a->v_stride_b;
+  p.vst = a->v_stride_t;
+  p.vsh = a->v_stride_h;
+  p.pk = static_cast<uint16_t*>(a->pool_k);
+  p.pv = static_cast<uint16_t*>(a->pool_v);
+  p.page_stride = a->page_stride;
+  p.head_stride = a->head_stride;
+  p.table = a->block_table;
+  p.table_stride = a->table_stride;
+  p.num_pages = a->num_pages;
+  p.token0 = a->token0;
+  p.tokens = a->tokens;
+  p.wrap = a->wrap_tokens;
+  p.heads = a->heads;
+  p.groups = ((a->token0 + a->tokens + 7) >> 3) - (a->token0 >> 3);
+  const int64_t total = static_cast<int64_t>(a->batch) * a->heads * p.groups * 16;
+  const int64_t blocks = (total + 255) / 256;
+  LKV_REQUIRE(blocks < (1LL << 31), "too many elements");
+  append_paged_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, 0, as_stream(stream)>>>(p, total);
+  return check_launch("lkv_append_paged");
+}

@@ -675,6 +675,30 @@ def blend_chunk(
     _lib.check(_lib.load().lkv_blend_chunk(ctypes.byref(a), _stream(device)), "lkv_blend_chunk")
 
 
+def append_paged(k: torch.Tensor, v: torch.Tensor, pool: PagedKV, table: torch.Tensor, *, token0: int,
+                 wrap_tokens: int = 0) -> None:
+    """Write ``k``/``v`` ``[B, T, H, 128]`` (any batch/token/head strides, unit dim stride) to
+    absolute positions ``[token0, token0 + T)`` of each sequence's pages: position p lands at
+    cache position ``p mod wrap_tokens`` (a ring) or ``p``, in page ``table[b, c // 32]``."""
+
+    for name, t in (("k", k), ("v", v)):
+        _require_bf16_cuda(name, t)
+        _require(t.dim() == 4 and t.shape[-1] == HEAD_DIM and t.stride(-1) == 1, f"{name} must be [B, T, H, 128]")
+    _require(k.shape == v.shape, "k and v shapes differ")
+    B, T, H, _ = k.shape
+    _require(H == pool.heads, "k/v heads differ from the pool's")
+    _table_arg(table, B, "append", pool.device)
+    a = _lib.AppendArgs()
+    a.struct_size = ctypes.sizeof(_lib.AppendArgs)
+    a.batch, a.tokens, a.heads, a.head_dim, a.token0, a.wrap_tokens = B, T, H, HEAD_DIM, int(token0), int(wrap_tokens)
+    a.k, a.k_stride_b, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1), k.stride(2)
+    a.v, a.v_stride_b, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1), v.stride(2)
+    a.pool_k, a.pool_v = pool.k.data_ptr(), pool.v.data_ptr()
+    a.page_stride, a.head_stride, a.num_pages = pool.page_stride, pool.head_stride, pool.pages
+    a.block_table, a.table_stride, a.table_width = table.data_ptr(), table.stride(0), int(table.shape[1])
+    _lib.check(_lib.load().lkv_append_paged(ctypes.byref(a), _stream(pool.device)), "lkv_append_paged")
+
+
 def ring_tokens_for_chunk(chunk: int) -> int:
     """Ring capacity of one layer: the two live chunks, rounded up to whole 32-token blocks, plus
     one spare block when chunks straddle block boundaries (so no two blocks of one chunk share a

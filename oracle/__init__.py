@@ -13,6 +13,8 @@ Modules:
   layout          -- the tiled cache layout as closed-form index maps (pack / unpack)
   model           -- the LastKV decoder restated in torch (modeling.py) plus the independent
                      eager transcription of the reference's own test (test_llm_inference.py:39-93)
+  wan             -- the Wan video model's shared-history cache, previous-block blend and
+                     bidirectional block attention (videogen/.../cache.py, model.py:153-272)
 
 Each function cites the reference file:line it restates; how each is pinned is stated in the
 function's docstring ("pinned by: ...").
