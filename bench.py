@@ -20,6 +20,12 @@ Printed JSON line (one, from this single process):
                  query tokens against [older shared | recent blended | current causal]);
                  algorithmic FLOPs 4*128*Hq*B*sum(unmasked pairs) over the kernel time, against
                  the 2.5 PFLOP/s dense bf16 peak
+  configs        the other BASELINE configs, measured in the same run:
+                 config4_decode_128k  lkv_decode_attn at B=4, 131072-token context (split-K), GB/s
+                 config5_wan          Wan-1.3B block attention over its full history structure,
+                                      30 layers, MFMA %
+                 config3_e2e_8b       the 8B-shape drop-in model: chunked prefill of 32 x 8192
+                                      tokens, then greedy decode steps, tok/s of each
 """
 
 from __future__ import annotations
@@ -55,6 +61,9 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sweep-splits", action="store_true", help="print the kernel time for several split counts")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA measurement")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the config 4 (128K decode), config 5 (Wan) and config 3 (8B end to end) measurements")
+    ap.add_argument("--decode-steps", type=int, default=256, help="greedy decode steps of the config 3 model run")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device copy (reference kernel for HBM byte counters)")
     return ap.parse_args()
@@ -96,6 +105,149 @@ def prefill_measurement(ops, torch, cache, dev, reps: int = 3) -> dict:
         "workload": "config 3 prefill attention, one layer: 8 x 1024-token chunk pieces, B=32, 8K context",
         "flops_per_layer": flops, "ms_per_layer": round(ms, 3), "achieved_tflops": round(tflops, 1),
         "peak_tflops": MFMA_PEAK_TFLOPS, "mfma_pct": round(100 * tflops / MFMA_PEAK_TFLOPS, 2),
+    }
+
+
+def decode_long_measurement(ops, torch, dev, layers: int = 32) -> dict:
+    """BASELINE config 4's decode attention: B=4 sequences at position 131072 (the first decode
+    step after a 131072-token prompt at C = 1024): older = 130048 shared tokens, local = the
+    blended previous chunk + the new token (1025 ring tokens); 32 layer-calls with distinct q over
+    the same 2 GiB shared cache, split-K over the context (only 32 (sequence, kv head) pairs)."""
+
+    Bl, Tl, C = 4, 131072, CHUNK
+    cur, rec = Tl, Tl - C
+    local_len = Tl + 1 - rec
+    R = ops.ring_tokens_for_chunk(C)
+    g = torch.Generator(device=dev).manual_seed(4)
+    store = ops.TiledKV(torch.randn((Bl, HKV, Tl // 32, 4096), generator=g, device=dev).bfloat16(),
+                        torch.randn((Bl, HKV, Tl // 32, 4096), generator=g, device=dev).bfloat16())
+    ring = ops.TiledKV(torch.randn((Bl, HKV, R // 32, 4096), generator=g, device=dev).bfloat16(),
+                       torch.randn((Bl, HKV, R // 32, 4096), generator=g, device=dev).bfloat16())
+    qs = torch.randn((layers, Bl, HQ, D), generator=g, device=dev).bfloat16()
+    outs = torch.empty_like(qs)
+    vscale = torch.full((HKV,), 0.5, device=dev)
+    splits = ops.default_decode_splits(Bl, HKV, rec + local_len, torch.cuda.get_device_properties(dev).multi_processor_count)
+    ws = torch.empty(max(16, ops.decode_workspace_bytes(Bl, HQ, splits)), dtype=torch.uint8, device=dev)
+    kw = dict(older=store, older_len=rec, vscale=vscale, local=ring, local_len=local_len, local_start=rec % R,
+              num_splits=splits, workspace=ws)
+    for l in range(layers):
+        ops.decode_attention(qs[l], out=outs[l], **kw)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(layers)]
+    torch.cuda.synchronize()
+    for l in range(layers):
+        ev[l][0].record()
+        ops.decode_attention(qs[l], out=outs[l], **kw)
+        ev[l][1].record()
+    torch.cuda.synchronize()
+    us = statistics.mean(e[0].elapsed_time(e[1]) for e in ev) * 1e3
+    nbytes = 2 * Bl * HKV * (rec + local_len) * D * 2 + 2 * Bl * HQ * D * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del store, ring
+    return {
+        "workload": "config 4 decode attention: B=4, position 131072, older 130048 shared + 1025 ring tokens, C=1024",
+        "bytes_per_call": nbytes, "num_splits": splits, "kernel_us_per_call": round(us, 2),
+        "attn_hbm_gbps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "attn_step_tok_s": round(Bl / (us * layers * 1e-6), 1),
+    }
+
+
+def wan_measurement(ops, torch, dev) -> dict:
+    """the Wan-1.3B block attention of the 8th 4680-token block (3 latent frames
+    x 1560 tokens), 12 heads (MHA), over the full history structure of the reference
+    (videogen/.../model.py:153-272): per-layer 1560-token prefix, shared final-layer K/V, the
+    blended previous block and the bidirectional current block = 37440 keys per query.  One
+    forward's 30 layers, each a lkv_prefill_attn call (causal = 0) plus its block append."""
+
+    from lastkv_amd.videogen import WanKVCache
+
+    layers, H, S, nblk, keep = 30, 12, 4680, 8, 1560
+    cache = WanKVCache(num_layers=layers, num_heads=H, block_tokens=S, total_tokens=nblk * S, keep_tokens=keep,
+                       device=dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    cache.set_alphas(torch.randn((layers, H), generator=g, device=dev))
+    rnd = lambda: torch.randn((1, S, H, D), generator=g, device=dev).bfloat16()
+    kvs = [(rnd(), rnd()) for _ in range(layers)]
+    for blk in range(nblk - 1):  # the history: 7 committed blocks (the same K/V each time)
+        cache.commit(blk * S, kvs)
+    q, k, v = rnd(), rnd(), rnd()
+    out = torch.empty_like(q)
+    start = (nblk - 1) * S
+    for l in range(layers):  # warm-up
+        cache.attention(l, q, k, v, start, out=out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for l in range(layers):
+        cache.attention(l, q, k, v, start, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    keys = nblk * S
+    flops = 4 * H * D * S * keys * layers
+    tflops = flops / (ms * 1e-3) / 1e12
+    del cache, kvs
+    return {
+        "workload": "config 5 Wan-1.3B block 8: q 4680 x 12 heads over 37440 keys (prefix | shared | blended | "
+                    "bidirectional current), 30 layers",
+        "flops_per_forward": flops, "ms_per_forward": round(ms, 3), "achieved_tflops": round(tflops, 1),
+        "mfma_pct": round(100 * tflops / MFMA_PEAK_TFLOPS, 2),
+    }
+
+
+def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
+    """BASELINE config 3 end to end through the drop-in model (lastkv_amd.llm): 8B geometry
+    (32 layers, 4096, 32 / 8 heads, FFN 14336, vocab 128256, llama3 RoPE theta 500000), random
+    N(0, 0.02) bf16 weights, B = 32, an 8192-token uniform-random prompt prefilled in 2048-token
+    calls (C = 1024), then greedy decode steps feeding one new token per sequence.  Eager PyTorch
+    host loop; projections / MLP / norms / lm_head are torch (hipBLASLt) ops, attention and cache
+    writes are this library's kernels."""
+
+    from lastkv_amd.llm import CustomRecurrentMarinAKV254ReuseKVForCausalLM, LastKVCache, LastKVConfig
+
+    Bm, prompt, call = 32, 8192, 2048
+    cfg = LastKVConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                       num_attention_heads=32, num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-5,
+                       rope_theta=500000.0, max_position_embeddings=131072, chunk_size=CHUNK,
+                       rope_scaling={"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+                                     "high_freq_factor": 4.0, "original_max_position_embeddings": 8192})
+    default = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = CustomRecurrentMarinAKV254ReuseKVForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(default)
+    model = model.to(dev, torch.bfloat16).init_weights(torch.Generator(device=dev).manual_seed(0)).eval()
+    params = sum(p.numel() for p in model.parameters())
+    ids = torch.randint(0, cfg.vocab_size, (Bm, prompt), generator=torch.Generator().manual_seed(1)).to(dev)
+    cache = LastKVCache(cfg.num_hidden_layers, CHUNK, capacity_tokens=prompt + decode_steps)
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(0, prompt, call):
+            out = model(ids[:, s:s + call], past_key_values=cache, logits_to_keep=1)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        generated = [tok]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(decode_steps):
+            out = model(tok, past_key_values=cache, logits_to_keep=1)
+            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+            generated.append(tok)
+        torch.cuda.synchronize()
+        t_decode = time.perf_counter() - t0
+    ids_out = torch.cat(generated, 1)
+    del model, cache, out
+    torch.cuda.empty_cache()
+    return {
+        "workload": "config 3: 8B-shape LastKV model, B=32, 8192-token prompt in 2048-token calls (C=1024), "
+                    f"then {decode_steps} greedy decode steps; eager host loop",
+        "params": params, "prefill_s": round(t_prefill, 3), "prefill_tok_s": round(Bm * prompt / t_prefill, 1),
+        "decode_steps": decode_steps, "decode_ms_per_step": round(t_decode * 1e3 / decode_steps, 3),
+        "decode_tok_s": round(Bm * decode_steps / t_decode, 1),
+        "distinct_ids_seq0": int(ids_out[0].unique().numel()),
     }
 
 
@@ -196,6 +348,14 @@ def main() -> int:
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     achieved = BYTES_PER_CALL / (kernel_ms * 1e-3) / 1e9
     prefill = None if args.no_prefill else prefill_measurement(ops, torch, cache, dev)
+    configs = None
+    if not args.no_configs:
+        del qs, outs
+        configs = {"config4_decode_128k": decode_long_measurement(ops, torch, dev),
+                   "config5_wan": wan_measurement(ops, torch, dev)}
+        del cache
+        torch.cuda.empty_cache()
+        configs["config3_e2e_8b"] = e2e_8b_measurement(torch, dev, args.decode_steps)
     if args.calibrate_copy:
         src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev)
         dst = torch.empty_like(src)
@@ -236,6 +396,7 @@ def main() -> int:
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
         "prefill": prefill,
+        "configs": configs,
     }
     print(json.dumps(result), flush=True)
     return 0
