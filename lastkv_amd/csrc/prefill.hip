@@ -159,7 +159,7 @@ struct RowState {
 };
 
 // Raises each row's reference to its maximum over this block (lm = lane maxima) and rescales l
-// and O by 2^(mc_old - mc_new).  Runs in a wave-uniform branch taken on the first block and
+// and O by 2^(mc_old - mc_new).  Runs for the first block and in a wave-uniform branch taken
 // whenever some P reached 2.
 __device__ inline void raise_rows(RowState& rs, float lm, float c, f32x4 (&o)[8]) {
   const float bm = wave_max_across_rows(lm);
@@ -322,6 +322,27 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
         sc[cg][1] = mfma_bf16(k1, qf[cg][kb], sc[cg][1]);
       }
     }
+    // Block 0 sets every row's reference to its exact maximum (a row that sees any key sees one
+    // in block 0: visible keys are a prefix of [older | local]).  Inside the loop the only rescale
+    // test is then the packed-probability overflow check, so the compiler keeps the QK^T MFMAs of
+    // block i + 1 and the probabilities of block i in one scheduling region and interleaves them.
+    {
+      const BlockRef r0 = block_range(sv, 0);
+      float s0[CG][8];
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s0[cg][i] = sc[cg][0][i];
+          s0[cg][4 + i] = sc[cg][1][i];
+        }
+      if (r0.lo > 0 || r0.hi < kBlockTokens || (!r0.older && r0.seg_tok + kBlockTokens - 1 > w_min_lim)) {
+#pragma unroll
+        for (int cg = 0; cg < CG; ++cg) mask_scores(s0[cg], r0, lim[cg], g4);
+      }
+#pragma unroll
+      for (int cg = 0; cg < CG; ++cg) raise_rows(rs[cg], max8(s0[cg]), c, o[cg]);
+    }
 
     // Step i: the 16 LDS reads (K of block i + 1, V of block i) are issued first so their latency
     // passes under the mask work; then the QK^T MFMAs of block i + 1 are interleaved with the
@@ -383,11 +404,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
         __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);  // exp
       }
-      // first block, or a new row maximum: exact maxima, rescale, recompute this block's P
+      // a new row maximum: exact maxima, rescale, recompute this block's P
       uint32_t ovf = 0;
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) ovf |= probs_overflow(pw[cg]);
-      if (blk == 0 || __builtin_amdgcn_ballot_w64(ovf != 0)) {
+      if (__builtin_amdgcn_ballot_w64(ovf != 0)) {
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
           raise_rows(rs[cg], max8(s[cg]), c, o[cg]);
@@ -412,14 +433,22 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
       }
       __syncthreads();
     };
-    for (int blk = 0; blk < nbt; blk += kRing) {
+    // Whole rounds of the ring in the loop, the 0-3 remaining blocks after it: an exit from the
+    // middle of a round gives the loop header a second predecessor on which that round's stage
+    // loads are still in flight, and the header then waits for every load each round.
+    int blk = 0;
+    for (; blk + kRing <= nbt; blk += kRing) {
       step(IC<0>{}, blk);
-      if (blk + 1 >= nbt) break;
       step(IC<1>{}, blk + 1);
-      if (blk + 2 >= nbt) break;
       step(IC<2>{}, blk + 2);
-      if (blk + 3 >= nbt) break;
       step(IC<3>{}, blk + 3);
+    }
+    if (blk < nbt) {
+      step(IC<0>{}, blk);
+      if (blk + 1 < nbt) {
+        step(IC<1>{}, blk + 1);
+        if (blk + 2 < nbt) step(IC<2>{}, blk + 2);
+      }
     }
   }
 
