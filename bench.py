@@ -24,8 +24,10 @@ Printed JSON line (one, from this single process):
                  config4_decode_128k  lkv_decode_attn at B=4, 131072-token context (split-K), GB/s
                  config5_wan          Wan-1.3B block attention over its full history structure,
                                       30 layers, MFMA %
-                 config3_e2e_8b       the 8B-shape drop-in model: chunked prefill of 32 x 8192
-                                      tokens, then greedy decode steps, tok/s of each
+                 config3_e2e_8b       the 8B-shape model: chunked prefill of 32 x 8192 tokens,
+                                      then greedy decode steps, tok/s of each, through the
+                                      drop-in model (eager) and through the serving path (paged
+                                      pool, decode steps replayed from one HIP graph)
 """
 
 from __future__ import annotations
@@ -238,16 +240,54 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
             generated.append(tok)
         torch.cuda.synchronize()
         t_decode = time.perf_counter() - t0
-    ids_out = torch.cat(generated, 1)
-    del model, cache, out
+    ids_hf = torch.cat(generated, 1)
+    del cache, out
+    torch.cuda.empty_cache()
+
+    # The serving path (lastkv_amd.serving, the vLLM fast-path counterpart): one paged pool, prefill
+    # steps of 32 rows x 1024 tokens, then the decode steps replayed from one HIP graph.
+    from lastkv_amd.serving import LastKVServingModel
+
+    runner = LastKVServingModel(model, max_batch=Bm, max_tokens_per_slot=prompt + decode_steps + 1)
+    slots = [runner.add_sequence() for _ in range(Bm)]
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(0, prompt, CHUNK):
+            logits = runner.step([(slot, ids[b, s:s + CHUNK]) for b, slot in enumerate(slots)])
+        torch.cuda.synchronize()
+        t_sprefill = time.perf_counter() - t0
+        tok = logits.argmax(-1)
+        graph = runner.decode_graph(slots)
+        _, tok = graph.step(tok)  # capture + first replay, untimed
+        served = [tok.clone()]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(decode_steps - 1):
+            _, tok = graph.step(tok)
+            served.append(tok.clone())
+        torch.cuda.synchronize()
+        t_sdecode = time.perf_counter() - t0
+    ids_served = torch.stack(served, 1)
+    del runner, graph, model
     torch.cuda.empty_cache()
     return {
-        "workload": "config 3: 8B-shape LastKV model, B=32, 8192-token prompt in 2048-token calls (C=1024), "
-                    f"then {decode_steps} greedy decode steps; eager host loop",
-        "params": params, "prefill_s": round(t_prefill, 3), "prefill_tok_s": round(Bm * prompt / t_prefill, 1),
-        "decode_steps": decode_steps, "decode_ms_per_step": round(t_decode * 1e3 / decode_steps, 3),
-        "decode_tok_s": round(Bm * decode_steps / t_decode, 1),
-        "distinct_ids_seq0": int(ids_out[0].unique().numel()),
+        "workload": "config 3: 8B-shape LastKV model, B=32, 8192-token prompt (C=1024), then "
+                    f"{decode_steps} greedy decode steps",
+        "params": params,
+        "hf_path": {
+            "how": "drop-in lastkv_amd.llm model, 2048-token prefill calls, eager host loop",
+            "prefill_s": round(t_prefill, 3), "prefill_tok_s": round(Bm * prompt / t_prefill, 1),
+            "decode_ms_per_step": round(t_decode * 1e3 / decode_steps, 3),
+            "decode_tok_s": round(Bm * decode_steps / t_decode, 1),
+        },
+        "serving_path": {
+            "how": "lastkv_amd.serving paged pool, 1024-token prefill rows, decode steps replayed from one HIP graph",
+            "prefill_s": round(t_sprefill, 3), "prefill_tok_s": round(Bm * prompt / t_sprefill, 1),
+            "decode_ms_per_step": round(t_sdecode * 1e3 / (decode_steps - 1), 3),
+            "decode_tok_s": round(Bm * (decode_steps - 1) / t_sdecode, 1),
+        },
+        "first_ids_agree": bool(torch.equal(ids_hf[:, 1:9], ids_served[:, :8])),
     }
 
 

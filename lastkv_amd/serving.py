@@ -229,7 +229,7 @@ class LastKVFastPath:
         return int(self._seen[slot])
 
     # -------------------------------------------------------------- host prologue
-    def prepare(self, rows: list[tuple[int, int]], pad_to: int | None = None) -> None:
+    def prepare(self, rows: list[tuple[int, int]], pad_to: int | None = None, num_splits: int | None = None) -> None:
         """Stage one step: ``rows`` = (slot, new tokens) per sequence, in the order their tokens
         appear in the step's q/k/v rows; each row continues its sequence at ``seen(slot)``.
 
@@ -238,7 +238,8 @@ class LastKVFastPath:
         at the first step after the boundary), hands out shared pages, and copies positions,
         lengths, ring starts and table rows to device memory.  A row must not cross a chunk
         boundary (split prompts at multiples of C).  ``pad_to`` pads a decode step with empty rows
-        that read and write only the scratch page."""
+        that read and write only the scratch page.  ``num_splits`` fixes a decode step's key
+        splits (default: the path's ``num_splits``, else chosen from the longest row)."""
 
         P = self.pool
         C = P.chunk_size
@@ -283,7 +284,8 @@ class LastKVFastPath:
             self._cos1[:Bp].copy_(cos)
             self._sin1[:Bp].copy_(sin)
             keys = max(r.older + r.local for r in parsed)
-            self.splits = self.num_splits or ops.default_decode_splits(Bp, P.kv_heads, keys, ops._cu_count(P.device))
+            self.splits = num_splits or self.num_splits or ops.default_decode_splits(Bp, P.kv_heads, keys,
+                                                                                      ops._cu_count(P.device))
             need = ops.decode_workspace_bytes(Bp, Hq, self.splits)
             if self._decode_ws.numel() < need:
                 self._decode_ws = torch.empty(need, dtype=torch.uint8, device=P.device)
@@ -427,8 +429,18 @@ class LastKVServingModel:
         ids = torch.cat([ids.reshape(-1).to(self.pool.device) for _, ids in rows])
         if T > ids.numel():
             ids = torch.cat([ids, ids.new_zeros(T - ids.numel())])
+        hidden = self._layers(ids)
+        last = torch.tensor(np.cumsum([int(ids.numel()) for _, ids in rows]) - 1, device=hidden.device)
+        return self.model.lm_head(inner.norm(hidden.index_select(0, last)))
+
+    def _layers(self, ids: torch.Tensor) -> torch.Tensor:
+        """Device part of a prepared step: embeddings and every decoder layer over the step's
+        ``[T]`` token ids; returns the final hidden states ``[T, hidden]`` (before the norm)."""
+
+        inner = self.model.model
+        T = ids.numel()
         hidden = inner.embed_tokens(ids)
-        Hq = cfg.num_attention_heads
+        Hq = self.config.num_attention_heads
         out = torch.empty((T, Hq, ops.HEAD_DIM), dtype=hidden.dtype, device=hidden.device)
         for i, layer in enumerate(inner.layers):
             att = layer.self_attn
@@ -436,8 +448,12 @@ class LastKVServingModel:
             self.fast.run_layer(i, att.q_proj(h), att.k_proj(h), att.v_proj(h), out)
             hidden = hidden + att.o_proj(out.view(T, Hq * ops.HEAD_DIM))
             hidden = hidden + layer.mlp(layer.post_attention_layernorm(hidden))
-        last = torch.tensor(np.cumsum([int(ids.numel()) for _, ids in rows]) - 1, device=hidden.device)
-        return self.model.lm_head(inner.norm(hidden.index_select(0, last)))
+        return hidden
+
+    def decode_graph(self, slots: list[int], num_splits: int | None = None) -> "DecodeGraph":
+        """A HIP-graph replay of greedy decode steps for ``slots`` (one token each per step)."""
+
+        return DecodeGraph(self, slots, num_splits)
 
     @torch.no_grad()
     def generate(self, prompts: list[torch.Tensor], max_new_tokens: int, *, prefill_chunk: int | None = None
@@ -473,3 +489,68 @@ class LastKVServingModel:
             for slot in slots:
                 self.free_sequence(slot)
         return [torch.cat([p.reshape(-1).cpu(), torch.tensor(g, dtype=p.dtype)]) for p, g in zip(prompts, gen)]
+
+
+class DecodeGraph:
+    """Greedy decode steps of a fixed set of sequences, one token each, replayed from one HIP graph.
+
+    The host prologue of a step (``LastKVFastPath.prepare``: boundary commits, page hand-out, and
+    positions, key lengths, ring starts, page-table rows and RoPE rows written into persistent
+    device buffers) runs eagerly before every replay.  The captured part is the device work of the
+    step: embeddings, every layer's projections, fused QKV epilogue, paged decode attention, o_proj
+    and MLP, the final norm, lm_head and the argmax, all reading only those buffers.  This is the
+    reference's graph-captured decode fast path (``fastpath.py:1-9``, ``:619-651``).  The split
+    count is fixed for the graph's lifetime (default: the one for the longest context a slot can
+    reach), so that every captured kernel argument stays valid."""
+
+    def __init__(self, runner: "LastKVServingModel", slots: list[int], num_splits: int | None = None):
+        if not slots:
+            raise ValueError("a decode graph needs at least one slot")
+        self.runner = runner
+        self.slots = list(slots)
+        fast, pool = runner.fast, runner.pool
+        B = len(self.slots)
+        if B > fast.max_batch:
+            raise ValueError(f"{B} slots exceed max_batch {fast.max_batch}")
+        max_keys = pool.src_width * BLOCK + pool.ring_tokens
+        self.num_splits = num_splits or fast.num_splits or ops.default_decode_splits(
+            B, pool.kv_heads, max_keys, ops._cu_count(pool.device))
+        self.ids = torch.zeros(B, dtype=torch.long, device=pool.device)
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.logits: torch.Tensor | None = None
+        self.tokens: torch.Tensor | None = None
+        self._key = None
+
+    def _device_step(self):
+        inner = self.runner.model.model
+        logits = self.runner.model.lm_head(inner.norm(self.runner._layers(self.ids)))
+        return logits, logits.argmax(-1)
+
+    def _buffers(self):
+        f = self.runner.fast
+        return (f.splits, f.batch, f.tokens, f._decode_ws.data_ptr(), f._q_out.data_ptr(), f._meta.data_ptr(),
+                f._older_table.data_ptr(), f._ring_table.data_ptr(), f._cos1.data_ptr(), f._sin1.data_ptr())
+
+    @torch.no_grad()
+    def step(self, tokens: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Feed ``tokens`` (``[B]`` ids on the device, one per slot in order) and return
+        (logits ``[B, vocab]``, greedy next ids ``[B]``), views of the graph's outputs that the next
+        step overwrites."""
+
+        fast = self.runner.fast
+        fast.prepare([(slot, 1) for slot in self.slots], num_splits=self.num_splits)
+        self.ids.copy_(tokens.reshape(-1))
+        key = self._buffers()
+        if self.graph is None:
+            # warm-up run (library handles, allocator); it writes this step's K/V, which the
+            # replay below writes again with the same values
+            self._device_step()
+            torch.cuda.current_stream().synchronize()
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self.logits, self.tokens = self._device_step()
+            self._key = key
+        elif key != self._key:
+            raise RuntimeError("the decode graph's buffers changed since capture (split count or workspace)")
+        self.graph.replay()
+        return self.logits, self.tokens

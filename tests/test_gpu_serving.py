@@ -162,3 +162,50 @@ def test_serving_generate_runs_and_frees_pages():
         assert torch.equal(a[: p.numel()], p.cpu())
         assert torch.equal(a, b)
     assert runner.pool.free_pages == total
+
+
+
+def _prefill(runner, slots, prompts, chunk):
+    """Feed each prompt in pieces cut at chunk boundaries; returns each row's next greedy id."""
+
+    nxt = []
+    for slot, p in zip(slots, prompts):
+        fed = 0
+        while fed < p.numel():
+            take = min(p.numel() - fed, chunk - runner.fast.seen(slot) % chunk)
+            logits = runner.step([(slot, p[fed:fed + take])])
+            fed += take
+        nxt.append(logits[0].argmax())
+    return torch.stack(nxt)
+
+
+def test_decode_graph_replays_match_eager_steps():
+    """DecodeGraph against eager LastKVServingModel.step on a second runner over the same model:
+    3 sequences prefilled eagerly, then 40 decode steps at C = 8 (boundary commits and ring wraps
+    run in the host prologue between replays), with unrelated eager work and synchronisations
+    between the replays; every replay's logits and greedy ids equal the eager step's."""
+
+    _, ours = _tiny(chunk=8)
+    eager = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=96, num_splits=2)
+    graphed = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=96, num_splits=2)
+    prompts = [torch.arange(3, 14, device=DEV), torch.tensor([1, 5, 17, 33, 2], device=DEV),
+               torch.arange(40, 61, device=DEV)]
+    se = [eager.add_sequence() for _ in prompts]
+    sg = [graphed.add_sequence() for _ in prompts]
+    with torch.inference_mode():
+        t_eager = _prefill(eager, se, prompts, 8)
+        t_graph = _prefill(graphed, sg, prompts, 8)
+        assert torch.equal(t_eager, t_graph)
+        graph = graphed.decode_graph(sg)
+        scratch = torch.randn(256, 256, device=DEV)
+        for i in range(40):
+            le = eager.step([(s, t_eager[j:j + 1]) for j, s in enumerate(se)])
+            lg, ng = graph.step(t_graph)
+            assert torch.equal(le, lg), f"step {i}: replay logits differ from the eager step"
+            t_eager = le.argmax(-1)
+            assert torch.equal(t_eager, ng), f"step {i}: greedy ids differ"
+            t_graph = ng.clone()
+            scratch = scratch @ scratch.T * 1e-3  # the program's own eager work between replays
+            if i % 3 == 0:
+                torch.cuda.synchronize()
+    assert graphed.fast.seen(sg[0]) == eager.fast.seen(se[0]) == prompts[0].numel() + 40
