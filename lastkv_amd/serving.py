@@ -50,6 +50,37 @@ def plan_row(position: int, tokens: int, chunk: int, ring_tokens: int) -> tuple[
     return rec, local, rec % ring_tokens
 
 
+class PinnedStager:
+    """Host-to-device copies of small host arrays through pinned staging slots, so that the host
+    prologue never waits for the stream: each copy is queued behind the work already on it (the
+    previous step), and a slot is rewritten only after the copy that last read it has completed."""
+
+    def __init__(self, device: torch.device, slots: int = 16, nbytes: int = 1 << 16):
+        self.device = device
+        self.nbytes = nbytes
+        self._bufs = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(slots)]
+        self._done: list[torch.cuda.Event | None] = [None] * slots
+        self._next = 0
+
+    def copy(self, dst: torch.Tensor, src: np.ndarray) -> None:
+        """``dst`` (a device tensor or view with the shape and dtype of ``src``) := ``src``."""
+
+        src = np.ascontiguousarray(src)
+        if src.nbytes > self.nbytes:
+            dst.copy_(torch.from_numpy(src))  # large: synchronous pageable copy
+            return
+        i = self._next
+        self._next = (i + 1) % len(self._bufs)
+        if self._done[i] is not None:
+            self._done[i].synchronize()
+        staged = self._bufs[i][: src.nbytes].view(dst.dtype).view(dst.shape)
+        staged.copy_(torch.from_numpy(src))
+        dst.copy_(staged, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self._done[i] = ev
+
+
 class PageAllocator:
     """Host bookkeeping of sequence slots and shared-cache pages: per slot a table row of page ids
     (unused entries name ``scratch``), pages handed out in order as a sequence grows and returned
@@ -118,6 +149,7 @@ class LastKVPagePool:
         self.ring_table = torch.from_numpy(ring.astype(np.int32)).to(self.device)
         self.pages = PageAllocator(max_slots=max_slots, pages=source_pages, width=self.src_width, scratch=self.scratch_page)
         self.src_table = torch.from_numpy(self.pages.table.copy()).to(self.device)
+        self.stager = PinnedStager(self.device)
 
     @property
     def free_pages(self) -> int:
@@ -135,7 +167,7 @@ class LastKVPagePool:
 
         lo, hi = self.pages.reserve(slot, tokens)
         if hi > lo:
-            self.src_table[slot, lo:hi].copy_(torch.from_numpy(self.pages.table[slot, lo:hi]))
+            self.stager.copy(self.src_table[slot, lo:hi], self.pages.table[slot, lo:hi])
 
 
 @dataclass
@@ -175,6 +207,7 @@ class LastKVFastPath:
         self._open = np.zeros(pool.max_slots, dtype=bool)
         i32 = dict(dtype=torch.int32, device=dev)
         self._meta = torch.zeros((4, max_batch), **i32)  # positions, older_len, local_len, local_start
+        self._slots = torch.zeros(max_batch, dtype=torch.long, device=dev)
         self._older_table = torch.full((max_batch, pool.src_width), pool.scratch_page, **i32)
         self._ring_table = torch.full((pool.num_layers, max_batch, pool.ring_blocks), pool.scratch_page, **i32)
         self._cos1 = torch.zeros((max_batch, 1, ops.HEAD_DIM), dtype=torch.bfloat16, device=dev)
@@ -269,9 +302,9 @@ class LastKVFastPath:
         meta = np.zeros((4, Bp), dtype=np.int32)  # padded rows: position 0, no keys
         for b, r in enumerate(parsed):
             meta[:, b] = (r.position, r.older, r.local, r.older % P.ring_tokens)
-        # pageable host memory: the copy has read it when the call returns
-        self._meta[:, :Bp].copy_(torch.from_numpy(meta))
-        slots = torch.tensor([r.slot for r in parsed], dtype=torch.long).to(P.device)
+        P.stager.copy(self._meta[:, :Bp], meta)
+        slots = self._slots[:B]
+        P.stager.copy(slots, np.array([r.slot for r in parsed], dtype=np.int64))
         self._older_table[:B].copy_(P.src_table.index_select(0, slots))
         self._ring_table[:, :B].copy_(P.ring_table.index_select(1, slots))
         if Bp > B:
