@@ -66,6 +66,9 @@ def parse_args():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 4 (128K decode), config 5 (Wan) and config 3 (8B end to end) measurements")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy decode steps of the config 3 model run")
+    ap.add_argument("--only", choices=["prefill", "config4", "config5", "config3"], default=None,
+                    help="run one secondary measurement alone and print its JSON (for profiling); "
+                         "this is not the bench line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device copy (reference kernel for HBM byte counters)")
     return ap.parse_args()
@@ -343,6 +346,19 @@ def main() -> int:
     from lastkv_amd import ops
 
     dev = torch.device("cuda:0")
+    if args.only is not None:
+        if args.only == "prefill":
+            store = ops.TiledKV(torch.randn((B, HKV, T // 32, 4096), device=dev).bfloat16(),
+                                torch.randn((B, HKV, T // 32, 4096), device=dev).bfloat16())
+            res = prefill_measurement(ops, torch, store, dev)
+        elif args.only == "config4":
+            res = decode_long_measurement(ops, torch, dev)
+        elif args.only == "config5":
+            res = wan_measurement(ops, torch, dev)
+        else:
+            res = e2e_8b_measurement(torch, dev, args.decode_steps)
+        print(json.dumps({"only": args.only, **res}), flush=True)
+        return 0
     g = torch.Generator(device=dev).manual_seed(2)
     k = torch.randn((B, HKV, T, D), generator=g, device=dev).bfloat16()
     v = torch.randn((B, HKV, T, D), generator=g, device=dev).bfloat16()
