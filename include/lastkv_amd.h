@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 3
+#define LKV_ABI_VERSION 4
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -436,6 +436,39 @@ typedef struct lkv_append_args {
 } lkv_append_args;
 
 int32_t lkv_append_paged(const lkv_append_args *args, lkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Decoder-layer glue of the serving path: RMSNorm with a fused residual add, and SwiGLU.
+ *
+ * lkv_rmsnorm replaces the serving model's input / post-attention / final norms and the
+ * residual adds before them (the reference's vLLM model uses vLLM's fused_add_rms_norm there;
+ * its HF model, modeling.py:150-171, uses transformers' LlamaRMSNorm, whose arithmetic this keeps):
+ * for each of `rows` rows of `hidden` bf16 values,
+ *   if residual != NULL: residual := bf16(residual + x), and the normalised row is residual;
+ *   h = float(row); r = rsqrt(sum(h^2) * (1 / hidden) + eps); out = bf16(weight * bf16(h * r)).
+ * hidden is a multiple of 8 up to 16384; rows are 16-byte aligned, strides in elements.
+ * ------------------------------------------------------------------------------------- */
+typedef struct lkv_rmsnorm_args {
+  int32_t struct_size; /* sizeof(lkv_rmsnorm_args) */
+  int32_t rows;
+  int32_t hidden;
+  float eps;
+  const void *x; /* bf16 [rows, hidden] */
+  int64_t x_stride;
+  void *residual; /* optional bf16 [rows, hidden], updated in place */
+  int64_t residual_stride;
+  const void *weight; /* bf16 [hidden] */
+  void *out;          /* bf16 [rows, hidden]; may alias x when residual is NULL */
+  int64_t out_stride;
+} lkv_rmsnorm_args;
+
+int32_t lkv_rmsnorm(const lkv_rmsnorm_args *args, lkv_stream_t stream);
+
+/* out = bf16(bf16(silu(gate)) * up) over rows x width bf16 values (torch's
+ * F.silu(gate_proj(x)) * up_proj(x) in the Llama MLP, with both of its roundings); width is a
+ * multiple of 8, rows 16-byte aligned, strides in elements. */
+int32_t lkv_silu_mul(const void *gate, int64_t gate_stride, const void *up, int64_t up_stride, void *out,
+                     int64_t out_stride, int32_t rows, int32_t width, lkv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -11,7 +11,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class LastKVNativeError(RuntimeError):
@@ -282,6 +282,24 @@ class BlendArgs(ctypes.Structure):
 
 
 # name -> (restype, argtypes)
+class NormArgs(ctypes.Structure):
+    """Mirror of ``lkv_rmsnorm_args``."""
+
+    _fields_ = [
+        ("struct_size", c_i32),
+        ("rows", c_i32),
+        ("hidden", c_i32),
+        ("eps", c_f32),
+        ("x", c_ptr),
+        ("x_stride", c_i64),
+        ("residual", c_ptr),
+        ("residual_stride", c_i64),
+        ("weight", c_ptr),
+        ("out", c_ptr),
+        ("out_stride", c_i64),
+    ]
+
+
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lkv_abi_version": (c_i32, []),
     "lkv_last_error": (ctypes.c_char_p, []),
@@ -301,6 +319,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lkv_append_paged": (c_i32, [ctypes.POINTER(AppendArgs), c_ptr]),
     "lkv_qkv_epilogue": (c_i32, [ctypes.POINTER(QkvArgs), c_ptr]),
     "lkv_blend_chunk": (c_i32, [ctypes.POINTER(BlendArgs), c_ptr]),
+    "lkv_rmsnorm": (c_i32, [ctypes.POINTER(NormArgs), c_ptr]),
+    "lkv_silu_mul": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_ptr]),
 }
 
 _lock = threading.Lock()

@@ -709,3 +709,61 @@ def ring_tokens_for_chunk(chunk: int) -> int:
     if chunk % BLOCK_TOKENS and BLOCK_TOKENS % chunk:
         ring += BLOCK_TOKENS
     return ring
+
+
+def _rows2d(name: str, t: torch.Tensor) -> tuple[int, int, int]:
+    """(rows, width, row stride) of a bf16 CUDA tensor viewed as [rows, width] with contiguous rows."""
+
+    _require_bf16_cuda(name, t)
+    _require(t.dim() >= 1 and t.stride(-1) == 1, f"{name} rows must be contiguous")
+    width = t.shape[-1]
+    if t.dim() == 1:
+        return 1, width, width
+    try:
+        flat = t.view(-1, width)
+    except RuntimeError:
+        flat = None
+    _require(flat is not None, f"{name} must be viewable as [rows, {width}] with one row stride")
+    return flat.shape[0], width, flat.stride(0)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, residual: torch.Tensor | None = None,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """LlamaRMSNorm of the rows of ``x`` (bf16 ``[..., hidden]``); with ``residual`` first
+    ``residual += x`` in bf16 (in place) and the sum is normalised.  Returns ``out``."""
+
+    rows, hidden, xs = _rows2d("x", x)
+    _require_bf16_cuda("weight", weight)
+    _require(weight.is_contiguous() and weight.numel() == hidden, "weight must be a contiguous bf16 [hidden] tensor")
+    rs = 0
+    if residual is not None:
+        r_rows, r_hidden, rs = _rows2d("residual", residual)
+        _require((r_rows, r_hidden) == (rows, hidden), "residual shape must match x")
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    o_rows, o_hidden, os_ = _rows2d("out", out)
+    _require((o_rows, o_hidden) == (rows, hidden), "out shape must match x")
+    a = _lib.NormArgs()
+    a.struct_size = ctypes.sizeof(_lib.NormArgs)
+    a.rows, a.hidden, a.eps = rows, hidden, float(eps)
+    a.x, a.x_stride = x.data_ptr(), xs
+    a.residual, a.residual_stride = _ptr(residual), rs
+    a.weight = weight.data_ptr()
+    a.out, a.out_stride = out.data_ptr(), os_
+    _lib.check(_lib.load().lkv_rmsnorm(ctypes.byref(a), _stream(x.device)), "lkv_rmsnorm")
+    return out
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.silu(gate) * up`` for bf16 ``[..., width]`` tensors, as torch rounds it."""
+
+    rows, width, gs = _rows2d("gate", gate)
+    u_rows, u_width, us = _rows2d("up", up)
+    _require((u_rows, u_width) == (rows, width), "up shape must match gate")
+    if out is None:
+        out = torch.empty(gate.shape, dtype=torch.bfloat16, device=gate.device)
+    o_rows, o_width, os_ = _rows2d("out", out)
+    _require((o_rows, o_width) == (rows, width), "out shape must match gate")
+    _lib.check(_lib.load().lkv_silu_mul(gate.data_ptr(), gs, up.data_ptr(), us, out.data_ptr(), os_, rows, width,
+                                        _stream(gate.device)), "lkv_silu_mul")
+    return out

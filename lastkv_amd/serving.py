@@ -456,32 +456,38 @@ class LastKVServingModel:
     def step(self, rows: list[tuple[int, torch.Tensor]], pad_to: int | None = None) -> torch.Tensor:
         """``rows`` = (slot, new token ids [n]); returns the logits of each row's last token ``[B, vocab]``."""
 
-        cfg, inner = self.config, self.model.model
         self.fast.prepare([(slot, int(ids.numel())) for slot, ids in rows], pad_to=pad_to)
         T = self.fast.tokens
         ids = torch.cat([ids.reshape(-1).to(self.pool.device) for _, ids in rows])
         if T > ids.numel():
             ids = torch.cat([ids, ids.new_zeros(T - ids.numel())])
-        hidden = self._layers(ids)
-        last = torch.tensor(np.cumsum([int(ids.numel()) for _, ids in rows]) - 1, device=hidden.device)
-        return self.model.lm_head(inner.norm(hidden.index_select(0, last)))
+        normed = self._layers(ids)
+        last = torch.tensor(np.cumsum([int(ids.numel()) for _, ids in rows]) - 1, device=normed.device)
+        return self.model.lm_head(normed.index_select(0, last))
 
     def _layers(self, ids: torch.Tensor) -> torch.Tensor:
         """Device part of a prepared step: embeddings and every decoder layer over the step's
-        ``[T]`` token ids; returns the final hidden states ``[T, hidden]`` (before the norm)."""
+        ``[T]`` token ids; returns the final norm's output ``[T, hidden]``.  The residual adds and
+        RMSNorms run fused (``lkv_rmsnorm``, LlamaRMSNorm arithmetic) and the MLP's SiLU product as
+        ``lkv_silu_mul``, the roles of vLLM's fused_add_rms_norm and silu_and_mul."""
 
         inner = self.model.model
+        layers = inner.layers
+        eps = self.config.rms_norm_eps
         T = ids.numel()
-        hidden = inner.embed_tokens(ids)
+        hidden = inner.embed_tokens(ids)  # the residual stream, updated in place
         Hq = self.config.num_attention_heads
         out = torch.empty((T, Hq, ops.HEAD_DIM), dtype=hidden.dtype, device=hidden.device)
-        for i, layer in enumerate(inner.layers):
-            att = layer.self_attn
-            h = layer.input_layernorm(hidden)
+        h = ops.rmsnorm(hidden, layers[0].input_layernorm.weight, eps)
+        for i, layer in enumerate(layers):
+            att, mlp = layer.self_attn, layer.mlp
             self.fast.run_layer(i, att.q_proj(h), att.k_proj(h), att.v_proj(h), out)
-            hidden = hidden + att.o_proj(out.view(T, Hq * ops.HEAD_DIM))
-            hidden = hidden + layer.mlp(layer.post_attention_layernorm(hidden))
-        return hidden
+            h = ops.rmsnorm(att.o_proj(out.view(T, Hq * ops.HEAD_DIM)), layer.post_attention_layernorm.weight, eps,
+                            residual=hidden)
+            m = mlp.down_proj(ops.silu_mul(mlp.gate_proj(h), mlp.up_proj(h)))
+            nxt = layers[i + 1].input_layernorm.weight if i + 1 < len(layers) else inner.norm.weight
+            h = ops.rmsnorm(m, nxt, eps, residual=hidden)
+        return h
 
     def decode_graph(self, slots: list[int], num_splits: int | None = None) -> "DecodeGraph":
         """A HIP-graph replay of greedy decode steps for ``slots`` (one token each per step)."""
@@ -555,8 +561,7 @@ class DecodeGraph:
         self._key = None
 
     def _device_step(self):
-        inner = self.runner.model.model
-        logits = self.runner.model.lm_head(inner.norm(self.runner._layers(self.ids)))
+        logits = self.runner.model.lm_head(self.runner._layers(self.ids))
         return logits, logits.argmax(-1)
 
     def _buffers(self):

@@ -276,3 +276,46 @@ def test_blend_chunk_bit_exact(chunk, cidx):
         # every other ring token is untouched
         rest = np.setdiff1d(np.arange(R), pos)
         assert np.array_equal(gk[:, :, rest], own[l][0][:, :, rest]) and np.array_equal(gv[:, :, rest], own[l][1][:, :, rest])
+
+
+def _torch_rmsnorm(x, w, eps):
+    h = x.float()
+    h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
+    return w * h.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,hidden,add", [(1, 4096, False), (32, 4096, True), (7, 1536, True), (33, 8, False),
+                                             (3, 16384, True)])
+def test_rmsnorm_matches_llama_rmsnorm(rows, hidden, add):
+    """lkv_rmsnorm against transformers' LlamaRMSNorm expression in torch (with the residual add
+    before it, a bf16 add): the residual is bit-exact; the normalised values differ only where the
+    fp32 sum of squares is rounded in another order (at most one bf16 ulp, on few elements)."""
+
+    g = torch.Generator(device=DEV).manual_seed(rows * 7 + hidden)
+    x = (torch.randn((rows, hidden), generator=g, device=DEV) * 3).bfloat16()
+    res = torch.randn((rows, hidden), generator=g, device=DEV).bfloat16()
+    w = (1 + 0.1 * torch.randn(hidden, generator=g, device=DEV)).bfloat16()
+    eps = 1e-5
+    want_res = res + x if add else None
+    want = _torch_rmsnorm(want_res if add else x, w, eps)
+    r = res.clone()
+    got = ops.rmsnorm(x, w, eps, residual=r if add else None)
+    torch.cuda.synchronize()
+    if add:
+        assert torch.equal(r, want_res)
+    else:
+        assert torch.equal(r, res)
+    diff = (got.float() - want.float()).abs()
+    ulp = want.float().abs().clamp_min(1e-30) * 2.0 ** -7
+    assert bool((diff <= ulp).all()), float((diff / ulp).max())
+    assert float((diff > 0).float().mean()) < 0.01
+
+
+def test_silu_mul_bit_exact():
+    g = torch.Generator(device=DEV).manual_seed(11)
+    gate = (torch.randn((37, 14336), generator=g, device=DEV) * 4).bfloat16()
+    up = torch.randn((37, 14336), generator=g, device=DEV).bfloat16()
+    got = ops.silu_mul(gate, up)
+    want = torch.nn.functional.silu(gate) * up
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
