@@ -61,24 +61,36 @@ class PinnedStager:
         self._bufs = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(slots)]
         self._done: list[torch.cuda.Event | None] = [None] * slots
         self._next = 0
+        self._big: torch.Tensor | None = None
+        self._big_done: torch.cuda.Event | None = None
 
     def copy(self, dst: torch.Tensor, src: np.ndarray) -> None:
         """``dst`` (a device tensor or view with the shape and dtype of ``src``) := ``src``."""
 
         src = np.ascontiguousarray(src)
-        if src.nbytes > self.nbytes:
-            dst.copy_(torch.from_numpy(src))  # large: synchronous pageable copy
-            return
-        i = self._next
-        self._next = (i + 1) % len(self._bufs)
-        if self._done[i] is not None:
-            self._done[i].synchronize()
-        staged = self._bufs[i][: src.nbytes].view(dst.dtype).view(dst.shape)
+        if src.nbytes > self.nbytes:  # large: one grow-on-demand buffer of its own
+            if self._big is None or self._big.numel() < src.nbytes:
+                if self._big_done is not None:
+                    self._big_done.synchronize()
+                self._big = torch.empty(src.nbytes, dtype=torch.uint8, pin_memory=True)
+                self._big_done = None
+            buf, i = self._big, -1
+        else:
+            i = self._next
+            self._next = (i + 1) % len(self._bufs)
+            buf = self._bufs[i]
+        done = self._big_done if i < 0 else self._done[i]
+        if done is not None:
+            done.synchronize()
+        staged = buf[: src.nbytes].view(dst.dtype).view(dst.shape)
         staged.copy_(torch.from_numpy(src))
         dst.copy_(staged, non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(self.device))
-        self._done[i] = ev
+        if i < 0:
+            self._big_done = ev
+        else:
+            self._done[i] = ev
 
 
 class PageAllocator:
@@ -150,6 +162,7 @@ class LastKVPagePool:
         self.pages = PageAllocator(max_slots=max_slots, pages=source_pages, width=self.src_width, scratch=self.scratch_page)
         self.src_table = torch.from_numpy(self.pages.table.copy()).to(self.device)
         self.stager = PinnedStager(self.device)
+        self._dirty_lo, self._dirty_hi = max_slots, 0  # table rows changed since the last flush
 
     @property
     def free_pages(self) -> int:
@@ -163,11 +176,21 @@ class LastKVPagePool:
         self.src_table[slot].fill_(self.scratch_page)
 
     def reserve(self, slot: int, tokens: int) -> None:
-        """Give ``slot`` shared pages for positions ``[0, tokens)``."""
+        """Give ``slot`` shared pages for positions ``[0, tokens)`` (host table; ``flush`` copies
+        the changed rows to the device table)."""
 
         lo, hi = self.pages.reserve(slot, tokens)
         if hi > lo:
-            self.stager.copy(self.src_table[slot, lo:hi], self.pages.table[slot, lo:hi])
+            self._dirty_lo = min(self._dirty_lo, slot)
+            self._dirty_hi = max(self._dirty_hi, slot + 1)
+
+    def flush(self) -> None:
+        """One host-to-device copy of the table rows changed since the last flush."""
+
+        if self._dirty_hi > self._dirty_lo:
+            lo, hi = self._dirty_lo, self._dirty_hi
+            self.stager.copy(self.src_table[lo:hi], self.pages.table[lo:hi])
+            self._dirty_lo, self._dirty_hi = self.max_slots, 0
 
 
 @dataclass
@@ -296,6 +319,7 @@ class LastKVFastPath:
             raise ValueError(f"{Bp} rows exceed max_batch {self.max_batch}")
         for r in parsed:
             P.reserve(r.slot, r.position + r.tokens)
+        P.flush()
         for r in parsed:
             if r.position > 0 and r.position % C == 0 and self._committed[r.slot] < r.position:
                 self._commit(r.slot, r.position)
