@@ -272,6 +272,8 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
         torch.cuda.synchronize()
         t_sdecode = time.perf_counter() - t0
     ids_served = torch.stack(served, 1)
+    same = (ids_hf[:, 1:1 + ids_served.shape[1]] == ids_served[:, : ids_hf.shape[1] - 1]).all(0).tolist()
+    agreement = next((i for i, ok in enumerate(same) if not ok), len(same))
     del runner, graph, model
     torch.cuda.empty_cache()
     return {
@@ -290,7 +292,10 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
             "decode_ms_per_step": round(t_sdecode * 1e3 / (decode_steps - 1), 3),
             "decode_tok_s": round(Bm * (decode_steps - 1) / t_sdecode, 1),
         },
-        "first_ids_agree": bool(torch.equal(ids_hf[:, 1:9], ids_served[:, :8])),
+        # leading decode steps on which all 32 greedy ids agree between the two paths: the serving
+        # path's fused RMSNorm sums in another order than torch's (last-bit differences now and
+        # then) and random-weight logits are near-flat, so the paths part after a few steps
+        "greedy_agreement_steps": agreement,
     }
 
 
