@@ -226,23 +226,55 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   }
 }
 
-// Merges the per-split states of one (sequence, query head); one thread per head dim.
-__global__ __launch_bounds__(128) void decode_combine_kernel(const DecodeParams p) {
+// Merges the per-split states of one (sequence, query head); one thread per head dim.  The splits'
+// (m, l) pairs are staged in LDS and reduced in parallel (maximum, then the weights 2^(m_s - M)
+// and L), so the per-dim accumulation over the splits has no dependent loads and keeps several
+// partial-O loads in flight.
+constexpr int kCombineThreads = kHeadDim;
+constexpr int kMaxSplits = 1024;
+
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const DecodeParams p) {
+  __shared__ float sm_w[kMaxSplits];
+  __shared__ float sm_red[kCombineThreads / 64];
   const int bh = blockIdx.x;
   const int d = threadIdx.x;
   const int b = bh / p.hq, h = bh % p.hq;
-  const float* ml = p.ws_ml + static_cast<int64_t>(bh) * p.splits * 2;
-  const float* o = p.ws_o + static_cast<int64_t>(bh) * p.splits * kHeadDim;
-  float M = kNegInf;
-  for (int s = 0; s < p.splits; ++s) M = fmaxf(M, ml[2 * s]);
-  float L = 0.f, O = 0.f;
-  for (int s = 0; s < p.splits; ++s) {
-    const float ms = ml[2 * s];
-    const float f = ms == kNegInf ? 0.f : fast_exp2(ms - M);
-    L += f * ml[2 * s + 1];
-    O += f * o[s * kHeadDim + d];
+  const int S = p.splits;
+  const float* ml = p.ws_ml + static_cast<int64_t>(bh) * S * 2;
+  const float* o = p.ws_o + static_cast<int64_t>(bh) * S * kHeadDim;
+  float mx = kNegInf;
+  for (int s = d; s < S; s += kCombineThreads) {
+    const float m = ml[2 * s];
+    sm_w[s] = m;
+    mx = fmaxf(mx, m);
   }
-  p.out[b * p.out_sb + static_cast<int64_t>(h) * kHeadDim + d] = f32_to_bf16_bits(L > 0.f ? O / L : 0.f);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if ((d & 63) == 0) sm_red[d >> 6] = mx;
+  __syncthreads();
+  const float M = fmaxf(sm_red[0], sm_red[1]);
+  __syncthreads();
+  float lsum = 0.f;
+  for (int s = d; s < S; s += kCombineThreads) {
+    const float m = sm_w[s];
+    const float f = m == kNegInf ? 0.f : fast_exp2(m - M);
+    sm_w[s] = f;
+    lsum += f * ml[2 * s + 1];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off);
+  if ((d & 63) == 0) sm_red[d >> 6] = lsum;
+  __syncthreads();
+  const float L = sm_red[0] + sm_red[1];
+  float O[4] = {0.f, 0.f, 0.f, 0.f};
+  int s = 0;
+  for (; s + 4 <= S; s += 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) O[j] += sm_w[s + j] * o[(s + j) * kHeadDim + d];
+  }
+  for (; s < S; ++s) O[0] += sm_w[s] * o[s * kHeadDim + d];
+  const float Ot = (O[0] + O[1]) + (O[2] + O[3]);
+  p.out[b * p.out_sb + static_cast<int64_t>(h) * kHeadDim + d] = f32_to_bf16_bits(L > 0.f ? Ot / L : 0.f);
   if (p.lse != nullptr && d == 0) p.lse[bh] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
 }
 
@@ -302,7 +334,7 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
     decode_split_kernel<false><<<grid, 256, 0, s>>>(p);
   if (int32_t st = check_launch("lkv_decode_attn split kernel")) return st;
   if (a->num_splits > 1) {
-    decode_combine_kernel<<<a->batch * a->num_q_heads, kHeadDim, 0, s>>>(p);
+    decode_combine_kernel<<<a->batch * a->num_q_heads, kCombineThreads, 0, s>>>(p);
     return check_launch("lkv_decode_attn combine kernel");
   }
   return LKV_OK;
