@@ -193,3 +193,59 @@ def test_config2_split_invariance_and_power_of_two_vscale_linearity(config2):
     two = torch.full((8,), 2.0, dtype=torch.float32, device=DEV)
     scaled = ops.decode_attention(q, older=cache, older_len=8192, vscale=two, num_splits=1)
     assert torch.equal(scaled, base * 2)
+
+
+def _two_segments(rng, B, Hkv, T0, n1, start, ring_blocks):
+    """Older segment of T0 tokens and a ring of ring_blocks blocks holding n1 tokens from ring token
+    `start` (wrapping), with a bf16 older V scale; returns the caches and the composed fp32 K/V the
+    kernel must attend to (older V as bf16(V * s))."""
+
+    ok, ov = _bf(rng, (B, Hkv, T0, 128)), _bf(rng, (B, Hkv, T0, 128))
+    lk, lv = _bf(rng, (B, Hkv, n1, 128)), _bf(rng, (B, Hkv, n1, 128))
+    s = bf16.round_bf16(rng.uniform(0.4, 1.4, Hkv).astype(np.float32))
+    older = ops.TiledKV.zeros(B, Hkv, max(32, -(-T0 // 32) * 32), DEV)
+    ops.pack_kv(_t(ok), _t(ov), older)
+    ring = ops.TiledKV.zeros(B, Hkv, ring_blocks * 32, DEV)
+    R = ring_blocks * 32
+    first = min(n1, R - start)
+    ops.pack_kv(_t(lk[:, :, :first]), _t(lv[:, :, :first]), ring, token0=start)
+    if first < n1:
+        ops.pack_kv(_t(lk[:, :, first:]), _t(lv[:, :, first:]), ring, token0=0)
+    k = np.concatenate([ok, lk], 2)
+    v = np.concatenate([bf16.mul(ov, s.reshape(1, -1, 1, 1)), lv], 2)
+    seg = dict(older=older, older_len=T0, vscale=torch.from_numpy(s).to(DEV), local=ring, local_len=n1,
+               local_start=start)
+    return seg, k, v
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (6, 2), (7, 1), (16, 2), (32, 2), (48, 3)])
+@pytest.mark.parametrize("splits", [1, 4])
+def test_decode_gqa_group_sizes(Hq, Hkv, splits):
+    """GQA groups 1 (MHA) to 16 (the kernel's limit), odd and not powers of two, over an older
+    segment with V scale and a wrapping ring segment; query head h reads kv head h // G."""
+
+    rng = np.random.default_rng(Hq * 31 + Hkv * 7 + splits)
+    B = 2
+    seg, k, v = _two_segments(rng, B, Hkv, T0=203, n1=150, start=90, ring_blocks=7)
+    q = _bf(rng, (B, Hq, 1, 128))
+    lse = torch.empty((B, Hq), dtype=torch.float32, device=DEV)
+    out = ops.decode_attention(_t(q), num_splits=splits, lse=lse, **seg)
+    want, want_lse = A.attention(q, k, v)
+    _close(out, bf16.round_bf16(want[:, :, 0].astype(np.float32)), f"decode G={Hq // Hkv} Hkv={Hkv} S={splits}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse[:, :, 0], rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("L,Hq,Hkv", [(40, 16, 1), (17, 6, 2), (9, 3, 1), (70, 20, 4)])
+def test_prefill_gqa_group_sizes_causal(L, Hq, Hkv):
+    """Prefill rows are (token, head) pairs of one GQA group: groups 16, 3, 5, with the causal
+    limit of each query token over the local segment (its last L tokens are the queries' own)."""
+
+    rng = np.random.default_rng(L * 13 + Hq + Hkv)
+    B = 2
+    seg, k, v = _two_segments(rng, B, Hkv, T0=96, n1=L + 45, start=20, ring_blocks=5)
+    q = _bf(rng, (B, L, Hq, 128))
+    lse = torch.empty((B, L, Hq), dtype=torch.float32, device=DEV)
+    out = ops.prefill_attention(_t(q), causal=True, lse=lse, **seg)
+    want, want_lse = A.attention(q.transpose(0, 2, 1, 3), k, v, causal_bottom_right=True)
+    _close(out, bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32)), f"prefill G={Hq // Hkv} L={L}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
