@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 4
+#define LKV_ABI_VERSION 5
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -210,6 +210,9 @@ typedef struct lkv_prefill_args {
   int64_t local_table_stride;
   int64_t local_page_stride;
   int32_t local_num_pages;
+  /* Waves per workgroup of the tile kernel for calls with more than 64 query rows per kv head:
+   * 0 = chosen from the grid and the device's CU count, or 4 / 8 (each wave takes 32 rows). */
+  int32_t tile_waves;
 } lkv_prefill_args;
 
 /* Workspace bytes lkv_prefill_attn needs for these args: the fp16 V of every key block of every

@@ -11,7 +11,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class LastKVNativeError(RuntimeError):
@@ -126,6 +126,7 @@ class PrefillArgs(ctypes.Structure):
         ("local_table_stride", c_i64),
         ("local_page_stride", c_i64),
         ("local_num_pages", c_i32),
+        ("tile_waves", c_i32),
     ]
 
 

@@ -547,12 +547,28 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.vscale_mode = a->older_vscale_mode;
   p.v16 = static_cast<uint16_t*>(a->workspace);
   p.v16_blocks = static_cast<int32_t>(vblocks);
+  LKV_REQUIRE(a->tile_waves == 0 || a->tile_waves == 4 || a->tile_waves == 8, "tile_waves must be 0, 4 or 8, got %d",
+              a->tile_waves);
   const int64_t rows = static_cast<int64_t>(a->tokens) * group;
-  // wide: 8 waves x 32 rows (two waves per SIMD); narrow: 2 waves x 32 rows for short calls
+  const int64_t heads = static_cast<int64_t>(a->num_kv_heads) * a->batch;
+  // Each wave takes 32 query rows.  Short calls (<= 64 rows per kv head): 2 waves.  Otherwise 8
+  // waves (two per SIMD, one workgroup per CU) or 4 waves (two workgroups per CU, whose barriers do
+  // not wait on each other).  Measured on 256 CUs, 4 waves win when the 4-wave grid still leaves
+  // at most one workgroup per CU (twice the CUs busy) and when the 8-wave grid covers the CUs 8
+  // times or more (finer tiles even out the causal work, and the two workgroups of a CU overlap
+  // their barrier waits); for one to eight rounds of 8-wave tiles the 8-wave tile is as fast or faster.
   const bool wide = rows > 64;
-  const int64_t rows_per_wg = wide ? 8 * 32 : 2 * 32;
+  int waves = wide ? 8 : 2;
+  if (wide && a->tile_waves != 0) {
+    waves = a->tile_waves;
+  } else if (wide) {
+    const int64_t cus = device_cu_count();
+    const int64_t wgs8 = (rows + 255) / 256 * heads, wgs4 = (rows + 127) / 128 * heads;
+    if (cus > 0 && (wgs4 <= cus || wgs8 >= 8 * cus)) waves = 4;
+  }
+  const int64_t rows_per_wg = waves * 32;
   const int64_t tiles = (rows + rows_per_wg - 1) / rows_per_wg;
-  const int64_t wgs = tiles * a->num_kv_heads * a->batch;
+  const int64_t wgs = tiles * heads;
   LKV_REQUIRE(wgs < (1LL << 31), "too many query rows");
   p.tiles = static_cast<int32_t>(tiles);
   p.hkv = a->num_kv_heads;
@@ -567,10 +583,14 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
     if (const int32_t e = check_launch("lkv_prefill_attn (V pre-pass)")) return e;
   }
   const dim3 grid(static_cast<unsigned>(wgs));
-  if (wide && paged)
+  if (waves == 8 && paged)
     prefill_kernel<8, 2, 2, true><<<grid, 8 * 64, 0, s>>>(p);
-  else if (wide)
+  else if (waves == 8)
     prefill_kernel<8, 2, 2, false><<<grid, 8 * 64, 0, s>>>(p);
+  else if (waves == 4 && paged)
+    prefill_kernel<4, 2, 2, true><<<grid, 4 * 64, 0, s>>>(p);
+  else if (waves == 4)
+    prefill_kernel<4, 2, 2, false><<<grid, 4 * 64, 0, s>>>(p);
   else if (paged)
     prefill_kernel<2, 2, 1, true><<<grid, 2 * 64, 0, s>>>(p);
   else

@@ -19,6 +19,9 @@ inline hipStream_t as_stream(lkv_stream_t s) { return reinterpret_cast<hipStream
 
 void clear_error();
 
+// Compute units of the current device (cached per device); 0 when the query fails.
+int device_cu_count();
+
 }  // namespace lkv
 
 #define LKV_REQUIRE(cond, ...)                                       \

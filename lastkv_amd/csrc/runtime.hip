@@ -1,6 +1,7 @@
 // Error state and version of the C ABI.
 #include "runtime.h"
 
+#include <atomic>
 #include <cstdio>
 
 namespace lkv {
@@ -24,6 +25,17 @@ int32_t check_launch(const char* what) {
 }
 
 void clear_error() { g_error[0] = '\0'; }
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0 && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+    cached[dev].store(n, std::memory_order_relaxed);
+  return n > 0 ? n : 0;
+}
 
 }  // namespace lkv
 

@@ -383,13 +383,16 @@ def prefill_attention(
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    tile_waves: int = 0,
 ) -> torch.Tensor:
     """Attention of ``q`` ``[B, L, Hq, 128]`` (L query tokens per sequence, the last L tokens of
     the local segment) over ``[older | local]``; the local segment is bottom-right causal
     (``causal``) or fully visible.  Returns ``out`` ``[B, L, Hq, 128]`` bf16.
 
     ``workspace`` (uint8, 16-byte aligned, at least ``prefill_workspace_bytes`` of the same
-    arguments) receives the fp16 V of every key block; without it one is allocated per call."""
+    arguments) receives the fp16 V of every key block; without it one is allocated per call.
+    ``tile_waves`` (0, 4 or 8) fixes the workgroup size of the tile kernel; 0 lets the library
+    choose from the grid size and the device's CU count."""
 
     _require_bf16_cuda("q", q)
     _require(q.dim() == 4 and q.shape[-1] == HEAD_DIM, "q must be [B, L, Hq, 128]")
@@ -412,6 +415,7 @@ def prefill_attention(
     a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = B, L, Hq, Hkv, HEAD_DIM
     a.sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
     a.causal = 1 if causal else 0
+    a.tile_waves = int(tile_waves)
     a.q, a.q_stride_b, a.q_stride_t = q.data_ptr(), q.stride(0), q.stride(1)
     a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
     a.lse = _ptr(lse)

@@ -124,6 +124,40 @@ def test_prefill_bidirectional_local_segment(L, Hq, Hkv, T0, n_local):
     _close(out, bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32)), f"bidirectional L={L} Hq={Hq}")
 
 
+@pytest.mark.parametrize("L,Hq,Hkv,causal", [(300, 8, 2, True), (129, 12, 12, False), (520, 32, 8, True)])
+def test_prefill_tile_waves_agree_and_match_oracle(L, Hq, Hkv, causal):
+    """The 4-wave and 8-wave tiles give the same bits (blocks past a row's causal limit add exact
+    zeros), and both match the oracle; 4 x 32 and 8 x 32 row tiles end at different rows, so
+    tile edges fall inside GQA groups and causal steps."""
+
+    rng = np.random.default_rng(L + Hq)
+    B, T0, n_local = 2, 233, L + 61
+    q = _bf(rng, (B, L, Hq, 128))
+    ok, ov = _bf(rng, (B, Hkv, T0, 128)), _bf(rng, (B, Hkv, T0, 128))
+    lk, lv = _bf(rng, (B, Hkv, n_local, 128)), _bf(rng, (B, Hkv, n_local, 128))
+    older = ops.TiledKV.zeros(B, Hkv, -(-T0 // 32) * 32, DEV)
+    ops.pack_kv(_t(ok), _t(ov), older)
+    ring_tokens = -(-n_local // 32) * 32 + 32
+    ring = ops.TiledKV.zeros(B, Hkv, ring_tokens, DEV)
+    start = ring_tokens - 40  # the segment wraps
+    ops.pack_kv(_t(lk[:, :, :40]), _t(lv[:, :, :40]), ring, token0=start)
+    ops.pack_kv(_t(lk[:, :, 40:]), _t(lv[:, :, 40:]), ring, token0=0)
+    kw = dict(older=older, older_len=T0, local=ring, local_len=n_local, local_start=start, causal=causal)
+    outs, lses = [], []
+    for tw in (4, 8, 0):
+        lse = torch.empty((B, L, Hq), dtype=torch.float32, device=DEV)
+        outs.append(ops.prefill_attention(_t(q), tile_waves=tw, lse=lse, **kw))
+        lses.append(lse)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    assert torch.equal(lses[0], lses[1]) and torch.equal(lses[0], lses[2])
+    want, want_lse = A.attention(q.transpose(0, 2, 1, 3), np.concatenate([ok, lk], 2), np.concatenate([ov, lv], 2),
+                                 causal_bottom_right=causal)
+    _close(outs[0], bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32)), f"tile waves L={L} Hq={Hq}")
+    np.testing.assert_allclose(lses[0].cpu().numpy(), want_lse.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
+    with pytest.raises(RuntimeError, match="tile_waves"):
+        ops.prefill_attention(_t(q), tile_waves=5, **kw)
+
+
 def test_prefill_agrees_with_decode_for_single_token():
     rng = np.random.default_rng(5)
     B, Hq, Hkv, C, p = 3, 16, 4, 64, 250

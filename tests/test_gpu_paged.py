@@ -86,9 +86,10 @@ def test_prefill_paged_equals_contiguous(L, older_len, local_len, start, causal)
         seg_c.update(older=older, older_len=older_len, vscale=vs)
         seg_p.update(older=pool, older_table=otab, older_len=older_len, vscale=vs)
     a = ops.prefill_attention(q, lse=lse_c, **seg_c)
-    b = ops.prefill_attention(q, lse=lse_p, **seg_p)
-    assert torch.equal(a, b)
-    assert torch.equal(lse_c, lse_p)
+    for tw in (0, 4, 8):
+        b = ops.prefill_attention(q, lse=lse_p, tile_waves=tw, **seg_p)
+        assert torch.equal(a, b), f"tile_waves={tw}"
+        assert torch.equal(lse_c, lse_p), f"tile_waves={tw}"
 
 
 def test_corrupt_page_ids_stay_inside_the_pool():
