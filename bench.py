@@ -233,6 +233,7 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
             out = model(ids[:, s:s + call], past_key_values=cache, logits_to_keep=1)
         torch.cuda.synchronize()
         t_prefill = time.perf_counter() - t0
+        hf_logits = out.logits[:, -1].float()
         tok = out.logits[:, -1].argmax(-1, keepdim=True)
         generated = [tok]
         torch.cuda.synchronize()
@@ -244,6 +245,26 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
         torch.cuda.synchronize()
         t_decode = time.perf_counter() - t0
     ids_hf = torch.cat(generated, 1)
+    del cache, out
+    torch.cuda.empty_cache()
+    # Noise floor of this random-weight bf16 model: the same drop-in prefill with every RMSNorm's
+    # eps scaled by 1 + 1e-4 (far below bf16 resolution).  One changed rounding anywhere grows
+    # through the layers' bf16 roundings, so two equally valid bf16 evaluations of the model sit
+    # about this far apart.
+    from lastkv_amd.llm.modeling import RMSNorm
+
+    norms = [m for m in model.modules() if isinstance(m, RMSNorm)]
+    for m in norms:
+        m.variance_epsilon *= 1 + 1e-4
+    try:
+        cache = LastKVCache(cfg.num_hidden_layers, CHUNK, capacity_tokens=prompt)
+        with torch.no_grad():
+            for s in range(0, prompt, call):
+                out = model(ids[:, s:s + call], past_key_values=cache, logits_to_keep=1)
+        floor = float((out.logits[:, -1].float() - hf_logits).norm() / hf_logits.norm())
+    finally:
+        for m in norms:
+            m.variance_epsilon /= 1 + 1e-4
     del cache, out
     torch.cuda.empty_cache()
 
@@ -260,7 +281,9 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
             logits = runner.step([(slot, ids[b, s:s + CHUNK]) for b, slot in enumerate(slots)])
         torch.cuda.synchronize()
         t_sprefill = time.perf_counter() - t0
+        sv_logits = logits.float()
         tok = logits.argmax(-1)
+        first = tok.clone()
         graph = runner.decode_graph(slots)
         _, tok = graph.step(tok)  # capture + first replay, untimed
         served = [tok.clone()]
@@ -271,9 +294,11 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
             served.append(tok.clone())
         torch.cuda.synchronize()
         t_sdecode = time.perf_counter() - t0
-    ids_served = torch.stack(served, 1)
-    same = (ids_hf[:, 1:1 + ids_served.shape[1]] == ids_served[:, : ids_hf.shape[1] - 1]).all(0).tolist()
-    agreement = next((i for i, ok in enumerate(same) if not ok), len(same))
+    ids_served = torch.cat([first.view(-1, 1), torch.stack(served, 1)], 1)
+    n = min(ids_hf.shape[1], ids_served.shape[1])
+    # per sequence: how many leading generated tokens (the prefill's argmax first) the paths share
+    prefix = (ids_hf[:, :n] == ids_served[:, :n]).int().cumprod(1).sum(1).cpu()
+    rel_l2 = float((sv_logits - hf_logits).norm() / hf_logits.norm())
     del runner, graph, model
     torch.cuda.empty_cache()
     return {
@@ -292,10 +317,18 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
             "decode_ms_per_step": round(t_sdecode * 1e3 / (decode_steps - 1), 3),
             "decode_tok_s": round(Bm * (decode_steps - 1) / t_sdecode, 1),
         },
-        # leading decode steps on which all 32 greedy ids agree between the two paths: the serving
-        # path's fused RMSNorm sums in another order than torch's (last-bit differences now and
-        # then) and random-weight logits are near-flat, so the paths part after a few steps
-        "greedy_agreement_steps": agreement,
+        # The serving path's fused RMSNorm sums its squares in another order than torch's norm
+        # (about 1 element in 1e5 differs by one bf16 ulp; with torch's norm in its place the two
+        # paths give identical logits), and that difference grows through the 32 layers like any
+        # other changed rounding: logits after the prompt (rel-L2 between the paths, next to the
+        # model's noise floor above) and each sequence's shared greedy prefix.
+        "agreement": {
+            "prefill_logits_rel_l2": round(rel_l2, 5),
+            "noise_floor_rel_l2": round(floor, 5),
+            "first_token_same": int((prefix > 0).sum()),
+            "greedy_prefix_tokens": {"min": int(prefix.min()), "median": int(prefix.median()),
+                                     "max": int(prefix.max()), "of": n, "sequences": int(prefix.numel())},
+        },
     }
 
 
