@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 5
+#define LKV_ABI_VERSION 6
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -137,6 +137,11 @@ typedef struct lkv_decode_args {
   int64_t local_table_stride;
   int64_t local_page_stride;
   int32_t local_num_pages;
+  /* Cache policy of the K/V loads: 0 = automatic (non-temporal when the call's K/V, bounded by the
+   * segment lengths or capacities, exceed 384 MiB: more than the 256 MB last-level cache could
+   * keep for the next layer's call over the same shared cache), 1 = default policy, 2 =
+   * non-temporal.  Results do not depend on it. */
+  int32_t kv_cache_hint;
 } lkv_decode_args;
 
 int64_t lkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_splits);

@@ -11,7 +11,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class LastKVNativeError(RuntimeError):
@@ -72,6 +72,7 @@ class DecodeArgs(ctypes.Structure):
         ("local_table_stride", c_i64),
         ("local_page_stride", c_i64),
         ("local_num_pages", c_i32),
+        ("kv_cache_hint", c_i32),
     ]
 
 

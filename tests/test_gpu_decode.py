@@ -193,6 +193,9 @@ def test_config2_split_invariance_and_power_of_two_vscale_linearity(config2):
     two = torch.full((8,), 2.0, dtype=torch.float32, device=DEV)
     scaled = ops.decode_attention(q, older=cache, older_len=8192, vscale=two, num_splits=1)
     assert torch.equal(scaled, base * 2)
+    # the 1 GiB cache takes non-temporal K/V loads by default; the default cache policy gives the same bits
+    for hint in (1, 2):
+        assert torch.equal(ops.decode_attention(q, older=cache, older_len=8192, num_splits=1, kv_cache_hint=hint), base)
 
 
 def _two_segments(rng, B, Hkv, T0, n1, start, ring_blocks):
@@ -249,3 +252,26 @@ def test_prefill_gqa_group_sizes_causal(L, Hq, Hkv):
     want, want_lse = A.attention(q.transpose(0, 2, 1, 3), k, v, causal_bottom_right=True)
     _close(out, bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32)), f"prefill G={Hq // Hkv} L={L}")
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("splits", [1, 3])
+def test_decode_kv_cache_hint_does_not_change_results(splits):
+    """Default and non-temporal K/V loads (and the automatic choice) give the same bits, and
+    both match the oracle; an unknown hint is rejected."""
+
+    rng = np.random.default_rng(40 + splits)
+    B, Hq, Hkv = 3, 16, 4
+    seg, k, v = _two_segments(rng, B, Hkv, T0=517, n1=77, start=150, ring_blocks=6)
+    q = _bf(rng, (B, Hq, 1, 128))
+    outs, lses = [], []
+    for hint in (0, 1, 2):
+        lse = torch.empty((B, Hq), dtype=torch.float32, device=DEV)
+        outs.append(ops.decode_attention(_t(q), num_splits=splits, lse=lse, kv_cache_hint=hint, **seg))
+        lses.append(lse)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+    assert torch.equal(lses[0], lses[1]) and torch.equal(lses[1], lses[2])
+    want, want_lse = A.attention(q, k, v)
+    _close(outs[2], bf16.round_bf16(want[:, :, 0].astype(np.float32)), f"decode nt S={splits}")
+    np.testing.assert_allclose(lses[2].cpu().numpy(), want_lse[:, :, 0], rtol=1e-4, atol=1e-4)
+    with pytest.raises(RuntimeError, match="kv_cache_hint"):
+        ops.decode_attention(_t(q), num_splits=splits, kv_cache_hint=3, **seg)
