@@ -172,25 +172,35 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) st.o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  int blk = blk_begin + wave;
-  if (blk < blk_end) {
-    const int last = blk + ((blk_end - 1 - blk) / kWaves) * kWaves;
+  // this wave's blocks: blk_begin + wave + kWaves * t, t < nw; block t + 1 is loaded while block
+  // t is computed.  The loop runs while two or more blocks remain, so its loads are unconditional
+  // (the compiler then counts them exactly for s_waitcnt); the last one or two blocks follow it.
+  const int first = blk_begin + wave;
+  if (first < blk_end) {
+    const int nw = (blk_end - 1 - first) / kWaves + 1;
     BlockFrags fa, fb;
-    BlockRef ra = block_ref(sv, blk);
+    BlockRef ra = block_ref(sv, first);
     load_block<kNT>(fa, ra, n16, g4);
-    // The prefetch of the block after the last one re-reads the last block (an L2 hit), which
-    // keeps the loads unconditional so the compiler can count them for s_waitcnt.
-    while (true) {
-      const BlockRef rb = block_ref(sv, min(blk + kWaves, last));
+    int t = 0;
+    // (the scheduling barriers keep the block being computed from moving above the next block's
+    // loads, where reusing its registers would make the loads wait for it)
+    for (; t + 2 < nw; t += 2) {
+      const BlockRef rb = block_ref(sv, first + kWaves * (t + 1));
+      load_block<kNT>(fb, rb, n16, g4);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_block<kVScale>(fa, ra, qf, vs, p.scale_log2, n16, g4, st);
+      ra = block_ref(sv, first + kWaves * (t + 2));
+      load_block<kNT>(fa, ra, n16, g4);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_block<kVScale>(fb, rb, qf, vs, p.scale_log2, n16, g4, st);
+    }
+    if (t + 1 < nw) {
+      const BlockRef rb = block_ref(sv, first + kWaves * (t + 1));
       load_block<kNT>(fb, rb, n16, g4);
       compute_block<kVScale>(fa, ra, qf, vs, p.scale_log2, n16, g4, st);
-      if (blk + kWaves > last) break;
-      blk += kWaves;
-      ra = block_ref(sv, min(blk + kWaves, last));
-      load_block<kNT>(fa, ra, n16, g4);
       compute_block<kVScale>(fb, rb, qf, vs, p.scale_log2, n16, g4, st);
-      if (blk + kWaves > last) break;
-      blk += kWaves;
+    } else {
+      compute_block<kVScale>(fa, ra, qf, vs, p.scale_log2, n16, g4, st);
     }
   }
 
