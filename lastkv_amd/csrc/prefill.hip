@@ -150,28 +150,28 @@ __device__ inline float max8(const float (&s)[8]) {
 }
 
 // Online-softmax state of one 16-row column group: m = the row's score reference (raw scores),
-// mc = m * c, the exp2 offset (0 while m = -inf), l = this lane's part of the row sum.
+// mc = m * c, the exp2 offset (0 while m = -inf).
 // Probabilities are P = 2^(s c - mc).  m is the exact row maximum after the first block; later it
 // is raised only when some P reaches 2 (a new maximum more than 1 / c above m), so P < 2 always
 // and fp16 keeps its full 11-bit precision.  O / l does not depend on the offset.
 struct RowState {
-  float m, mc, l;
+  float m, mc;
 };
 
-// Raises each row's reference to its maximum over this block (lm = lane maxima) and rescales l
-// and O by 2^(mc_old - mc_new).  Runs for the first block and in a wave-uniform branch taken
-// whenever some P reached 2.
-__device__ inline void raise_rows(RowState& rs, float lm, float c, f32x4 (&o)[8]) {
+// Raises each row's reference to its maximum over this block (lm = lane maxima) and rescales O
+// and the row sums by 2^(mc_old - mc_new).  Runs for the first block and in a wave-uniform branch
+// taken whenever some P reached 2.
+__device__ inline void raise_rows(RowState& rs, float lm, float c, f32x4 (&o)[8], f32x4& ol) {
   const float bm = wave_max_across_rows(lm);
   const bool up = bm > rs.m;  // m = -inf: true for the first finite maximum
   const float mc_new = up ? bm * c : rs.mc;
   const float alpha = up ? fast_exp2(rs.mc - mc_new) : 1.f;  // l and O are 0 while m = -inf
   rs.m = up ? bm : rs.m;
   rs.mc = rs.m == kNegInf ? 0.f : mc_new;
-  rs.l *= alpha;
   if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) o[nb] *= alpha;
+    ol *= alpha;
   }
 }
 
@@ -186,10 +186,6 @@ __device__ inline void probs(const float (&s)[8], float c, float mc, float (&pr)
 // Nonzero when some packed fp16 probability is >= 2 (exponent field >= 16), infinite or NaN.
 __device__ inline uint32_t probs_overflow(const uint32_t (&w)[4]) {
   return (w[0] | w[1] | w[2] | w[3]) & 0x40004000u;
-}
-
-__device__ inline float sum8(const float (&pr)[8]) {
-  return ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
 }
 
 template <int N>
@@ -280,12 +276,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
 
   RowState rs[CG];
 #pragma unroll
-  for (int cg = 0; cg < CG; ++cg) rs[cg] = RowState{kNegInf, 0.f, 0.f};
-  f32x4 o[CG][8];
+  for (int cg = 0; cg < CG; ++cg) rs[cg] = RowState{kNegInf, 0.f};
+  // O^T tiles (lane (n16, g4): dims 16 nb + 4 g4 + i of row n16) and the row sums of the fp16 P,
+  // accumulated on the matrix pipe as P times a tile of ones (each lane holds its row's sum).
+  f32x4 o[CG][8], ol[CG];
+  const uint4 kOnes = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
 #pragma unroll
-  for (int cg = 0; cg < CG; ++cg)
+  for (int cg = 0; cg < CG; ++cg) {
+    ol[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) o[cg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   if (nbt > 0) {
     SegBase rsrc;
@@ -341,7 +342,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
         for (int cg = 0; cg < CG; ++cg) mask_scores(s0[cg], r0, lim[cg], g4);
       }
 #pragma unroll
-      for (int cg = 0; cg < CG; ++cg) raise_rows(rs[cg], max8(s0[cg]), c, o[cg]);
+      for (int cg = 0; cg < CG; ++cg) raise_rows(rs[cg], max8(s0[cg]), c, o[cg], ol[cg]);
     }
 
     // Step i: the 16 LDS reads (K of block i + 1, V of block i) are issued first so their latency
@@ -388,12 +389,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
           sc[cg][1] = mfma_bf16(kf[4 + kb], qf[cg][kb], sc[cg][1]);
         }
       uint32_t pw[CG][4];
-      float lb[CG];  // this block's contribution to l
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) {
         float pr[8];
         probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
-        lb[cg] = sum8(pr);
       }
       uint4 vf[8];
 #pragma unroll
@@ -411,10 +410,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
       if (__builtin_amdgcn_ballot_w64(ovf != 0)) {
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
-          raise_rows(rs[cg], max8(s[cg]), c, o[cg]);
+          raise_rows(rs[cg], max8(s[cg]), c, o[cg], ol[cg]);
           float pr[8];
           probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
-          lb[cg] = sum8(pr);
         }
       }
 #pragma unroll
@@ -423,12 +421,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
         for (int cg = 0; cg < CG; ++cg)
           o[cg][nb] = mfma_f16(vf[nb], make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]), o[cg][nb]);
 #pragma unroll
-      for (int cg = 0; cg < CG; ++cg) rs[cg].l += lb[cg];
+      for (int cg = 0; cg < CG; ++cg) ol[cg] = mfma_f16(kOnes, make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]), ol[cg]);
       stage_store<NW>(st, wr, wave, lane);
       stage_load<NW>(st, rsrc, ld_k, ld_blk, wave, lane_off);
 #pragma unroll
-      for (int i = 0; i < 8 * CG; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (P V of block i)
+      for (int i = 0; i < 9 * CG; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (P V and P 1 of block i)
         __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
       }
       __syncthreads();
@@ -455,7 +453,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   // normalise and write: lane (n16, g4) holds dims 16 * nb + 4 * g4 + i of row n16 of each group
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
-    const float lt = wave_sum_across_rows(rs[cg].l);
+    const float lt = ol[cg][0];
     const float linv = lt > 0.f ? 1.f / lt : 0.f;
     const int row = row0 + 16 * cg + n16;
     if (row < rows_total) {
