@@ -511,6 +511,8 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   LKV_REQUIRE(a->num_q_heads % a->num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
   const int group = a->num_q_heads / a->num_kv_heads;
   LKV_REQUIRE(a->causal == 0 || a->causal == 1, "causal must be 0 or 1");
+  LKV_REQUIRE(a->tile_waves == 0 || a->tile_waves == 4 || a->tile_waves == 8, "tile_waves must be 0, 4 or 8, got %d",
+              a->tile_waves);
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->older_vscale_mode == 1, "older_vscale_mode must be 0 or 1");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->vscale != nullptr, "older_vscale_mode 1 needs vscale");
   LKV_REQUIRE(a->q != nullptr && a->out != nullptr, "null q/out");
@@ -545,8 +547,6 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.vscale_mode = a->older_vscale_mode;
   p.v16 = static_cast<uint16_t*>(a->workspace);
   p.v16_blocks = static_cast<int32_t>(vblocks);
-  LKV_REQUIRE(a->tile_waves == 0 || a->tile_waves == 4 || a->tile_waves == 8, "tile_waves must be 0, 4 or 8, got %d",
-              a->tile_waves);
   const int64_t rows = static_cast<int64_t>(a->tokens) * group;
   const int64_t heads = static_cast<int64_t>(a->num_kv_heads) * a->batch;
   // Each wave takes 32 query rows.  Short calls (<= 64 rows per kv head): 2 waves.  Otherwise 8

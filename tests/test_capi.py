@@ -47,6 +47,7 @@ def test_abi_version_and_struct_size_guard():
         ("num_kv_heads", 3, b"multiple"),
         ("num_splits", 0, b"num_splits"),
         ("older_vscale_mode", 1, b"vscale"),
+        ("kv_cache_hint", 3, b"kv_cache_hint"),
     ],
 )
 def test_decode_rejects_bad_arguments_before_any_launch(field, value, message):
@@ -70,3 +71,19 @@ def test_pack_rejects_capacity_overflow():
     lib = _lib.load()
     st = lib.lkv_cache_pack(16, 0, 0, 128, 1, 1, 40, 0, 16, 0, 0, 0, 32, None)
     assert st == 1 and b"capacity" in lib.lkv_last_error()
+
+
+@pytest.mark.parametrize("field,value,message", [("tile_waves", 5, b"tile_waves"), ("causal", 2, b"causal"),
+                                                 ("head_dim", 96, b"head_dim")])
+@pytest.mark.parametrize("batch", [0, 1])
+def test_prefill_rejects_bad_arguments_before_any_launch(field, value, message, batch):
+    """Checked before the empty-call early return, so a bad value never passes silently."""
+
+    lib = _lib.load()
+    a = _lib.PrefillArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim, a.causal = batch, 4, 8, 2, 128, 1
+    a.q = a.out = 16
+    setattr(a, field, value)
+    assert lib.lkv_prefill_attn(ctypes.byref(a), None) == 1
+    assert message in lib.lkv_last_error()
