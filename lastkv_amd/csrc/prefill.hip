@@ -397,6 +397,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
       uint4 vf[8];
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) vf[nb] = cur[512 + nb * 64 + lane];
+      // the first probabilities go ahead of the first MFMA, which waits for the K fragments
+      // just read from LDS (in-order issue would otherwise hold every exp behind that wait)
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x400, 4, 0);  // exp
 #pragma unroll
       for (int i = 0; i < 8 * CG; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (QK^T of block i + 1)
