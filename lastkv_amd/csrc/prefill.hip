@@ -432,6 +432,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
       for (int i = 0; i < 9 * CG; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (P V and P 1 of block i)
         __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write (staging of block i + 2)
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (load of block i + 4)
       }
       __syncthreads();
     };
