@@ -398,9 +398,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) vf[nb] = cur[512 + nb * 64 + lane];
       // the first probabilities go ahead of the first MFMA, which waits for the K fragments
-      // just read from LDS (in-order issue would otherwise hold every exp behind that wait)
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
-      __builtin_amdgcn_sched_group_barrier(0x400, 4, 0);  // exp
+      // just read from LDS (in-order issue would otherwise hold every exp behind that wait);
+      // measured best: 4 with 4-wave tiles, 2 with 8-wave tiles
+      __builtin_amdgcn_sched_group_barrier(0x002, NW == 8 ? 2 : 4, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x400, NW == 8 ? 2 : 4, 0);  // exp
 #pragma unroll
       for (int i = 0; i < 8 * CG; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (QK^T of block i + 1)
