@@ -26,15 +26,16 @@ constexpr float kNegInf = -__builtin_inff();
 
 struct DecodeParams {
   const uint16_t* q;
-  int64_t q_sb;
+  int64_t q_sb, q_st;
   uint16_t* out;
-  int64_t out_sb;
+  int64_t out_sb, out_st;
   float* lse;
   SegParams seg;
   const float* vscale;
   float* ws_o;
   float* ws_ml;
   int32_t hq, group, splits;
+  int32_t L, causal;  // query tokens per sequence (1 for decode calls) and bottom-right causality
   float scale_log2;
 };
 
@@ -65,9 +66,11 @@ struct SoftmaxState {
   f32x4 o[8];  // O rows (heads 4*g4 + i) x dims 16*nb + n16
 };
 
-template <bool kVScale>
+// kMulti: the columns are (query token, head) pairs; lim is this lane's column's last visible local
+// token and lim_min the smallest over the columns (local blocks past it need the causal mask).
+template <bool kVScale, bool kMulti>
 __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, const uint4 (&qf)[4], float vs,
-                                     float scale_log2, int n16, int g4, SoftmaxState& st) {
+                                     float scale_log2, int n16, int g4, int lim, int lim_min, SoftmaxState& st) {
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
@@ -81,10 +84,10 @@ __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, con
     s[i] = s0[i] * scale_log2;
     s[4 + i] = s1[i] * scale_log2;
   }
-  if (r.lo > 0 || r.hi < kBlockTokens) {
+  if (r.lo > 0 || r.hi < kBlockTokens || (kMulti && !r.older && r.seg_tok + kBlockTokens - 1 > lim_min)) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (8 * g4 + j < r.lo || 8 * g4 + j >= r.hi) s[j] = kNegInf;
+      if (8 * g4 + j < r.lo || 8 * g4 + j >= r.hi || (kMulti && !r.older && r.seg_tok + 8 * g4 + j > lim)) s[j] = kNegInf;
   }
   float mx = s[0];
 #pragma unroll
@@ -139,7 +142,9 @@ __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, con
   }
 }
 
-template <bool kVScale, bool kNT>
+// kMulti: L > 1 query tokens per sequence, column c of the score tile = (token c / G, head c % G),
+// G * L <= 16 (short prefill calls); otherwise column c = head c (L = 1).
+template <bool kVScale, bool kNT, bool kMulti>
 __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p) {
   __shared__ float sm_m[kWaves][16];
   __shared__ float sm_l[kWaves][16];
@@ -157,12 +162,19 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   const int blk_begin = split * bps;
   const int blk_end = min(blk_begin + bps, nbt);
 
+  const int cols = kMulti ? G * p.L : G;
   uint4 qf[4];
+  int lim = 0, lim_min = 0;  // causal limits (local token index) of this lane's column and of column 0
   {
-    const uint16_t* qrow = p.q + b * p.q_sb + static_cast<int64_t>(kvh * G + n16) * kHeadDim;
+    const int t = kMulti ? n16 / G : 0, h = n16 - t * G;
+    const uint16_t* qrow = p.q + b * p.q_sb + (kMulti ? t * p.q_st : 0) + static_cast<int64_t>(kvh * G + h) * kHeadDim;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-      qf[kb] = n16 < G ? *reinterpret_cast<const uint4*>(qrow + 32 * kb + 8 * g4) : make_uint4(0, 0, 0, 0);
+      qf[kb] = n16 < cols ? *reinterpret_cast<const uint4*>(qrow + 32 * kb + 8 * g4) : make_uint4(0, 0, 0, 0);
+    if (kMulti) {
+      lim_min = p.causal ? sv.n1 - p.L : sv.n1 - 1;
+      lim = p.causal ? lim_min + t : lim_min;
+    }
   }
   const float vs = kVScale ? p.vscale[kvh] : 1.f;
 
@@ -188,39 +200,40 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
       const BlockRef rb = block_ref(sv, first + kWaves * (t + 1));
       load_block<kNT>(fb, rb, n16, g4);
       __builtin_amdgcn_sched_barrier(0);
-      compute_block<kVScale>(fa, ra, qf, vs, p.scale_log2, n16, g4, st);
+      compute_block<kVScale, kMulti>(fa, ra, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
       ra = block_ref(sv, first + kWaves * (t + 2));
       load_block<kNT>(fa, ra, n16, g4);
       __builtin_amdgcn_sched_barrier(0);
-      compute_block<kVScale>(fb, rb, qf, vs, p.scale_log2, n16, g4, st);
+      compute_block<kVScale, kMulti>(fb, rb, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
     }
     if (t + 1 < nw) {
       const BlockRef rb = block_ref(sv, first + kWaves * (t + 1));
       load_block<kNT>(fb, rb, n16, g4);
-      compute_block<kVScale>(fa, ra, qf, vs, p.scale_log2, n16, g4, st);
-      compute_block<kVScale>(fb, rb, qf, vs, p.scale_log2, n16, g4, st);
+      compute_block<kVScale, kMulti>(fa, ra, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
+      compute_block<kVScale, kMulti>(fb, rb, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
     } else {
-      compute_block<kVScale>(fa, ra, qf, vs, p.scale_log2, n16, g4, st);
+      compute_block<kVScale, kMulti>(fa, ra, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
     }
   }
 
   // merge the four waves' states
-  if (g4 == 0 && n16 < G) {
+  if (g4 == 0 && n16 < cols) {
     sm_m[wave][n16] = st.m;
     sm_l[wave][n16] = st.l;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int h = 4 * g4 + i;
-    if (h < G) {
+    if (h < cols) {
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) sm_o[wave][h][16 * nb + n16] = st.o[nb][i];
     }
   }
   __syncthreads();
-  const int bh0 = b * p.hq + kvh * G;
-  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += 256) {
-    const int h = idx >> 7, d = idx & (kHeadDim - 1);
+  for (int idx = threadIdx.x; idx < cols * kHeadDim; idx += 256) {
+    const int h = idx >> 7, d = idx & (kHeadDim - 1);  // column h = (token tq, head hh)
+    const int tq = kMulti ? h / G : 0, hh = h - tq * G;
+    const int64_t row_q = (static_cast<int64_t>(b) * (kMulti ? p.L : 1) + tq) * p.hq + kvh * G + hh;  // [B, L, Hq] row
     float M = sm_m[0][h];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
@@ -232,10 +245,11 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
       O += f * sm_o[w][h][d];
     }
     if (p.splits == 1) {
-      p.out[b * p.out_sb + static_cast<int64_t>(kvh * G + h) * kHeadDim + d] = f32_to_bf16_bits(L > 0.f ? O / L : 0.f);
-      if (p.lse != nullptr && d == 0) p.lse[bh0 + h] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
+      p.out[b * p.out_sb + (kMulti ? tq * p.out_st : 0) + static_cast<int64_t>(kvh * G + hh) * kHeadDim + d] =
+          f32_to_bf16_bits(L > 0.f ? O / L : 0.f);
+      if (p.lse != nullptr && d == 0) p.lse[row_q] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
     } else {
-      const int64_t row = static_cast<int64_t>(bh0 + h) * p.splits + split;
+      const int64_t row = row_q * p.splits + split;
       p.ws_o[row * kHeadDim + d] = O;
       if (d == 0) {
         p.ws_ml[row * 2] = M;
@@ -255,9 +269,9 @@ constexpr int kMaxSplits = 1024;
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const DecodeParams p) {
   __shared__ float sm_w[kMaxSplits];
   __shared__ float sm_red[kCombineThreads / 64];
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.x;  // [B, L, Hq] row
   const int d = threadIdx.x;
-  const int b = bh / p.hq, h = bh % p.hq;
+  const int b = bh / (p.L * p.hq), tq = (bh / p.hq) % p.L, h = bh % p.hq;
   const int S = p.splits;
   const float* ml = p.ws_ml + static_cast<int64_t>(bh) * S * 2;
   const float* o = p.ws_o + static_cast<int64_t>(bh) * S * kHeadDim;
@@ -293,11 +307,91 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const D
   }
   for (; s < S; ++s) O[0] += sm_w[s] * o[s * kHeadDim + d];
   const float Ot = (O[0] + O[1]) + (O[2] + O[3]);
-  p.out[b * p.out_sb + static_cast<int64_t>(h) * kHeadDim + d] = f32_to_bf16_bits(L > 0.f ? Ot / L : 0.f);
+  p.out[b * p.out_sb + tq * p.out_st + static_cast<int64_t>(h) * kHeadDim + d] = f32_to_bf16_bits(L > 0.f ? Ot / L : 0.f);
   if (p.lse != nullptr && d == 0) p.lse[bh] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
 }
 
+// Key tokens a call can read per sequence (lengths read from device memory bounded by the
+// capacities); Args is lkv_decode_args or lkv_prefill_args (same segment fields).
+template <typename Args>
+int64_t call_key_tokens(const Args* a) {
+  const int64_t ring_tokens = static_cast<int64_t>(a->local_ring_blocks) * kBlockTokens;
+  const int64_t older = a->older_k == nullptr ? 0
+                                              : (a->older_len != nullptr ? a->older_capacity_tokens
+                                                                         : std::min(a->older_len_const, a->older_capacity_tokens));
+  const int64_t local = a->local_k == nullptr
+                            ? 0
+                            : (a->local_len != nullptr ? ring_tokens : std::min<int64_t>(a->local_len_const, ring_tokens));
+  return std::max<int64_t>(older, 0) + std::max<int64_t>(local, 0);
+}
+
+// Non-temporal K/V loads when a call's K/V exceed 384 MiB (more than the 256 MB last-level cache
+// could keep for the next layer's call over the same shared cache); hint 1 / 2 force a policy.
+bool use_nontemporal(int32_t hint, int64_t kv_bytes) { return hint == 2 || (hint == 0 && kv_bytes > (int64_t{384} << 20)); }
+
+int32_t launch_decode(const DecodeParams& p, dim3 grid, bool vscale, bool nt, bool multi, int rows, hipStream_t s,
+                      const char* what) {
+  if (multi) {
+    if (vscale && nt)
+      decode_split_kernel<true, true, true><<<grid, 256, 0, s>>>(p);
+    else if (vscale)
+      decode_split_kernel<true, false, true><<<grid, 256, 0, s>>>(p);
+    else if (nt)
+      decode_split_kernel<false, true, true><<<grid, 256, 0, s>>>(p);
+    else
+      decode_split_kernel<false, false, true><<<grid, 256, 0, s>>>(p);
+  } else {
+    if (vscale && nt)
+      decode_split_kernel<true, true, false><<<grid, 256, 0, s>>>(p);
+    else if (vscale)
+      decode_split_kernel<true, false, false><<<grid, 256, 0, s>>>(p);
+    else if (nt)
+      decode_split_kernel<false, true, false><<<grid, 256, 0, s>>>(p);
+    else
+      decode_split_kernel<false, false, false><<<grid, 256, 0, s>>>(p);
+  }
+  if (const int32_t st = check_launch(what)) return st;
+  if (p.splits > 1) {
+    decode_combine_kernel<<<rows, kCombineThreads, 0, s>>>(p);
+    return check_launch(what);
+  }
+  return LKV_OK;
+}
+
 }  // namespace
+
+int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, hipStream_t s) {
+  DecodeParams p;
+  p.seg = seg;
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.q_sb = a->q_stride_b;
+  p.q_st = a->q_stride_t;
+  p.out = static_cast<uint16_t*>(a->out);
+  p.out_sb = a->out_stride_b;
+  p.out_st = a->out_stride_t;
+  p.lse = a->lse;
+  p.vscale = a->vscale;
+  p.hq = a->num_q_heads;
+  p.group = group;
+  p.L = a->tokens;
+  p.causal = a->causal;
+  p.scale_log2 = a->sm_scale * kLog2e;
+  const int64_t tokens = call_key_tokens(a);
+  const int64_t blocks = (tokens + 2 * kBlockTokens - 1) / kBlockTokens;  // (+1 for a ring start inside a block)
+  const int64_t pairs = static_cast<int64_t>(a->batch) * a->num_kv_heads;
+  const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  // about one workgroup per CU, at least 4 blocks per split, partial states within the workspace
+  int64_t splits = std::min<int64_t>({(cus + pairs - 1) / pairs, std::max<int64_t>(blocks / 4, 1), 1024});
+  const int64_t rows = static_cast<int64_t>(a->batch) * a->tokens * a->num_q_heads;
+  while (splits > 1 && rows * splits * (kHeadDim + 2) * 4 > a->workspace_bytes) splits = (splits + 1) / 2;
+  p.splits = static_cast<int32_t>(splits);
+  p.ws_o = splits > 1 ? static_cast<float*>(a->workspace) : nullptr;
+  p.ws_ml = splits > 1 ? p.ws_o + rows * splits * kHeadDim : nullptr;
+  const bool nt = use_nontemporal(0, pairs * tokens * kHeadDim * 2 * 2);
+  return launch_decode(p, dim3(p.splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1, nt, true,
+                       static_cast<int>(rows), s, "lkv_prefill_attn (short call on the decode kernel)");
+}
+
 }  // namespace lkv
 
 extern "C" int64_t lkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_splits) {
@@ -336,8 +430,12 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   }
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_stride_b;
+  p.q_st = 0;
   p.out = static_cast<uint16_t*>(a->out);
   p.out_sb = a->out_stride_b;
+  p.out_st = 0;
+  p.L = 1;
+  p.causal = 0;
   p.lse = a->lse;
   p.vscale = a->vscale;
   p.ws_o = static_cast<float*>(a->workspace);
@@ -346,32 +444,8 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   p.group = group;
   p.splits = a->num_splits;
   p.scale_log2 = a->sm_scale * kLog2e;
-  const dim3 grid(a->num_splits, a->num_kv_heads, a->batch);
-  hipStream_t s = as_stream(stream);
-  // K/V bytes the call can read (lengths read from device memory bounded by the capacities)
-  const int64_t ring_tokens = static_cast<int64_t>(a->local_ring_blocks) * kBlockTokens;
-  const int64_t older_tokens =
-      a->older_k == nullptr ? 0
-                            : (a->older_len != nullptr ? a->older_capacity_tokens
-                                                       : std::min(a->older_len_const, a->older_capacity_tokens));
-  const int64_t local_tokens =
-      a->local_k == nullptr ? 0
-                            : (a->local_len != nullptr ? ring_tokens : std::min<int64_t>(a->local_len_const, ring_tokens));
-  const int64_t kv_bytes = static_cast<int64_t>(a->batch) * a->num_kv_heads *
-                           (std::max<int64_t>(older_tokens, 0) + std::max<int64_t>(local_tokens, 0)) * kHeadDim * 2 * 2;
-  const bool nt = a->kv_cache_hint == 2 || (a->kv_cache_hint == 0 && kv_bytes > (int64_t{384} << 20));
-  if (a->older_vscale_mode == 1 && nt)
-    decode_split_kernel<true, true><<<grid, 256, 0, s>>>(p);
-  else if (a->older_vscale_mode == 1)
-    decode_split_kernel<true, false><<<grid, 256, 0, s>>>(p);
-  else if (nt)
-    decode_split_kernel<false, true><<<grid, 256, 0, s>>>(p);
-  else
-    decode_split_kernel<false, false><<<grid, 256, 0, s>>>(p);
-  if (int32_t st = check_launch("lkv_decode_attn split kernel")) return st;
-  if (a->num_splits > 1) {
-    decode_combine_kernel<<<a->batch * a->num_q_heads, kCombineThreads, 0, s>>>(p);
-    return check_launch("lkv_decode_attn combine kernel");
-  }
-  return LKV_OK;
+  const int64_t kv_bytes = static_cast<int64_t>(a->batch) * a->num_kv_heads * call_key_tokens(a) * kHeadDim * 2 * 2;
+  return launch_decode(p, dim3(a->num_splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1,
+                       use_nontemporal(a->kv_cache_hint, kv_bytes), false, a->batch * a->num_q_heads, as_stream(stream),
+                       "lkv_decode_attn");
 }

@@ -275,3 +275,23 @@ def test_decode_kv_cache_hint_does_not_change_results(splits):
     np.testing.assert_allclose(lses[2].cpu().numpy(), want_lse[:, :, 0], rtol=1e-4, atol=1e-4)
     with pytest.raises(RuntimeError, match="kv_cache_hint"):
         ops.decode_attention(_t(q), num_splits=splits, kv_cache_hint=3, **seg)
+
+
+@pytest.mark.parametrize("L,Hq,Hkv,causal,B", [(2, 32, 8, True, 2), (4, 8, 2, True, 3), (3, 15, 3, False, 1),
+                                              (16, 16, 16, True, 2), (1, 64, 4, True, 2), (5, 6, 2, True, 1)])
+def test_short_prefill_on_decode_kernel(L, Hq, Hkv, causal, B):
+    """Prefill calls of at most 16 query rows per kv head run on the decode kernel, one score column
+    per (token, head) with its own causal limit: against the oracle (older V scale, a wrapping ring,
+    split partials combined per (token, head) when the batch is small) and against the tile kernel."""
+
+    rng = np.random.default_rng(L * 100 + Hq + B)
+    seg, k, v = _two_segments(rng, B, Hkv, T0=203, n1=L + 150, start=150, ring_blocks=8)
+    q = _bf(rng, (B, L, Hq, 128))
+    lse = torch.empty((B, L, Hq), dtype=torch.float32, device=DEV)
+    out = ops.prefill_attention(_t(q), causal=causal, lse=lse, **seg)
+    want, want_lse = A.attention(q.transpose(0, 2, 1, 3), k, v, causal_bottom_right=causal)
+    want_out = bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32))
+    _close(out, want_out, f"short prefill L={L} G={Hq // Hkv} B={B}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
+    tile = ops.prefill_attention(_t(q), causal=causal, tile_waves=4, **seg)
+    _close(tile, out.float().cpu().numpy(), f"short prefill tile vs decode kernel L={L}")

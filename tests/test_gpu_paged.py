@@ -69,7 +69,8 @@ def test_decode_paged_equals_contiguous(older_len, local_len, start):
 
 
 @pytest.mark.parametrize("L,older_len,local_len,start,causal", [
-    (64, 640, 96, 200, True), (17, 96, 17, 0, True), (300, 0, 300, 13, False), (100, 1000, 100, 283, True)])
+    (64, 640, 96, 200, True), (17, 96, 17, 0, True), (300, 0, 300, 13, False), (100, 1000, 100, 283, True),
+    (3, 500, 40, 290, True)])
 def test_prefill_paged_equals_contiguous(L, older_len, local_len, start, causal):
     g = torch.Generator(device=DEV).manual_seed(L * 7 + older_len)
     B, Hq, Hkv = 2, 8, 2
@@ -85,8 +86,8 @@ def test_prefill_paged_equals_contiguous(L, older_len, local_len, start, causal)
     if older_len:
         seg_c.update(older=older, older_len=older_len, vscale=vs)
         seg_p.update(older=pool, older_table=otab, older_len=older_len, vscale=vs)
-    a = ops.prefill_attention(q, lse=lse_c, **seg_c)
-    for tw in (0, 4, 8):
+    for tw in (0, 4, 8):  # (L = 3: the decode kernel at 0, the tile kernel otherwise)
+        a = ops.prefill_attention(q, lse=lse_c, tile_waves=tw, **seg_c)
         b = ops.prefill_attention(q, lse=lse_p, tile_waves=tw, **seg_p)
         assert torch.equal(a, b), f"tile_waves={tw}"
         assert torch.equal(lse_c, lse_p), f"tile_waves={tw}"
