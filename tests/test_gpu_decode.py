@@ -183,6 +183,20 @@ def test_config2_full_size_matches_reference_sdpa(config2):
     assert A.max_abs(out.float().cpu().numpy(), ref16.float().cpu().numpy()) <= MAX_ABS
 
 
+def test_config2_two_token_call_on_decode_kernel_matches_tile_kernel(config2):
+    """Full size: two query tokens per sequence over the 1 GiB shared cache (no causal part: the
+    cache is all older history) on the decode kernel's (token, head) columns with non-temporal
+    loads, against the same call on the MFMA tile kernel."""
+
+    q1, _, _, cache = config2
+    q = torch.stack([q1[:, :, 0], q1[:, :, 0].flip(1).contiguous()], 1)  # [32, 2, 32, 128]
+    got = ops.prefill_attention(q, older=cache, older_len=8192, causal=False)
+    tile = ops.prefill_attention(q, older=cache, older_len=8192, causal=False, tile_waves=4)
+    _close(got, tile.float().cpu().numpy(), "config2 two-token call: decode kernel vs tile kernel")
+    one = ops.decode_attention(q1, older=cache, older_len=8192, num_splits=1)
+    assert torch.equal(got[:, 0], one), "token 0 equals the one-token decode call"
+
+
 def test_config2_split_invariance_and_power_of_two_vscale_linearity(config2):
     q, _, _, cache = config2
     base = ops.decode_attention(q, older=cache, older_len=8192, num_splits=1)
