@@ -142,13 +142,14 @@ __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, con
   }
 }
 
-// kMulti: L > 1 query tokens per sequence, column c of the score tile = (token c / G, head c % G),
-// G * L <= 16 (short prefill calls); otherwise column c = head c (L = 1).
-template <bool kVScale, bool kNT, bool kMulti>
+// kMulti: L > 1 query tokens per sequence, column c = (token c / G, head c % G) for c < G * L <=
+// 16 * CG (CG <= 2: four groups spill), in CG groups of 16 columns that share each block's K/V fragments (short prefill calls);
+// otherwise column c = head c (L = 1, CG = 1).
+template <bool kVScale, bool kNT, bool kMulti, int CG = 1>
 __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p) {
-  __shared__ float sm_m[kWaves][16];
-  __shared__ float sm_l[kWaves][16];
-  __shared__ float sm_o[kWaves][16][kHeadDim];
+  __shared__ float sm_m[kWaves][16 * CG];
+  __shared__ float sm_l[kWaves][16 * CG];
+  __shared__ float sm_o[kWaves][16 * CG][kHeadDim];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -163,26 +164,34 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   const int blk_end = min(blk_begin + bps, nbt);
 
   const int cols = kMulti ? G * p.L : G;
-  uint4 qf[4];
-  int lim = 0, lim_min = 0;  // causal limits (local token index) of this lane's column and of column 0
-  {
-    const int t = kMulti ? n16 / G : 0, h = n16 - t * G;
+  uint4 qf[CG][4];
+  int lim[CG], lim_min = 0;  // causal limits (local token index) of this lane's columns and of column 0
+  if (kMulti) lim_min = p.causal ? sv.n1 - p.L : sv.n1 - 1;
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) {
+    const int c = 16 * cg + n16;
+    const int t = kMulti ? c / G : 0, h = c - t * G;
     const uint16_t* qrow = p.q + b * p.q_sb + (kMulti ? t * p.q_st : 0) + static_cast<int64_t>(kvh * G + h) * kHeadDim;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-      qf[kb] = n16 < cols ? *reinterpret_cast<const uint4*>(qrow + 32 * kb + 8 * g4) : make_uint4(0, 0, 0, 0);
-    if (kMulti) {
-      lim_min = p.causal ? sv.n1 - p.L : sv.n1 - 1;
-      lim = p.causal ? lim_min + t : lim_min;
-    }
+      qf[cg][kb] = c < cols ? *reinterpret_cast<const uint4*>(qrow + 32 * kb + 8 * g4) : make_uint4(0, 0, 0, 0);
+    lim[cg] = kMulti && p.causal ? lim_min + t : lim_min;
   }
   const float vs = kVScale ? p.vscale[kvh] : 1.f;
 
-  SoftmaxState st;
-  st.m = kNegInf;
-  st.l = 0.f;
+  SoftmaxState st[CG];
 #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) st.o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int cg = 0; cg < CG; ++cg) {
+    st[cg].m = kNegInf;
+    st[cg].l = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) st[cg].o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  auto compute = [&](const BlockFrags& f, const BlockRef& r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int cg = 0; cg < CG; ++cg)
+      compute_block<kVScale, kMulti>(f, r, qf[cg], vs, p.scale_log2, n16, g4, lim[cg], lim_min, st[cg]);
+  };
 
   // this wave's blocks: blk_begin + wave + kWaves * t, t < nw; block t + 1 is loaded while block
   // t is computed.  The loop runs while two or more blocks remain, so its loads are unconditional
@@ -200,33 +209,36 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
       const BlockRef rb = block_ref(sv, first + kWaves * (t + 1));
       load_block<kNT>(fb, rb, n16, g4);
       __builtin_amdgcn_sched_barrier(0);
-      compute_block<kVScale, kMulti>(fa, ra, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
+      compute(fa, ra);
       ra = block_ref(sv, first + kWaves * (t + 2));
       load_block<kNT>(fa, ra, n16, g4);
       __builtin_amdgcn_sched_barrier(0);
-      compute_block<kVScale, kMulti>(fb, rb, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
+      compute(fb, rb);
     }
     if (t + 1 < nw) {
       const BlockRef rb = block_ref(sv, first + kWaves * (t + 1));
       load_block<kNT>(fb, rb, n16, g4);
-      compute_block<kVScale, kMulti>(fa, ra, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
-      compute_block<kVScale, kMulti>(fb, rb, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
+      compute(fa, ra);
+      compute(fb, rb);
     } else {
-      compute_block<kVScale, kMulti>(fa, ra, qf, vs, p.scale_log2, n16, g4, lim, lim_min, st);
+      compute(fa, ra);
     }
   }
 
   // merge the four waves' states
-  if (g4 == 0 && n16 < cols) {
-    sm_m[wave][n16] = st.m;
-    sm_l[wave][n16] = st.l;
-  }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int h = 4 * g4 + i;
-    if (h < cols) {
+  for (int cg = 0; cg < CG; ++cg) {
+    if (g4 == 0 && 16 * cg + n16 < cols) {
+      sm_m[wave][16 * cg + n16] = st[cg].m;
+      sm_l[wave][16 * cg + n16] = st[cg].l;
+    }
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) sm_o[wave][h][16 * nb + n16] = st.o[nb][i];
+    for (int i = 0; i < 4; ++i) {
+      const int h = 16 * cg + 4 * g4 + i;
+      if (h < cols) {
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) sm_o[wave][h][16 * nb + n16] = st[cg].o[nb][i];
+      }
     }
   }
   __syncthreads();
@@ -329,17 +341,25 @@ int64_t call_key_tokens(const Args* a) {
 // could keep for the next layer's call over the same shared cache); hint 1 / 2 force a policy.
 bool use_nontemporal(int32_t hint, int64_t kv_bytes) { return hint == 2 || (hint == 0 && kv_bytes > (int64_t{384} << 20)); }
 
-int32_t launch_decode(const DecodeParams& p, dim3 grid, bool vscale, bool nt, bool multi, int rows, hipStream_t s,
+template <int CG>
+void launch_multi(const DecodeParams& p, dim3 grid, bool vscale, bool nt, hipStream_t s) {
+  if (vscale && nt)
+    decode_split_kernel<true, true, true, CG><<<grid, 256, 0, s>>>(p);
+  else if (vscale)
+    decode_split_kernel<true, false, true, CG><<<grid, 256, 0, s>>>(p);
+  else if (nt)
+    decode_split_kernel<false, true, true, CG><<<grid, 256, 0, s>>>(p);
+  else
+    decode_split_kernel<false, false, true, CG><<<grid, 256, 0, s>>>(p);
+}
+
+// cg: 0 for decode calls (one column per head), else the 16-column groups of a short prefill call
+int32_t launch_decode(const DecodeParams& p, dim3 grid, bool vscale, bool nt, int cg, int rows, hipStream_t s,
                       const char* what) {
-  if (multi) {
-    if (vscale && nt)
-      decode_split_kernel<true, true, true><<<grid, 256, 0, s>>>(p);
-    else if (vscale)
-      decode_split_kernel<true, false, true><<<grid, 256, 0, s>>>(p);
-    else if (nt)
-      decode_split_kernel<false, true, true><<<grid, 256, 0, s>>>(p);
-    else
-      decode_split_kernel<false, false, true><<<grid, 256, 0, s>>>(p);
+  if (cg == 1) {
+    launch_multi<1>(p, grid, vscale, nt, s);
+  } else if (cg == 2) {
+    launch_multi<2>(p, grid, vscale, nt, s);
   } else {
     if (vscale && nt)
       decode_split_kernel<true, true, false><<<grid, 256, 0, s>>>(p);
@@ -388,7 +408,9 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   p.ws_o = splits > 1 ? static_cast<float*>(a->workspace) : nullptr;
   p.ws_ml = splits > 1 ? p.ws_o + rows * splits * kHeadDim : nullptr;
   const bool nt = use_nontemporal(0, pairs * tokens * kHeadDim * 2 * 2);
-  return launch_decode(p, dim3(p.splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1, nt, true,
+  const int64_t cols = static_cast<int64_t>(group) * a->tokens;
+  const int cg = cols <= 16 ? 1 : 2;
+  return launch_decode(p, dim3(p.splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1, nt, cg,
                        static_cast<int>(rows), s, "lkv_prefill_attn (short call on the decode kernel)");
 }
 
@@ -446,6 +468,6 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   p.scale_log2 = a->sm_scale * kLog2e;
   const int64_t kv_bytes = static_cast<int64_t>(a->batch) * a->num_kv_heads * call_key_tokens(a) * kHeadDim * 2 * 2;
   return launch_decode(p, dim3(a->num_splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1,
-                       use_nontemporal(a->kv_cache_hint, kv_bytes), false, a->batch * a->num_q_heads, as_stream(stream),
+                       use_nontemporal(a->kv_cache_hint, kv_bytes), 0, a->batch * a->num_q_heads, as_stream(stream),
                        "lkv_decode_attn");
 }

@@ -292,11 +292,13 @@ def test_decode_kv_cache_hint_does_not_change_results(splits):
 
 
 @pytest.mark.parametrize("L,Hq,Hkv,causal,B", [(2, 32, 8, True, 2), (4, 8, 2, True, 3), (3, 15, 3, False, 1),
-                                              (16, 16, 16, True, 2), (1, 64, 4, True, 2), (5, 6, 2, True, 1)])
+                                              (16, 16, 16, True, 2), (1, 64, 4, True, 2), (5, 6, 2, True, 1),
+                                              (8, 32, 8, True, 1), (11, 6, 2, False, 2), (32, 8, 8, True, 1)])
 def test_short_prefill_on_decode_kernel(L, Hq, Hkv, causal, B):
-    """Prefill calls of at most 16 query rows per kv head run on the decode kernel, one score column
-    per (token, head) with its own causal limit: against the oracle (older V scale, a wrapping ring,
-    split partials combined per (token, head) when the batch is small) and against the tile kernel."""
+    """Prefill calls of at most 32 query rows per kv head run on the decode kernel, one score column
+    per (token, head) with its own causal limit, in one or two 16-column groups: against the oracle
+    (older V scale, a wrapping ring, split partials combined per (token, head) when the batch is
+    small) and against the tile kernel."""
 
     rng = np.random.default_rng(L * 100 + Hq + B)
     seg, k, v = _two_segments(rng, B, Hkv, T0=203, n1=L + 150, start=150, ring_blocks=8)
