@@ -562,19 +562,17 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   const int64_t rows = static_cast<int64_t>(a->tokens) * group;
   const int64_t heads = static_cast<int64_t>(a->num_kv_heads) * a->batch;
   // Each wave takes 32 query rows.  Short calls (<= 64 rows per kv head): 2 waves.  Otherwise 8
-  // waves (two per SIMD, one workgroup per CU) or 4 waves (two workgroups per CU, whose barriers do
-  // not wait on each other).  Measured on 256 CUs, 4 waves win when the 4-wave grid still leaves
-  // at most one workgroup per CU (twice the CUs busy) and when the 8-wave grid covers the CUs 8
-  // times or more (finer tiles even out the causal work, and the two workgroups of a CU overlap
-  // their barrier waits); for one to eight rounds of 8-wave tiles the 8-wave tile is as fast or faster.
+  // waves (two per SIMD, one workgroup per CU), or 4 waves (two workgroups per CU) when the 4-wave
+  // grid still leaves at most one workgroup per CU, which keeps twice the CUs busy (measured on 256
+  // CUs: at B = 1 of a config-3 piece 23 vs 18 %; from B = 2 up the 8-wave tile is 0.5-1.5 points ahead).
   const bool wide = rows > 64;
   int waves = wide ? 8 : 2;
   if (wide && a->tile_waves != 0) {
     waves = a->tile_waves;
   } else if (wide) {
     const int64_t cus = device_cu_count();
-    const int64_t wgs8 = (rows + 255) / 256 * heads, wgs4 = (rows + 127) / 128 * heads;
-    if (cus > 0 && (wgs4 <= cus || wgs8 >= 8 * cus)) waves = 4;
+    const int64_t wgs4 = (rows + 127) / 128 * heads;
+    if (cus > 0 && wgs4 <= cus) waves = 4;
   }
   const int64_t rows_per_wg = waves * 32;
   const int64_t tiles = (rows + rows_per_wg - 1) / rows_per_wg;
