@@ -66,7 +66,7 @@ def parse_args():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 4 (128K decode), config 5 (Wan) and config 3 (8B end to end) measurements")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy decode steps of the config 3 model run")
-    ap.add_argument("--only", choices=["prefill", "config4", "config5", "config3"], default=None,
+    ap.add_argument("--only", choices=["prefill", "short", "config4", "config5", "config3"], default=None,
                     help="run one secondary measurement alone and print its JSON (for profiling); "
                          "this is not the bench line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -154,6 +154,33 @@ def decode_long_measurement(ops, torch, dev, layers: int = 32) -> dict:
         "attn_hbm_gbps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "attn_step_tok_s": round(Bl / (us * layers * 1e-6), 1),
     }
+
+
+def short_prefill_measurement(ops, torch, cache, dev, reps: int = 20) -> dict:
+    """Prefill calls of a few query tokens per sequence (speculative-decoding drafts, tiny chunks)
+    over config 2's 1 GiB shared cache: B=32, L = 1, 2, 4, 8 tokens attending to all 8192 history
+    tokens.  Calls of <= 32 query rows per kv head run on the decode kernel with one score column
+    per (token, head); the 4-token call is also timed on the MFMA tile kernel (tile_waves = 4)."""
+
+    g = torch.Generator(device=dev).manual_seed(6)
+    res = {"workload": "config 2 shared cache (B=32, 8192 tokens, 8 kv heads), L query tokens x 32 heads per sequence"}
+    for L, tw in ((1, 0), (2, 0), (4, 0), (8, 0), (4, 4)):
+        q = torch.randn((B, L, HQ, D), generator=g, device=dev).bfloat16()
+        kw = dict(older=cache, older_len=T, causal=False, tile_waves=tw)
+        ops.prefill_attention(q, **kw)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            ops.prefill_attention(q, **kw)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = 2 * B * HKV * T * D * 2 + 2 * B * L * HQ * D * 2
+        key = f"L{L}" + ("_tile_kernel" if tw else "")
+        res[key] = {"us_per_call": round(us, 2), "kv_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                    "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    return res
 
 
 def wan_measurement(ops, torch, dev) -> dict:
@@ -389,6 +416,10 @@ def main() -> int:
             store = ops.TiledKV(torch.randn((B, HKV, T // 32, 4096), device=dev).bfloat16(),
                                 torch.randn((B, HKV, T // 32, 4096), device=dev).bfloat16())
             res = prefill_measurement(ops, torch, store, dev)
+        elif args.only == "short":
+            cache = ops.TiledKV(torch.randn((B, HKV, T // 32, 4096), device=dev).bfloat16(),
+                                torch.randn((B, HKV, T // 32, 4096), device=dev).bfloat16())
+            res = short_prefill_measurement(ops, torch, cache, dev)
         elif args.only == "config4":
             res = decode_long_measurement(ops, torch, dev)
         elif args.only == "config5":
@@ -445,7 +476,8 @@ def main() -> int:
     configs = None
     if not args.no_configs:
         del qs, outs
-        configs = {"config4_decode_128k": decode_long_measurement(ops, torch, dev),
+        configs = {"short_prefill_calls": short_prefill_measurement(ops, torch, cache, dev),
+                   "config4_decode_128k": decode_long_measurement(ops, torch, dev),
                    "config5_wan": wan_measurement(ops, torch, dev)}
         del cache
         torch.cuda.empty_cache()
