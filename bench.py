@@ -164,7 +164,7 @@ def short_prefill_measurement(ops, torch, cache, dev, reps: int = 20) -> dict:
 
     g = torch.Generator(device=dev).manual_seed(6)
     res = {"workload": "config 2 shared cache (B=32, 8192 tokens, 8 kv heads), L query tokens x 32 heads per sequence"}
-    for L, tw in ((1, 0), (2, 0), (4, 0), (8, 0), (4, 4)):
+    for L, tw in ((1, 0), (2, 0), (4, 0), (8, 0), (16, 0), (4, 4)):
         q = torch.randn((B, L, HQ, D), generator=g, device=dev).bfloat16()
         kw = dict(older=cache, older_len=T, causal=False, tile_waves=tw)
         ops.prefill_attention(q, **kw)

@@ -215,7 +215,7 @@ typedef struct lkv_prefill_args {
   int64_t local_table_stride;
   int64_t local_page_stride;
   int32_t local_num_pages;
-  /* Kernel choice.  0: calls of at most 32 query rows per kv head (tokens * Hq / Hkv <= 32) run on
+  /* Kernel choice.  0: calls of at most 64 query rows per kv head (tokens * Hq / Hkv <= 64) run on
    * the decode kernel (one score column per (token, head), each key read once); larger calls on the
    * MFMA tile kernel with 4 or 8 waves per workgroup chosen from the grid and the device's CU
    * count.  4 / 8: always the tile kernel, with that many waves (32 rows each) above 64 rows per

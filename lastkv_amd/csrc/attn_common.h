@@ -235,7 +235,7 @@ __device__ inline uint4 scale_frag(uint4 v, float s) {
   return r;
 }
 
-// A prefill call with group * tokens <= 32 query rows per kv head, run on the decode kernel with one
+// A prefill call with group * tokens <= 64 query rows per kv head, run on the decode kernel with one
 // score column per (query token, head) (decode.hip).  The arguments have passed lkv_prefill_attn's
 // checks; seg was filled from them.
 int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, hipStream_t s);

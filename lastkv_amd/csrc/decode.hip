@@ -143,13 +143,18 @@ __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, con
 }
 
 // kMulti: L > 1 query tokens per sequence, column c = (token c / G, head c % G) for c < G * L <=
-// 16 * CG (CG <= 2: four groups spill), in CG groups of 16 columns that share each block's K/V fragments (short prefill calls);
+// 16 * CG (CG <= 2 per wave: four groups spill), in CG groups of 16 columns that share each block's K/V fragments (short prefill calls);
 // otherwise column c = head c (L = 1, CG = 1).
-template <bool kVScale, bool kNT, bool kMulti, int CG = 1>
+// kPairs (with kMulti): 32 * CG columns; waves 0-1 take column groups [0, CG), waves 2-3 groups
+// [CG, 2 CG), and each pair walks all of the split's blocks (every block is fetched by both pairs,
+// the second time normally from L2), so no wave holds more than CG groups of state.
+template <bool kVScale, bool kNT, bool kMulti, int CG = 1, bool kPairs = false>
 __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p) {
-  __shared__ float sm_m[kWaves][16 * CG];
-  __shared__ float sm_l[kWaves][16 * CG];
-  __shared__ float sm_o[kWaves][16 * CG][kHeadDim];
+  constexpr int kCols = (kPairs ? 32 : 16) * CG;
+  constexpr int kStride = kPairs ? 2 : kWaves;  // block stride of one wave
+  __shared__ float sm_m[kWaves][kCols];
+  __shared__ float sm_l[kWaves][kCols];
+  __shared__ float sm_o[kWaves][kCols][kHeadDim];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -167,9 +172,10 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   uint4 qf[CG][4];
   int lim[CG], lim_min = 0;  // causal limits (local token index) of this lane's columns and of column 0
   if (kMulti) lim_min = p.causal ? sv.n1 - p.L : sv.n1 - 1;
+  const int cg0 = kPairs ? (wave >> 1) * CG : 0;  // this wave's first column group
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
-    const int c = 16 * cg + n16;
+    const int c = 16 * (cg0 + cg) + n16;
     const int t = kMulti ? c / G : 0, h = c - t * G;
     const uint16_t* qrow = p.q + b * p.q_sb + (kMulti ? t * p.q_st : 0) + static_cast<int64_t>(kvh * G + h) * kHeadDim;
 #pragma unroll
@@ -196,9 +202,9 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   // this wave's blocks: blk_begin + wave + kWaves * t, t < nw; block t + 1 is loaded while block
   // t is computed.  The loop runs while two or more blocks remain, so its loads are unconditional
   // (the compiler then counts them exactly for s_waitcnt); the last one or two blocks follow it.
-  const int first = blk_begin + wave;
+  const int first = blk_begin + (kPairs ? (wave & 1) : wave);
   if (first < blk_end) {
-    const int nw = (blk_end - 1 - first) / kWaves + 1;
+    const int nw = (blk_end - 1 - first) / kStride + 1;
     BlockFrags fa, fb;
     BlockRef ra = block_ref(sv, first);
     load_block<kNT>(fa, ra, n16, g4);
@@ -206,17 +212,17 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     // (the scheduling barriers keep the block being computed from moving above the next block's
     // loads, where reusing its registers would make the loads wait for it)
     for (; t + 2 < nw; t += 2) {
-      const BlockRef rb = block_ref(sv, first + kWaves * (t + 1));
+      const BlockRef rb = block_ref(sv, first + kStride * (t + 1));
       load_block<kNT>(fb, rb, n16, g4);
       __builtin_amdgcn_sched_barrier(0);
       compute(fa, ra);
-      ra = block_ref(sv, first + kWaves * (t + 2));
+      ra = block_ref(sv, first + kStride * (t + 2));
       load_block<kNT>(fa, ra, n16, g4);
       __builtin_amdgcn_sched_barrier(0);
       compute(fb, rb);
     }
     if (t + 1 < nw) {
-      const BlockRef rb = block_ref(sv, first + kWaves * (t + 1));
+      const BlockRef rb = block_ref(sv, first + kStride * (t + 1));
       load_block<kNT>(fb, rb, n16, g4);
       compute(fa, ra);
       compute(fb, rb);
@@ -228,13 +234,13 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   // merge the four waves' states
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
-    if (g4 == 0 && 16 * cg + n16 < cols) {
-      sm_m[wave][16 * cg + n16] = st[cg].m;
-      sm_l[wave][16 * cg + n16] = st[cg].l;
+    if (g4 == 0 && 16 * (cg0 + cg) + n16 < cols) {
+      sm_m[wave][16 * (cg0 + cg) + n16] = st[cg].m;
+      sm_l[wave][16 * (cg0 + cg) + n16] = st[cg].l;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int h = 16 * cg + 4 * g4 + i;
+      const int h = 16 * (cg0 + cg) + 4 * g4 + i;
       if (h < cols) {
 #pragma unroll
         for (int nb = 0; nb < 8; ++nb) sm_o[wave][h][16 * nb + n16] = st[cg].o[nb][i];
@@ -246,12 +252,15 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     const int h = idx >> 7, d = idx & (kHeadDim - 1);  // column h = (token tq, head hh)
     const int tq = kMulti ? h / G : 0, hh = h - tq * G;
     const int64_t row_q = (static_cast<int64_t>(b) * (kMulti ? p.L : 1) + tq) * p.hq + kvh * G + hh;  // [B, L, Hq] row
-    float M = sm_m[0][h];
+    // the waves that hold column h: all four, or the pair of its column group
+    const int w0 = kPairs ? 2 * (h / (16 * CG)) : 0;
+    constexpr int kMergeWaves = kPairs ? 2 : kWaves;
+    float M = sm_m[w0][h];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
+    for (int w = w0 + 1; w < w0 + kMergeWaves; ++w) M = fmaxf(M, sm_m[w][h]);
     float L = 0.f, O = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = w0; w < w0 + kMergeWaves; ++w) {
       const float f = sm_m[w][h] == kNegInf ? 0.f : fast_exp2(sm_m[w][h] - M);
       L += f * sm_l[w][h];
       O += f * sm_o[w][h][d];
@@ -341,16 +350,16 @@ int64_t call_key_tokens(const Args* a) {
 // could keep for the next layer's call over the same shared cache); hint 1 / 2 force a policy.
 bool use_nontemporal(int32_t hint, int64_t kv_bytes) { return hint == 2 || (hint == 0 && kv_bytes > (int64_t{384} << 20)); }
 
-template <int CG>
+template <int CG, bool kPairs = false>
 void launch_multi(const DecodeParams& p, dim3 grid, bool vscale, bool nt, hipStream_t s) {
   if (vscale && nt)
-    decode_split_kernel<true, true, true, CG><<<grid, 256, 0, s>>>(p);
+    decode_split_kernel<true, true, true, CG, kPairs><<<grid, 256, 0, s>>>(p);
   else if (vscale)
-    decode_split_kernel<true, false, true, CG><<<grid, 256, 0, s>>>(p);
+    decode_split_kernel<true, false, true, CG, kPairs><<<grid, 256, 0, s>>>(p);
   else if (nt)
-    decode_split_kernel<false, true, true, CG><<<grid, 256, 0, s>>>(p);
+    decode_split_kernel<false, true, true, CG, kPairs><<<grid, 256, 0, s>>>(p);
   else
-    decode_split_kernel<false, false, true, CG><<<grid, 256, 0, s>>>(p);
+    decode_split_kernel<false, false, true, CG, kPairs><<<grid, 256, 0, s>>>(p);
 }
 
 // cg: 0 for decode calls (one column per head), else the 16-column groups of a short prefill call
@@ -360,6 +369,8 @@ int32_t launch_decode(const DecodeParams& p, dim3 grid, bool vscale, bool nt, in
     launch_multi<1>(p, grid, vscale, nt, s);
   } else if (cg == 2) {
     launch_multi<2>(p, grid, vscale, nt, s);
+  } else if (cg == 4) {  // two wave pairs of two groups each
+    launch_multi<2, true>(p, grid, vscale, nt, s);
   } else {
     if (vscale && nt)
       decode_split_kernel<true, true, false><<<grid, 256, 0, s>>>(p);
@@ -409,7 +420,7 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   p.ws_ml = splits > 1 ? p.ws_o + rows * splits * kHeadDim : nullptr;
   const bool nt = use_nontemporal(0, pairs * tokens * kHeadDim * 2 * 2);
   const int64_t cols = static_cast<int64_t>(group) * a->tokens;
-  const int cg = cols <= 16 ? 1 : 2;
+  const int cg = cols <= 16 ? 1 : cols <= 32 ? 2 : 4;
   return launch_decode(p, dim3(p.splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1, nt, cg,
                        static_cast<int>(rows), s, "lkv_prefill_attn (short call on the decode kernel)");
 }

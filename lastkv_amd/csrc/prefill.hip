@@ -538,10 +538,10 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
               "prefill needs a workspace of %lld bytes (lkv_prefill_workspace_bytes), got %lld",
               static_cast<long long>(need), static_cast<long long>(a->workspace_bytes));
   LKV_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 15) == 0, "workspace must be 16-byte aligned");
-  // Calls of at most 32 query rows per kv head (e.g. up to 8 tokens of a GQA group of 4) read every
+  // Calls of at most 64 query rows per kv head (e.g. up to 16 tokens of a GQA group of 4) read every
   // key once on the decode kernel (one score column per (token, head)) instead of converting V to
   // fp16 and running 2-wave tiles; tile_waves 4 or 8 keep them on the tile kernel.
-  if (a->tile_waves == 0 && static_cast<int64_t>(a->tokens) * group <= 32)
+  if (a->tile_waves == 0 && static_cast<int64_t>(a->tokens) * group <= 64)
     return prefill_on_decode_kernel(a, p.seg, group, as_stream(stream));
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_stride_b;

@@ -2,7 +2,7 @@
 
 Each case draws a batch, GQA geometry, query count, older-segment length, ring size and start
 (wrapping or not), causal or bidirectional masking; prefill runs through the automatic kernel
-choice (decode kernel for <= 32 query rows per kv head, MFMA tiles above) and through the tile
+choice (decode kernel for <= 64 query rows per kv head, MFMA tiles above) and through the tile
 kernel forced with tile_waves = 4, decode through one and several key splits."""
 
 from __future__ import annotations
