@@ -294,7 +294,8 @@ def test_decode_kv_cache_hint_does_not_change_results(splits):
 @pytest.mark.parametrize("L,Hq,Hkv,causal,B", [(2, 32, 8, True, 2), (4, 8, 2, True, 3), (3, 15, 3, False, 1),
                                               (16, 16, 16, True, 2), (1, 64, 4, True, 2), (5, 6, 2, True, 1),
                                               (8, 32, 8, True, 1), (11, 6, 2, False, 2), (32, 8, 8, True, 1),
-                                              (16, 32, 8, True, 1), (13, 12, 3, False, 2), (40, 8, 8, True, 1)])
+                                              (16, 32, 8, True, 1), (13, 12, 3, False, 2), (40, 8, 8, True, 1),
+                                              (2, 64, 2, True, 1), (1, 64, 1, True, 2)])
 def test_short_prefill_on_decode_kernel(L, Hq, Hkv, causal, B):
     """Prefill calls of at most 64 query rows per kv head run on the decode kernel, one score column
     per (token, head) with its own causal limit, in one or two 16-column groups per wave (two wave
