@@ -77,7 +77,7 @@ int32_t lkv_cache_unpack(const void *src, int64_t src_seq_stride, int64_t src_he
  *           ring token local_start[b] (wrapping at 32 * local_ring_blocks), e.g. the recent
  *           (already blended) chunk followed by the current chunk.
  * out[b, h, :] = softmax(q[b, h] . K^T * sm_scale) V for query head h, GQA group
- * Hq / Hkv <= 16 (query head h reads kv head h / group).  Optional lse[b * Hq + h] receives the
+ * Hq / Hkv <= 64 (query head h reads kv head h / group).  Optional lse[b * Hq + h] receives the
  * natural-log log-sum-exp of the scaled scores (-inf when there are no keys).
  * num_splits > 1 splits each sequence's keys across workgroups; the workspace must then hold
  * lkv_decode_workspace_bytes(batch, num_q_heads, num_splits) bytes.

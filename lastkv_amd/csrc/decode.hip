@@ -442,7 +442,7 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   LKV_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->num_q_heads > 0, "bad sizes");
   LKV_REQUIRE(a->num_q_heads % a->num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
   const int group = a->num_q_heads / a->num_kv_heads;
-  LKV_REQUIRE(group <= 16, "GQA group %d exceeds 16", group);
+  LKV_REQUIRE(group <= 64, "GQA group %d exceeds 64", group);
   LKV_REQUIRE(a->num_splits >= 1 && a->num_splits <= 1024, "num_splits must be in [1, 1024]");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->older_vscale_mode == 1, "older_vscale_mode must be 0 or 1");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->vscale != nullptr, "older_vscale_mode 1 needs vscale");
@@ -478,7 +478,9 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   p.splits = a->num_splits;
   p.scale_log2 = a->sm_scale * kLog2e;
   const int64_t kv_bytes = static_cast<int64_t>(a->batch) * a->num_kv_heads * call_key_tokens(a) * kHeadDim * 2 * 2;
+  // groups above 16 query heads per kv head take the multi-column instances (columns = heads)
+  const int cg = group <= 16 ? 0 : group <= 32 ? 2 : 4;
   return launch_decode(p, dim3(a->num_splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1,
-                       use_nontemporal(a->kv_cache_hint, kv_bytes), 0, a->batch * a->num_q_heads, as_stream(stream),
+                       use_nontemporal(a->kv_cache_hint, kv_bytes), cg, a->batch * a->num_q_heads, as_stream(stream),
                        "lkv_decode_attn");
 }

@@ -331,7 +331,7 @@ def decode_attention(
     a.struct_size = ctypes.sizeof(_lib.DecodeArgs)
     Hkv = _fill_segments(a, B, device, older, older_len, older_slot, vscale, local, local_len, local_start, local_slot,
                          older_table, local_table, local_ring_blocks)
-    _require(Hq % Hkv == 0 and Hq // Hkv <= 16, "Hq must be a multiple of Hkv with group <= 16")
+    _require(Hq % Hkv == 0 and Hq // Hkv <= 64, "Hq must be a multiple of Hkv with group <= 64")
     if out is None:
         out = torch.empty((B, Hq, HEAD_DIM), dtype=torch.bfloat16, device=device)
     _require_bf16_cuda("out", out)

@@ -235,11 +235,12 @@ def _two_segments(rng, B, Hkv, T0, n1, start, ring_blocks):
     return seg, k, v
 
 
-@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (6, 2), (7, 1), (16, 2), (32, 2), (48, 3)])
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (6, 2), (7, 1), (16, 2), (32, 2), (48, 3), (24, 1), (64, 2), (64, 1)])
 @pytest.mark.parametrize("splits", [1, 4])
 def test_decode_gqa_group_sizes(Hq, Hkv, splits):
-    """GQA groups 1 (MHA) to 16 (the kernel's limit), odd and not powers of two, over an older
-    segment with V scale and a wrapping ring segment; query head h reads kv head h // G."""
+    """GQA groups 1 (MHA) to 64 (above 16 the multi-column instances: 24, 32, 64), odd and not
+    powers of two, over an older segment with V scale and a wrapping ring segment; query head h
+    reads kv head h // G."""
 
     rng = np.random.default_rng(Hq * 31 + Hkv * 7 + splits)
     B = 2
