@@ -161,8 +161,13 @@ int32_t lkv_decode_attn(const lkv_decode_args *args, lkv_stream_t stream);
  * local tokens (causal = 0); the last L local tokens are the queries' own K/V.  Segments,
  * slots, clamping and vscale are as in lkv_decode_args.  out is bf16 [B, L, Hq, 128] with
  * 8-byte-aligned rows (q: 16-byte-aligned rows); optional lse is fp32 [B, L, Hq] (natural log).
- * P*V runs in fp16, which represents bf16 V exactly for |V| < 65504 (larger magnitudes
- * saturate).  The call first writes the fp16 V (older segment as bf16(V * vscale)) of every key
+ * P*V runs in fp16, which represents bf16 V exactly for 2^-17 <= |V| <= 65280 and 0 (smaller
+ * magnitudes are truncated toward zero, an absolute error below 2^-24; larger ones saturate at
+ * 65504).  causal = 1 masks only the local segment, whose last `tokens` tokens are the queries' own
+ * keys: a host-constant local_len in [1, tokens) is rejected (the mask would have to reach into
+ * the older segment); without a local segment, or with local_len 0, the older segment is fully
+ * visible (the two-pass path's source pass).  Device lengths are not checked: a row then sees the
+ * local tokens up to its bottom-right limit, if any.  The call first writes the fp16 V (older segment as bf16(V * vscale)) of every key
  * block into the caller's workspace (lkv_prefill_workspace_bytes), then runs the attention over
  * it; both launches go on `stream`, and the workspace may be reused once the call has run.
  * ------------------------------------------------------------------------------------- */

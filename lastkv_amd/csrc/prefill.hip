@@ -7,18 +7,20 @@
 // Each wave owns 32 rows (two 16-column groups of the 16x16x32 MFMA tiles), few enough registers
 // (< 256 VGPRs, accumulators in VGPRs) for two waves per SIMD.
 // Per 32-token key block:
-//   - the NW waves each fetch 16 / NW of the block's 16 one-KiB fragments from HBM/L2 into
-//     registers one block ahead (one contiguous 1 KiB run per load instruction), convert V to
-//     fp16 (applying bf16(V * s) on the older segment) and publish the block to an LDS double
-//     buffer in lane order, so every MFMA operand is one conflict-free ds_read_b128;
+//   - the NW waves each fetch 16 / NW of the block's 16 one-KiB fragments (K bf16 from the cache,
+//     V fp16 from the call's V pre-pass) from HBM/L2 into registers two blocks ahead (one
+//     contiguous 1 KiB run per load instruction) and publish them to a ring of LDS buffers in
+//     lane order, so every MFMA operand is one conflict-free ds_read_b128;
 //   - S^T = K * Q^T with 16x16x32 bf16 MFMAs (exact products, fp32 sums);
 //   - online softmax in the exp2 domain (scale and offset folded into one FMA), row max over the
-//     four 16-lane rows with VALU lane swaps, row sums kept per lane and reduced once at the end,
-//     O rescaled (a branch taken only when some row's offset moved) with the factor each lane
-//     already holds;
-//   - O^T += V^T * P^T with 16x16x32 fp16 MFMAs: P in [0, 1] carries 11 mantissa bits (bf16
-//     would carry 8, a 1.7e-3 relative error the rel-L2 1e-3 bound does not allow), and bf16 V
-//     converts to fp16 exactly for |V| < 65504 (larger values saturate).
+//     four 16-lane rows with VALU lane swaps, O rescaled (a branch taken only when some row's
+//     offset moved) with the factor each lane already holds;
+//   - O^T += V^T * P^T with 16x16x32 fp16 MFMAs, and the row sums as P times a tile of ones on
+//     the same pipe: P in (0, 2) carries 11 mantissa bits (bf16 would carry 8, a 1.7e-3 relative
+//     error the rel-L2 1e-3 bound does not allow); the 2-wave instance adds the fp16 residual of
+//     P (hi + lo, ~22 bits).  bf16 V converts to fp16 exactly for 2^-17 <= |V| <= 65280 and 0;
+//     smaller magnitudes are truncated toward zero (absolute error < 2^-24), larger ones
+//     saturate at 65504.
 #include <algorithm>
 
 #include "attn_common.h"
@@ -165,7 +167,9 @@ __device__ inline void raise_rows(RowState& rs, float lm, float c, f32x4 (&o)[8]
   const float bm = wave_max_across_rows(lm);
   const bool up = bm > rs.m;  // m = -inf: true for the first finite maximum
   const float mc_new = up ? bm * c : rs.mc;
-  const float alpha = up ? fast_exp2(rs.mc - mc_new) : 1.f;  // l and O are 0 while m = -inf
+  // l and O are 0 while m = -inf: scale them by 0, not by 2^(0 - mc_new), which overflows to inf
+  // (and 0 * inf = NaN) when the first maximum is below -128 / c
+  const float alpha = up ? (rs.m == kNegInf ? 0.f : fast_exp2(rs.mc - mc_new)) : 1.f;
   rs.m = up ? bm : rs.m;
   rs.mc = rs.m == kNegInf ? 0.f : mc_new;
   if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
@@ -181,6 +185,17 @@ __device__ inline void probs(const float (&s)[8], float c, float mc, float (&pr)
   for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(s[j], c, -mc));
 #pragma unroll
   for (int j = 0; j < 4; ++j) w[j] = pack_f16_rne(pr[2 * j], pr[2 * j + 1]);
+}
+
+// The fp16 residuals pr - fp16(pr) of the probabilities packed in w (exact in fp32; fp16
+// subnormals keep them to 2^-24 absolute), so hi + lo carries ~22 bits of each probability.
+__device__ inline void probs_lo(const float (&pr)[8], const uint32_t (&w)[4], uint32_t (&lo)[4]) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const h2 hi = __builtin_bit_cast(h2, w[j]);
+    lo[j] = pack_f16_rne(pr[2 * j] - static_cast<float>(hi.x), pr[2 * j + 1] - static_cast<float>(hi.y));
+  }
 }
 
 // Nonzero when some packed fp16 probability is >= 2 (exponent field >= 16), infinite or NaN.
@@ -221,9 +236,13 @@ __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
 // buffer i % 4, block i + 1 in buffer (i + 1) % 4): probabilities of block i from the scores
 // computed in step i - 1, QK^T of block i + 1, P V of block i, store block i + 2 into buffer
 // (i + 2) % 4, load block i + 4, one barrier.
+// The 2-wave instance (calls of at most 64 query rows per kv head, bound by HBM, not by the matrix
+// pipe) splits P into fp16 hi + lo and runs P V twice, so its probabilities carry ~22 bits
+// instead of 11.
 template <int NW, int CG, int WPE, bool kPaged>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_kernel(
     const PrefillParams p) {
+  constexpr bool kSplitP = NW == 2;
   constexpr int kRing = 4;
   constexpr int kBuf = 1024;  // uint4 per block buffer (16 KiB)
   __shared__ uint4 lds[kRing * kBuf];
@@ -388,11 +407,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
           sc[cg][0] = mfma_bf16(kf[kb], qf[cg][kb], sc[cg][0]);
           sc[cg][1] = mfma_bf16(kf[4 + kb], qf[cg][kb], sc[cg][1]);
         }
-      uint32_t pw[CG][4];
+      uint32_t pw[CG][4], pl[CG][4];
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) {
         float pr[8];
         probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
+        if (kSplitP) probs_lo(pr, pw[cg], pl[cg]);
       }
       uint4 vf[8];
 #pragma unroll
@@ -418,19 +438,25 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
           raise_rows(rs[cg], max8(s[cg]), c, o[cg], ol[cg]);
           float pr[8];
           probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
+          if (kSplitP) probs_lo(pr, pw[cg], pl[cg]);
         }
       }
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
-        for (int cg = 0; cg < CG; ++cg)
+        for (int cg = 0; cg < CG; ++cg) {
           o[cg][nb] = mfma_f16(vf[nb], make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]), o[cg][nb]);
+          if (kSplitP) o[cg][nb] = mfma_f16(vf[nb], make_uint4(pl[cg][0], pl[cg][1], pl[cg][2], pl[cg][3]), o[cg][nb]);
+        }
 #pragma unroll
-      for (int cg = 0; cg < CG; ++cg) ol[cg] = mfma_f16(kOnes, make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]), ol[cg]);
+      for (int cg = 0; cg < CG; ++cg) {
+        ol[cg] = mfma_f16(kOnes, make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]), ol[cg]);
+        if (kSplitP) ol[cg] = mfma_f16(kOnes, make_uint4(pl[cg][0], pl[cg][1], pl[cg][2], pl[cg][3]), ol[cg]);
+      }
       stage_store<NW>(st, wr, wave, lane);
       stage_load<NW>(st, rsrc, ld_k, ld_blk, wave, lane_off);
 #pragma unroll
-      for (int i = 0; i < 9 * CG; ++i) {
+      for (int i = 0; i < (kSplitP ? 18 : 9) * CG; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (P V and P 1 of block i)
         __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write (staging of block i + 2)
@@ -527,6 +553,13 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
               "q rows must be 16-byte aligned");
   LKV_REQUIRE((a->out_stride_b % 4) == 0 && (a->out_stride_t % 4) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 7) == 0,
               "out rows must be 8-byte aligned");
+  // causal = 1 masks the local segment bottom-right, the queries' own keys being its last `tokens`
+  // tokens; a non-empty local segment shorter than that would need the mask to reach into the older
+  // segment (without a local segment, or with an empty one, the older segment is fully visible)
+  LKV_REQUIRE(a->causal == 0 || a->local_k == nullptr || a->local_len != nullptr || a->local_len_const <= 0 ||
+                  a->local_len_const >= a->tokens,
+              "causal calls need local_len >= tokens (the queries' own keys end the local segment), got %d < %d",
+              a->local_len_const, a->tokens);
   PrefillParams p;
   if (const int32_t st = fill_segments(a, p.seg)) return st;
   LKV_REQUIRE(a->batch <= 65535 && a->num_kv_heads <= 65535, "batch and num_kv_heads must be <= 65535");

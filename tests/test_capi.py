@@ -87,3 +87,22 @@ def test_prefill_rejects_bad_arguments_before_any_launch(field, value, message, 
     setattr(a, field, value)
     assert lib.lkv_prefill_attn(ctypes.byref(a), None) == 1
     assert message in lib.lkv_last_error()
+
+
+@pytest.mark.parametrize("local_len,ok_expected", [(3, False), (1, False), (4, True), (0, True)])
+def test_prefill_causal_needs_the_queries_own_keys(local_len, ok_expected):
+    """A causal call whose host-constant local length is shorter than its query count (but not
+    empty) is rejected: the bottom-right rule would have to hide older keys from early rows."""
+
+    lib = _lib.load()
+    a = _lib.PrefillArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim, a.causal = 0, 4, 8, 2, 128, 1
+    a.q = a.out = 16
+    a.local_k = a.local_v = 16
+    a.local_ring_blocks, a.local_num_slots, a.local_len_const = 1, 1, local_len
+    status = lib.lkv_prefill_attn(ctypes.byref(a), None)
+    if ok_expected:
+        assert status == 0  # batch 0: validated, nothing launched
+    else:
+        assert status == 1 and b"local_len >= tokens" in lib.lkv_last_error()

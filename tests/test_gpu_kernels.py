@@ -353,3 +353,35 @@ def test_silu_mul_bit_exact():
     want = torch.nn.functional.silu(gate) * up
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("L,G", [(160, 4), (12, 4)])
+def test_prefill_extreme_score_ranges(L, G):
+    """Regression: rows whose first visible scores are all far below zero (scaled scores near -180,
+    as q/k RMSNorm gains of ~8 produce) once made the tile kernel rescale its empty state by
+    2^(0 - m c) = inf and return NaN rows.  Keys of the first blocks point against the queries,
+    later keys along them (the running maximum then jumps by ~360), causal, over an older segment
+    and the local ring; the tile kernel (4 / 8 / automatic waves) and, for the short call, the
+    decode kernel, against the fp64 oracle."""
+
+    rng = np.random.default_rng(L)
+    B, Hkv, T0 = 2, 2, 40
+    Hq = G * Hkv
+    n_local = L + 70
+    u = bf16.round_bf16(np.full(128, 1.0, np.float32))
+    q = bf16.round_bf16((16 * u + rng.standard_normal((B, L, Hq, 128))).astype(np.float32))
+    keys = T0 + n_local
+    sign = np.where(np.arange(keys) < 48, -1.0, 1.0)[None, None, :, None]
+    k = bf16.round_bf16((sign * u + 0.3 * rng.standard_normal((B, Hkv, keys, 128))).astype(np.float32))
+    v = _bf(rng, (B, Hkv, keys, 128))
+    older = ops.TiledKV.zeros(B, Hkv, 64, DEV)
+    ops.pack_kv(_t(k[:, :, :T0]), _t(v[:, :, :T0]), older)
+    ring = ops.TiledKV.zeros(B, Hkv, -(-n_local // 32) * 32, DEV)
+    ops.pack_kv(_t(k[:, :, T0:]), _t(v[:, :, T0:]), ring)
+    kw = dict(older=older, older_len=T0, local=ring, local_len=n_local, causal=True)
+    want, _ = A.attention(q.transpose(0, 2, 1, 3), k, v, causal_bottom_right=True)
+    want = bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32))
+    for tw in (0, 4, 8):
+        out = ops.prefill_attention(_t(q), tile_waves=tw, **kw)
+        assert not torch.isnan(out.float()).any(), f"tile_waves={tw}: NaN rows"
+        _close(out, want, f"extreme scores L={L} G={G} tile_waves={tw}")
