@@ -33,6 +33,7 @@ class CustomRecurrentMarinAKV254ReuseKVConfig:
     bos_token_id: int | None = 1
     eos_token_id: int | list | None = 2
     tie_word_embeddings: bool = False
+    use_cache: bool = True
     # LastKV (configuration.py:13-24)
     chunk_size: int = 1024
     v_gap: int = 95

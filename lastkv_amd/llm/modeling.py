@@ -174,7 +174,9 @@ class CustomRecurrentMarinAKV254ReuseKVModel(nn.Module):
         self.layers = nn.ModuleList(LastKVDecoderLayer(config, i) for i in range(config.num_hidden_layers))
         self.norm = RMSNorm(config.hidden_size, config.rms_norm_eps)
         # fp32 and outside the module's buffers: casting the model to bf16 must not round it
-        self.inv_freq, self.rope_attention_scaling = rope_inv_freq(config)
+        # (on the CPU whatever the default device: from_pretrained builds the modules on "meta")
+        with torch.device("cpu"):
+            self.inv_freq, self.rope_attention_scaling = rope_inv_freq(config)
         self._inv_freq_dev: dict[torch.device, torch.Tensor] = {}
         self._blend_key = None
         self._blend = None
@@ -258,10 +260,26 @@ class CausalLMOutput:
     past_key_values: LastKVCache | None
 
 
+@dataclass
+class GenerationConfig:
+    """The fields of transformers' ``GenerationConfig`` that greedy generation reads (its
+    defaults; token ids from the model config, as ``GenerationConfig.from_model_config``)."""
+
+    max_length: int = 20
+    max_new_tokens: int | None = None
+    do_sample: bool = False
+    use_cache: bool = True
+    bos_token_id: int | None = None
+    eos_token_id: int | list | None = None
+    pad_token_id: int | None = None
+
+
 class CustomRecurrentMarinAKV254ReuseKVForCausalLM(nn.Module):
     def __init__(self, config):
         super().__init__()
         self.config = config
+        self.generation_config = GenerationConfig(bos_token_id=config.bos_token_id, eos_token_id=config.eos_token_id,
+                                                  pad_token_id=config.pad_token_id)
         self.model = CustomRecurrentMarinAKV254ReuseKVModel(config)
         self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
         if config.tie_word_embeddings:
@@ -298,25 +316,71 @@ class CustomRecurrentMarinAKV254ReuseKVForCausalLM(nn.Module):
         return CausalLMOutput(logits=self.lm_head(hidden[:, index]), past_key_values=cache)
 
     @torch.no_grad()
-    def generate(self, input_ids, max_new_tokens: int, *, prefill_chunk: int | None = None, cache=None):
-        """Greedy decoding feeding only new tokens (modeling.py:263-274); the prompt is prefilled
-        in calls of ``prefill_chunk`` tokens.  Returns [B, prompt + max_new_tokens] ids."""
+    def generate(self, input_ids=None, max_new_tokens: int | None = None, *, attention_mask=None, do_sample=None,
+                 use_cache=None, pad_token_id=None, eos_token_id=None, max_length=None,
+                 prefill_chunk: int | None = None, cache=None, **kwargs):
+        """Greedy decoding with the semantics of transformers' ``GenerationMixin.generate`` as the
+        reference calls it (llm/examples/generate.py:30-33: ``generate(**inputs, max_new_tokens=..,
+        do_sample=False, use_cache=True, pad_token_id=..)``, modeling.py:263-274): only new tokens
+        are fed (``use_cache=True``) or the whole sequence is recomputed every step
+        (``use_cache=False``), ``logits_to_keep=1``, argmax; a sequence that emits an EOS id is
+        continued with ``pad_token_id`` and generation stops once every sequence has finished
+        or ``max_new_tokens`` (else ``max_length`` in total) is reached.  ``attention_mask`` must
+        be all ones (LastKV takes unpadded prompts).  The prompt is prefilled in calls of
+        ``prefill_chunk`` tokens (default: one call).  Returns the [B, prompt + new] ids."""
 
+        gc = self.generation_config
+        if kwargs:
+            raise ValueError(f"The following generation arguments are not supported: {sorted(kwargs)}")
+        if input_ids is None:
+            raise ValueError("generate needs input_ids")
+        if do_sample if do_sample is not None else gc.do_sample:
+            raise ValueError("LastKV generation on MI355X is greedy only (do_sample=False)")
+        use_cache = gc.use_cache if use_cache is None else bool(use_cache)
         L = input_ids.shape[1]
-        step = prefill_chunk or L
-        start, out = 0, None
-        while start < L:
-            out = self(input_ids[:, start:start + step], past_key_values=cache, logits_to_keep=1)
-            cache = out.past_key_values
-            start += step
-        tokens = [input_ids]
-        for i in range(max_new_tokens):
-            token = out.logits[:, -1].argmax(-1, keepdim=True)
-            tokens.append(token)
-            if i + 1 < max_new_tokens:
-                out = self(token, past_key_values=cache, logits_to_keep=1)
+        if max_new_tokens is None:
+            max_new_tokens = gc.max_new_tokens
+        if max_new_tokens is None:
+            max_new_tokens = (gc.max_length if max_length is None else max_length) - L
+        if max_new_tokens < 1:
+            raise ValueError("max_new_tokens must be positive")
+        eos = gc.eos_token_id if eos_token_id is None else eos_token_id
+        eos = [] if eos is None else ([eos] if isinstance(eos, int) else list(eos))
+        pad = gc.pad_token_id if pad_token_id is None else pad_token_id
+        if pad is None and eos:
+            pad = eos[0]
+        eos_ids = torch.tensor(eos, dtype=input_ids.dtype, device=input_ids.device)
+
+        if attention_mask is not None and not bool(torch.all(attention_mask != 0)):
+            raise ValueError("LastKV supports unpadded sequences; generate each padded prompt separately")
+
+        def run(ids, cache):
+            step = prefill_chunk or ids.shape[1]
+            start, out = 0, None
+            while start < ids.shape[1]:
+                out = self(ids[:, start:start + step], past_key_values=cache, logits_to_keep=1)
                 cache = out.past_key_values
-        return torch.cat(tokens, dim=1)
+                start += step
+            return out
+
+        out = run(input_ids, cache if use_cache else None)
+        cache = out.past_key_values if use_cache else None
+        sequence = input_ids
+        unfinished = torch.ones(input_ids.shape[0], dtype=torch.bool, device=input_ids.device)
+        for i in range(max_new_tokens):
+            token = out.logits[:, -1].argmax(-1).to(input_ids.dtype)
+            if eos:
+                token = torch.where(unfinished, token, torch.full_like(token, pad))
+                unfinished &= ~torch.isin(token, eos_ids)
+            sequence = torch.cat((sequence, token[:, None]), dim=1)
+            if i + 1 == max_new_tokens or (eos and not bool(unfinished.any())):
+                break
+            if use_cache:
+                out = self(token[:, None], past_key_values=cache, logits_to_keep=1)
+                cache = out.past_key_values
+            else:
+                out = run(sequence, None)
+        return sequence
 
     @classmethod
     def from_pretrained(cls, path, *, dtype=torch.bfloat16, device="cuda"):
@@ -355,7 +419,33 @@ class CustomRecurrentMarinAKV254ReuseKVForCausalLM(nn.Module):
         return model.to(dtype).eval()
 
 
-def load_model(path, *, device="cuda", dtype=torch.bfloat16):
-    """Strictly load a local LastKV checkpoint for cached inference (llm/src/lastkv/llm/__init__.py:13-26)."""
+ATTENTION_BACKENDS = ("sdpa", "eager")
 
-    return CustomRecurrentMarinAKV254ReuseKVForCausalLM.from_pretrained(path, dtype=dtype, device=device)
+
+def load_model(model_name_or_path="ZefanCai/LastKV-LLM-8B-Base", *, revision=None, device="cuda",
+               dtype=torch.bfloat16, attention_backend="sdpa"):
+    """Strictly load a LastKV checkpoint for cached inference (llm/src/lastkv/llm/__init__.py:13-26).
+
+    Same keywords as the reference.  ``model_name_or_path`` must be a local checkpoint directory:
+    this build has no hub access, so a hub name raises ``ValueError`` (as does a ``revision`` of
+    one); for a local directory ``revision`` is ignored, as transformers ignores it there.
+    ``attention_backend`` 'sdpa' and 'eager' both select the HIP attention kernels (the
+    reference's two backends compute the same attention); anything else raises ``ValueError``.
+    The model runs in bfloat16 on the GPU; other devices or dtypes raise ``ValueError``."""
+
+    if attention_backend not in ATTENTION_BACKENDS:
+        raise ValueError("attention_backend must be 'sdpa' or 'eager'")
+    path = pathlib.Path(model_name_or_path)
+    if not (path / "config.json").is_file():
+        rev = f" at revision {revision!r}" if revision not in (None, "main") else ""
+        raise ValueError(f"{str(model_name_or_path)!r}{rev} is not a local LastKV checkpoint directory (config.json "
+                         "missing); this build loads local checkpoints only, download the revision first")
+    if torch.device(device).type != "cuda":
+        raise ValueError("the MI355X LastKV model runs on the GPU (device='cuda')")
+    if dtype != torch.bfloat16:
+        raise ValueError("the MI355X LastKV model runs in bfloat16")
+    model = CustomRecurrentMarinAKV254ReuseKVForCausalLM.from_pretrained(path, dtype=dtype, device=device)
+    model.config._attn_implementation = attention_backend
+    model.config.use_cache = True
+    model.generation_config.use_cache = True
+    return model.eval()

@@ -48,6 +48,7 @@ def _tiny(chunk=4, layers=3, seed=19):
     oracle = oracle.to(DEV, torch.bfloat16).eval()
     ours = Model(LastKVConfig(**kw)).to(DEV, torch.bfloat16).eval()
     ours.load_state_dict(oracle.state_dict(), strict=True)
+    ours.generation_config.eos_token_id = None  # the oracle's greedy loop has no EOS stop
     return oracle, ours
 
 
@@ -245,5 +246,113 @@ def test_8b_geometry_greedy_64_steps():
     oracle = oracle.to(torch.bfloat16).eval()
     ours = Model(LastKVConfig.from_dict(cfg)).to(DEV, torch.bfloat16).eval()
     ours.load_state_dict(oracle.state_dict(), strict=True)
+    ours.generation_config.eos_token_id = None
     prompt = torch.randint(0, 32000, (4, 2304), generator=torch.Generator().manual_seed(1)).to(DEV)
     _margin_aware_greedy(oracle, ours, prompt, 64, prefill_chunk=1024)
+
+
+def _decisive_pair(cfg, prompt_len, seed=0):
+    """The decisive-by-construction model (tests/decisive_model.py) as the oracle model (bf16)
+    and the drop-in model holding the same weights."""
+
+    import decisive_model as DM
+
+    oracle, tables = DM.build(cfg, prompt_len, seed=seed, device=DEV)
+    oracle = oracle.to(torch.bfloat16).eval()
+    ours = Model(LastKVConfig.from_dict(dict(cfg.__dict__))).to(DEV, torch.bfloat16).eval()
+    ours.load_state_dict(oracle.state_dict(), strict=True)
+    ours.generation_config.eos_token_id = None
+    return oracle, ours, tables
+
+
+def test_8b_geometry_decisive_greedy_ids_identical_64_steps():
+    """North-star criterion: greedy ids identical for the first 64 steps.  8B-shaped layers (Hq 32,
+    Hkv 8, head_dim 128, FFN 14336, llama3 RoPE) cut to 4 layers and a 32K vocabulary, weights of
+    tests/decisive_model.py (one-hot attention, wide logit margins, ids that depend on whether the
+    token a query finds sits in the older shared segment or in the local ring); B = 4 prompts of
+    2304 distinct tokens prefilled in 1024-token calls at C = 1024, then 64 greedy steps (queries
+    at positions 2303-2366: older [0, 1024), recent [1024, 2048), current from 2048).  The
+    reference path in fp32 (o32) and in bf16 (o16) give the closed-form ids; the drop-in model,
+    the serving path (eager steps) and its HIP-graph decode must give exactly the same 64 ids."""
+
+    import decisive_model as DM
+    from lastkv_amd.serving import LastKVServingModel
+
+    cfg = M.config_8b(num_hidden_layers=4, vocab_size=32000)
+    oracle, ours, tables = _decisive_pair(cfg, 2304)
+    prompt = DM.prompts(tables, 4)
+    want = DM.expected_ids(tables, prompt, 64, cfg.chunk_size)
+    regions = []
+    for row, ids in zip(prompt.tolist(), want.tolist()):
+        where = {t: i for i, t in enumerate(row)}
+        regions.append(sum(where[int(tables["sigma"][t])] < 1024 for t in [row[-1]] + ids[:-1]))
+    print(f"steps whose lookup lands in the older segment, per sequence: {regions} of 64", flush=True)
+    assert all(0 < r < 64 for r in regions)
+    prompt = prompt.to(DEV)
+    P = prompt.shape[1]
+    with torch.inference_mode():
+        o32 = _o32(oracle).generate_greedy(prompt, 64, prefill_chunk=1024).cpu()
+        o16 = _o16(oracle).generate_greedy(prompt, 64, prefill_chunk=1024).cpu()
+        got = ours.generate(prompt, 64, prefill_chunk=1024)[:, P:].cpu()
+    assert torch.equal(o32, want), "o32 departs from the construction's closed form"
+    assert torch.equal(o16, want), "o16 departs from the construction's closed form"
+    assert torch.equal(got, o32), f"drop-in ids differ from o32 at steps {(got != o32).nonzero().tolist()[:8]}"
+    del oracle
+    runner = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=P + 64)
+    with torch.inference_mode():
+        served = torch.stack([r[P:] for r in runner.generate(list(prompt), 64, prefill_chunk=1024)])
+        assert torch.equal(served, o32), f"serving ids differ from o32 at {(served != o32).nonzero().tolist()[:8]}"
+        slots = [runner.add_sequence() for _ in range(4)]
+        for start in range(0, P, 1024):
+            logits = runner.step([(s, prompt[i, start:start + 1024]) for i, s in enumerate(slots)])
+        graph = runner.decode_graph(slots)
+        token, graphed = logits.argmax(-1), [logits.argmax(-1)]
+        for _ in range(63):
+            _, token = graph.step(token)
+            graphed.append(token.clone())
+    graphed = torch.stack(graphed, 1).cpu()
+    assert torch.equal(graphed, o32), f"graph decode ids differ from o32 at {(graphed != o32).nonzero().tolist()[:8]}"
+
+
+def test_reference_generate_example_call_sequence(tmp_path):
+    """llm/examples/generate.py:27-33 without the tokenizer, on a local checkpoint: load_model(path,
+    revision=, device=, dtype=, attention_backend=), then generate(**inputs, max_new_tokens=,
+    do_sample=False, use_cache=True, pad_token_id=) with the tokenizer's input_ids and
+    attention_mask.  The model is a small decisive one (tests/decisive_model.py, C = 32, prompts
+    of 100 distinct tokens crossing three chunk boundaries), so the ids are checked exactly:
+    against the construction's closed form, for both attention backends, with use_cache False
+    (full-prefix replay, the reference's test_generate_matches_full_prefix_replay) and True; an
+    EOS id stops a sequence, pads it with pad_token_id and ends the call once all have stopped."""
+
+    import decisive_model as DM
+    from safetensors.torch import save_file
+
+    from lastkv_amd.llm import load_model
+
+    cfg = M.config_8b(hidden_size=768, intermediate_size=1024, num_attention_heads=4, num_key_value_heads=2,
+                      num_hidden_layers=3, vocab_size=1024, chunk_size=32)
+    _, ours, tables = _decisive_pair(cfg, 100, seed=3)
+    save_file({k: v.detach().cpu().contiguous() for k, v in ours.state_dict().items()}, str(tmp_path / "model.safetensors"))
+    saved = ours.config.to_dict()
+    saved["eos_token_id"] = None
+    (tmp_path / "config.json").write_text(json.dumps(saved))
+    prompt = DM.prompts(tables, 2)
+    want = DM.expected_ids(tables, prompt, 20, 32)
+    inputs = {"input_ids": prompt.to(DEV), "attention_mask": torch.ones_like(prompt).to(DEV)}
+    for backend in ("sdpa", "eager"):
+        model = load_model(str(tmp_path), revision="main", device=DEV, dtype=torch.bfloat16, attention_backend=backend)
+        with torch.inference_mode():
+            result = model.generate(**inputs, max_new_tokens=20, do_sample=False, use_cache=True, pad_token_id=0)
+            replay = model.generate(**inputs, max_new_tokens=20, do_sample=False, use_cache=False, pad_token_id=0)
+        assert result.shape == (2, 120) and torch.equal(result[:, :100].cpu(), prompt)
+        assert torch.equal(result[:, 100:].cpu(), want), backend
+        assert torch.equal(replay.cpu(), result.cpu()), backend
+    # EOS (transformers' greedy loop): a sequence that emits an EOS id continues with pad_token_id,
+    # and the call ends at the step where the last sequence emits one
+    eos = [int(want[0, 4]), int(want[1, 8])]
+    stop = [next(i for i, t in enumerate(row) if t in eos) for row in want.tolist()]
+    n = max(stop) + 1
+    expect = torch.stack([torch.cat([want[r, :stop[r] + 1], torch.full((n - stop[r] - 1,), 7)]) for r in range(2)])
+    with torch.inference_mode():
+        out = model.generate(**inputs, max_new_tokens=20, pad_token_id=7, eos_token_id=eos).cpu()
+    assert torch.equal(out[:, 100:], expect)
