@@ -1,0 +1,161 @@
+"""Full-size parity of BASELINE configs 4 and 5 against fp32 attention on the GPU.
+
+The CPU oracle (fp64) cannot run these sizes, so the reference here is the attention the
+reference path computes (modeling.py:109-146 for config 4, videogen/.../attention.py:9-32 over
+_compose_history_kv's history for config 5), evaluated in fp32 with torch on the same bf16
+inputs, one (sequence, kv head) at a time, and rounded to bf16.  The bar is the north star's:
+max-abs 2e-2 and rel-L2 1e-3.
+
+- config 4 decode: B = 4 at position 131072 (the first decode step after a 131072-token prompt at
+  C = 1024): 130048 older shared tokens with the V scale, 1025 ring tokens (the blended previous
+  chunk and the new token) starting mid-ring, the default split count (split-K over the context);
+- config 4 prefill: the last 1024-token chunk piece of the prompt's final 4096-token call (the
+  model's chunk loop cuts every call at C, modeling.py:196-208): queries at positions
+  [130048, 131072) over 129024 older tokens and 2048 ring tokens, bottom-right causal;
+- config 5: the Wan block at 32760 (the 8th 4680-token block, 12 heads) of a WanKVCache rollout
+  with a 1560-token retained prefix: 32760 history keys (prefix | shared | blended previous
+  block) + 4680 bidirectional current keys, checked against oracle/wan.py's history.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from lastkv_amd import ops
+from oracle import attention as A
+from oracle import wan as W
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+MAX_ABS, REL_L2 = 2e-2, 1e-3
+D = 128
+
+
+def _bf16_scale(v: torch.Tensor, s: float) -> torch.Tensor:
+    """bf16(V * s): the reference's older-segment V (modeling.py:93-96)."""
+
+    return (v.float() * torch.tensor(s, dtype=torch.bfloat16).float()).bfloat16()
+
+
+def _attention_fp32(q, k, v, visible=None, rows_per_chunk=2048):
+    """softmax(q k^T / sqrt(128)) v in fp32 for q [R, 128] against k, v [S, 128]; ``visible[r]`` =
+    number of leading keys row r sees (all when None).  Returns fp32 [R, 128]."""
+
+    q, k, v = q.float(), k.float(), v.float()
+    out = torch.empty_like(q)
+    for r0 in range(0, q.shape[0], rows_per_chunk):
+        s = (q[r0:r0 + rows_per_chunk] @ k.T) * D ** -0.5
+        if visible is not None:
+            n = visible[r0:r0 + rows_per_chunk]
+            s = s.masked_fill(torch.arange(k.shape[0], device=q.device)[None, :] >= n[:, None], float("-inf"))
+        out[r0:r0 + rows_per_chunk] = torch.softmax(s, dim=-1) @ v
+    return out
+
+
+def _check(got: torch.Tensor, want32: torch.Tensor, label: str):
+    a = got.float().cpu().numpy()
+    e = want32.bfloat16().float().cpu().numpy()
+    ma, rl = A.max_abs(a, e), A.rel_l2(a, e)
+    print(f"{label}: max_abs={ma:.3e} rel_l2={rl:.3e}", flush=True)
+    assert ma <= MAX_ABS and rl <= REL_L2, f"{label}: max_abs={ma} rel_l2={rl}"
+
+
+def _long_context(seed, B, Hkv, older_len, local_len, chunk=1024):
+    """Random shared store of older_len tokens and a ring holding local_len tokens from ring token
+    rec % R (its position in the drop-in cache's ring), as tiled caches and [B, H, T, 128] tensors."""
+
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    R = ops.ring_tokens_for_chunk(chunk)
+    start = older_len % R
+    ok = torch.randn((B, Hkv, older_len, D), generator=g, device=DEV).bfloat16()
+    ov = torch.randn((B, Hkv, older_len, D), generator=g, device=DEV).bfloat16()
+    lk = torch.randn((B, Hkv, local_len, D), generator=g, device=DEV).bfloat16()
+    lv = torch.randn((B, Hkv, local_len, D), generator=g, device=DEV).bfloat16()
+    store = ops.TiledKV.zeros(B, Hkv, -(-older_len // 32) * 32, DEV)
+    ops.pack_kv(ok, ov, store)
+    ring = ops.TiledKV.zeros(B, Hkv, R, DEV)
+    first = min(local_len, R - start)
+    ops.pack_kv(lk[:, :, :first].contiguous(), lv[:, :, :first].contiguous(), ring, token0=start)
+    if first < local_len:
+        ops.pack_kv(lk[:, :, first:].contiguous(), lv[:, :, first:].contiguous(), ring, token0=0)
+    return store, ring, start, (ok, ov, lk, lv), g
+
+
+def test_config4_decode_128k_against_fp32():
+    B, Hq, Hkv, C = 4, 32, 8, 1024
+    pos = 131072
+    rec = pos // C * C - C
+    local_len = pos + 1 - rec
+    store, ring, start, (ok, ov, lk, lv), g = _long_context(41, B, Hkv, rec, local_len, C)
+    scales = [0.55, 0.7, 0.85, 1.0, 1.15, 0.6, 0.9, 1.25]
+    vscale = torch.tensor(scales, dtype=torch.bfloat16).float().to(DEV)
+    q = torch.randn((B, Hq, D), generator=g, device=DEV).bfloat16()
+    splits = ops.default_decode_splits(B, Hkv, rec + local_len, torch.cuda.get_device_properties(0).multi_processor_count)
+    print(f"config 4 decode: older {rec} + ring {local_len} tokens from ring token {start}, {splits} splits", flush=True)
+    out = ops.decode_attention(q, older=store, older_len=rec, vscale=vscale, local=ring, local_len=local_len,
+                               local_start=start, num_splits=splits)
+    G = Hq // Hkv
+    want = torch.empty((B, Hq, D), dtype=torch.float32, device=DEV)
+    for b in range(B):
+        for h in range(Hkv):
+            k = torch.cat([ok[b, h], lk[b, h]])
+            v = torch.cat([_bf16_scale(ov[b, h], scales[h]), lv[b, h]])
+            want[b, h * G:(h + 1) * G] = _attention_fp32(q[b, h * G:(h + 1) * G], k, v)
+    _check(out, want, "config 4 decode B=4 @131072")
+
+
+def test_config4_prefill_piece_at_128k_against_fp32():
+    B, Hq, Hkv, C, L = 4, 32, 8, 1024, 1024
+    cur = 131072 - C  # the last chunk piece of the prompt: queries at [130048, 131072)
+    rec = cur - C
+    local_len = cur + L - rec
+    store, ring, start, (ok, ov, lk, lv), g = _long_context(42, B, Hkv, rec, local_len, C)
+    scales = [1.1, 0.65, 0.8, 0.95, 1.2, 0.75, 0.5, 1.05]
+    vscale = torch.tensor(scales, dtype=torch.bfloat16).float().to(DEV)
+    q = torch.randn((B, L, Hq, D), generator=g, device=DEV).bfloat16()
+    print(f"config 4 prefill piece: {L} queries, older {rec} + ring {local_len} tokens from {start}", flush=True)
+    out = ops.prefill_attention(q, older=store, older_len=rec, vscale=vscale, local=ring, local_len=local_len,
+                                local_start=start, causal=True)
+    G = Hq // Hkv
+    # row (token i, head) sees the older segment and local tokens [0, local_len - L + i]
+    visible = (rec + local_len - L + 1 + torch.arange(L, device=DEV)).repeat_interleave(G)
+    for b in range(B):
+        for h in range(Hkv):
+            k = torch.cat([ok[b, h], lk[b, h]])
+            v = torch.cat([_bf16_scale(ov[b, h], scales[h]), lv[b, h]])
+            qr = q[b, :, h * G:(h + 1) * G].reshape(L * G, D)
+            want = _attention_fp32(qr, k, v, visible).view(L, G, D)
+            _check(out[b, :, h * G:(h + 1) * G], want, f"config 4 prefill piece b={b} kv head {h}")
+
+
+def test_config5_wan_block8_full_size_against_oracle_history():
+    from lastkv_amd.videogen import WanKVCache
+
+    Lyr, H, S, keep, nblk = 3, 12, 4680, 1560, 8
+    total = (nblk - 1) * S
+    cache = WanKVCache(num_layers=Lyr, num_heads=H, block_tokens=S, total_tokens=total, keep_tokens=keep, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    cache.set_alphas(torch.randn((Lyr, H), generator=torch.Generator().manual_seed(6)))
+    alphas = cache.alpha.view(Lyr, H).cpu().numpy()
+    oracle = W.WanCache(Lyr, 1, H, total, S, keep, shared=True)
+    rnd = lambda: torch.randn((1, S, H, D), generator=g, device=DEV).bfloat16()
+    np32 = lambda t: t.float().cpu().numpy()
+    for blk in range(nblk - 1):
+        kvs = [(rnd(), rnd()) for _ in range(Lyr)]
+        cache.commit(blk * S, kvs)
+        oracle.commit([(np32(k), np32(v)) for k, v in kvs], blk * S)
+    s = (nblk - 1) * S
+    for layer in range(Lyr):
+        q, k, v = rnd(), rnd(), rnd()
+        out = cache.attention(layer, q, k, v, s)
+        hk, hv = oracle.history(layer, s, S, alphas[layer])
+        gk, gv = cache.history(layer, s)
+        assert np.array_equal(np32(gk), hk) and np.array_equal(np32(gv), hv), f"history of layer {layer}"
+        keys = torch.cat([torch.from_numpy(hk).to(DEV), k.float()], 1)[0]  # [37440, H, 128]
+        vals = torch.cat([torch.from_numpy(hv).to(DEV), v.float()], 1)[0]
+        assert keys.shape[0] == nblk * S
+        for h in range(H):
+            want = _attention_fp32(q[0, :, h], keys[:, h], vals[:, h])
+            _check(out[0, :, h], want, f"config 5 block 8 layer {layer} head {h}")
