@@ -209,3 +209,47 @@ def test_decode_graph_replays_match_eager_steps():
             if i % 3 == 0:
                 torch.cuda.synchronize()
     assert graphed.fast.seen(sg[0]) == eager.fast.seen(se[0]) == prompts[0].numel() + 40
+
+
+def test_vllm_impl_adapter_runs_the_fast_path():
+    """lastkv_amd.vllm_backend.LastKVAttentionImpl.forward (the reference's Impl contract,
+    vllm_backend.py:637-717) over steps prepared on the current fast path: a ragged prefill step,
+    a uniform prefill step and padded decode steps crossing a chunk boundary.  vLLM hands it padded
+    buffers (more rows than num_actual_tokens); rows past the real tokens must come back zero and
+    the real rows must equal LastKVFastPath.run_layer's output bit for bit."""
+
+    from types import SimpleNamespace
+
+    from lastkv_amd import vllm_backend as VB
+
+    _, ours = _tiny(chunk=8)
+    cfg = ours.config
+    Hq, Hkv, L = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
+    runner = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=64)
+    fast = runner.fast
+    slots = [runner.add_sequence() for _ in range(3)]
+    impl = VB.LastKVAttentionImpl(Hq, 128, 128 ** -0.5, Hkv, None, None, "auto")
+    g = torch.Generator(device=DEV).manual_seed(9)
+    steps = [([(slots[0], 5), (slots[1], 3), (slots[2], 8)], None), ([(s, 2) for s in slots], None)]
+    steps += [([(s, 1) for s in slots], 4)] * 6
+    VB.set_current(fast)
+    try:
+        for i, (rows, pad) in enumerate(steps):
+            fast.prepare(rows, pad_to=pad)
+            T = fast.tokens
+            actual = sum(n for _, n in rows)
+            for l in range(L):
+                q = torch.randn((T + 3, Hq * 128), generator=g, device=DEV).bfloat16()
+                k = torch.randn((T + 3, Hkv * 128), generator=g, device=DEV).bfloat16()
+                v = torch.randn((T + 3, Hkv * 128), generator=g, device=DEV).bfloat16()
+                out = torch.full((T + 3, Hq, 128), 7.0, dtype=torch.bfloat16, device=DEV)
+                got = impl.forward(SimpleNamespace(rmarin_layer_index=l), q, k, v, None,
+                                   SimpleNamespace(num_actual_tokens=actual), out)
+                ref = torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=DEV)
+                fast.run_layer(l, q[:T], k[:T], v[:T], ref)
+                assert got is out
+                assert torch.equal(out[:actual], ref[:actual]), f"step {i} layer {l}"
+                assert not out[actual:].any(), f"step {i} layer {l}: padded rows not zero"
+        assert impl.forward(SimpleNamespace(rmarin_layer_index=0), q, k, v, None, None, out) is out and not out.any()
+    finally:
+        VB.set_current(None)
