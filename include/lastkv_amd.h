@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 6
+#define LKV_ABI_VERSION 7
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -147,6 +147,23 @@ typedef struct lkv_decode_args {
 int64_t lkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_splits);
 
 int32_t lkv_decode_attn(const lkv_decode_args *args, lkv_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Allocation-free variant of lkv_decode_attn.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving loops or harnesses
+ * that forbid hipMalloc) and cannot keep a workspace of their own.  Same arguments, kernels and
+ * results as lkv_decode_attn, except that args->workspace must be NULL and workspace_bytes 0: the
+ * split-K partial states live in a static device array of LKV_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every GPU it runs on until the process ends.  Calls whose
+ * lkv_decode_workspace_bytes(batch, num_q_heads, num_splits) exceeds it are rejected
+ * (LKV_ERR_INVALID_ARGUMENT).  Nothing is allocated and nothing needs clearing (every split writes
+ * its whole partial state), but every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (streams or host threads running concurrently) race and must be serialised by the
+ * caller.  Call it with the stream's device current.
+ * ------------------------------------------------------------------------------------- */
+#define LKV_NOALLOC_SCRATCH_BYTES (16 << 20)
+
+int32_t lkv_decode_attn_noalloc(const lkv_decode_args *args, lkv_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
  * Chunked-prefill attention (L >= 1 query tokens per sequence, MFMA).

@@ -13,6 +13,7 @@
 // workgroup writes the normalised bf16 output; otherwise it writes an unnormalised partial
 // state and lkv_decode_combine merges the splits.
 #include <algorithm>
+#include <atomic>
 
 #include "attn_common.h"
 #include "common.h"
@@ -432,8 +433,11 @@ extern "C" int64_t lkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads
   return static_cast<int64_t>(batch) * num_q_heads * num_splits * (lkv::kHeadDim + 2) * 4;
 }
 
-extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream) {
-  using namespace lkv;
+namespace lkv {
+namespace {
+
+// Argument checks of lkv_decode_attn and lkv_decode_attn_noalloc (no device calls).
+int32_t check_decode_args(const lkv_decode_args* a) {
   LKV_REQUIRE(a != nullptr, "null args");
   LKV_REQUIRE(a->struct_size == static_cast<int32_t>(sizeof(lkv_decode_args)),
               "lkv_decode_args size mismatch (caller %d, library %d)", a->struct_size,
@@ -441,8 +445,7 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   LKV_REQUIRE(a->head_dim == kHeadDim, "head_dim must be 128, got %d", a->head_dim);
   LKV_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->num_q_heads > 0, "bad sizes");
   LKV_REQUIRE(a->num_q_heads % a->num_kv_heads == 0, "num_q_heads must be a multiple of num_kv_heads");
-  const int group = a->num_q_heads / a->num_kv_heads;
-  LKV_REQUIRE(group <= 64, "GQA group %d exceeds 64", group);
+  LKV_REQUIRE(a->num_q_heads / a->num_kv_heads <= 64, "GQA group %d exceeds 64", a->num_q_heads / a->num_kv_heads);
   LKV_REQUIRE(a->num_splits >= 1 && a->num_splits <= 1024, "num_splits must be in [1, 1024]");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->older_vscale_mode == 1, "older_vscale_mode must be 0 or 1");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->vscale != nullptr, "older_vscale_mode 1 needs vscale");
@@ -450,16 +453,21 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   LKV_REQUIRE(a->q != nullptr && a->out != nullptr, "null q/out");
   LKV_REQUIRE((a->q_stride_b % 8) == 0 && (reinterpret_cast<uintptr_t>(a->q) & 15) == 0,
               "q rows must be 16-byte aligned");
+  return LKV_OK;
+}
+
+// The decode call of checked args with the split partials in `ws` (ws_bytes bytes).
+int32_t run_decode(const lkv_decode_args* a, void* ws, int64_t ws_bytes, hipStream_t stream) {
   DecodeParams p;
   if (const int32_t st = fill_segments(a, p.seg)) return st;
   if (a->batch == 0) return LKV_OK;
+  const int group = a->num_q_heads / a->num_kv_heads;
   const int64_t need = lkv_decode_workspace_bytes(a->batch, a->num_q_heads, a->num_splits);
   if (need > 0) {
-    if (a->workspace == nullptr || a->workspace_bytes < need)
+    if (ws == nullptr || ws_bytes < need)
       return fail(LKV_ERR_WORKSPACE, "decode workspace needs %lld bytes, got %lld", static_cast<long long>(need),
-                  static_cast<long long>(a->workspace_bytes));
-    if ((reinterpret_cast<uintptr_t>(a->workspace) & 15) != 0)
-      return fail(LKV_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+                  static_cast<long long>(ws_bytes));
+    if ((reinterpret_cast<uintptr_t>(ws) & 15) != 0) return fail(LKV_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   }
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_stride_b;
@@ -471,7 +479,7 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   p.causal = 0;
   p.lse = a->lse;
   p.vscale = a->vscale;
-  p.ws_o = static_cast<float*>(a->workspace);
+  p.ws_o = static_cast<float*>(ws);
   p.ws_ml = need > 0 ? p.ws_o + static_cast<int64_t>(a->batch) * a->num_q_heads * a->num_splits * kHeadDim : nullptr;
   p.hq = a->num_q_heads;
   p.group = group;
@@ -481,6 +489,59 @@ extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream
   // groups above 16 query heads per kv head take the multi-column instances (columns = heads)
   const int cg = group <= 16 ? 0 : group <= 32 ? 2 : 4;
   return launch_decode(p, dim3(a->num_splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1,
-                       use_nontemporal(a->kv_cache_hint, kv_bytes), cg, a->batch * a->num_q_heads, as_stream(stream),
+                       use_nontemporal(a->kv_cache_hint, kv_bytes), cg, a->batch * a->num_q_heads, stream,
                        "lkv_decode_attn");
+}
+
+// Scratch of the allocation-free entry point: the split partials of one call, in a static device
+// array that each GPU holds for the life of the process.  Host code must not use the array's name
+// as a device address (it is a host-side stand-in): the address on a device comes from
+// hipGetSymbolAddress, taken once per device with that device current and kept here.
+constexpr int64_t kNoAllocScratchBytes = LKV_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of the current device's scratch.
+int32_t current_device_scratch(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(LKV_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxScratchDevices) return fail(LKV_ERR_UNSUPPORTED, "device %d beyond the scratch table", dev);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr)
+      return fail(LKV_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(err));
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return LKV_OK;
+}
+
+}  // namespace
+}  // namespace lkv
+
+extern "C" int32_t lkv_decode_attn(const lkv_decode_args* a, lkv_stream_t stream) {
+  using namespace lkv;
+  if (const int32_t st = check_decode_args(a)) return st;
+  return run_decode(a, a->workspace, a->workspace_bytes, as_stream(stream));
+}
+
+extern "C" int32_t lkv_decode_attn_noalloc(const lkv_decode_args* a, lkv_stream_t stream) {
+  using namespace lkv;
+  if (const int32_t st = check_decode_args(a)) return st;
+  LKV_REQUIRE(a->workspace == nullptr && a->workspace_bytes == 0,
+              "lkv_decode_attn_noalloc uses the library's static scratch: workspace must be NULL and workspace_bytes 0");
+  const int64_t need = lkv_decode_workspace_bytes(a->batch, a->num_q_heads, a->num_splits);
+  LKV_REQUIRE(need <= kNoAllocScratchBytes,
+              "%d splits of %d x %d query heads need %lld bytes of split state, more than the %lld bytes of static "
+              "scratch: use fewer splits, or lkv_decode_attn with a workspace",
+              a->num_splits, a->batch, a->num_q_heads, static_cast<long long>(need),
+              static_cast<long long>(kNoAllocScratchBytes));
+  void* ws = nullptr;
+  if (need > 0 && a->batch > 0) {
+    if (const int32_t st = current_device_scratch(&ws)) return st;
+  }
+  return run_decode(a, ws, kNoAllocScratchBytes, as_stream(stream));
 }

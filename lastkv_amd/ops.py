@@ -310,13 +310,17 @@ def decode_attention(
     lse: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     kv_cache_hint: int = 0,
+    no_alloc: bool = False,
 ) -> torch.Tensor:
     """One-token-per-sequence attention over ``[older shared segment | local ring segment]``.
 
     ``q`` is ``[B, Hq, 128]`` bf16 (or ``[B, Hq, 1, 128]``).  ``vscale`` ``[Hkv]`` fp32 switches
     the older segment's V to ``bf16(V * vscale[h])``.  Returns ``out`` ``[B, Hq, 128]`` bf16.
     ``kv_cache_hint`` selects the cache policy of the K/V loads (0 = by the call's K/V size,
-    1 = default, 2 = non-temporal); the results do not depend on it.
+    1 = default, 2 = non-temporal); the results do not depend on it.  ``no_alloc`` calls
+    ``lkv_decode_attn_noalloc``: the split states go to the library's static per-GPU scratch
+    (LKV_NOALLOC_SCRATCH_BYTES) instead of a workspace (pass ``out`` too for a call that allocates
+    nothing); calls overlapping on one GPU then race.
     """
 
     _require_bf16_cuda("q", q)
@@ -351,7 +355,9 @@ def decode_attention(
         num_splits = default_decode_splits(B, Hkv, max_tokens, _cu_count(device))
     lib = _lib.load()
     need = lib.lkv_decode_workspace_bytes(B, Hq, num_splits)
-    if need > 0:
+    if no_alloc:
+        _require(workspace is None, "no_alloc calls use the library's static scratch, not a workspace")
+    elif need > 0:
         if workspace is None:
             workspace = torch.empty(need, dtype=torch.uint8, device=device)
         _require(workspace.device == device and workspace.numel() * workspace.element_size() >= need, "workspace too small")
@@ -364,7 +370,10 @@ def decode_attention(
     a.lse = _ptr(lse)
     a.workspace = _ptr(workspace)
     a.workspace_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    _lib.check(lib.lkv_decode_attn(ctypes.byref(a), _stream(device)), "lkv_decode_attn")
+    if no_alloc:
+        _lib.check(lib.lkv_decode_attn_noalloc(ctypes.byref(a), _stream(device)), "lkv_decode_attn_noalloc")
+    else:
+        _lib.check(lib.lkv_decode_attn(ctypes.byref(a), _stream(device)), "lkv_decode_attn")
     return out
 
 

@@ -106,3 +106,15 @@ def test_prefill_causal_needs_the_queries_own_keys(local_len, ok_expected):
         assert status == 0  # batch 0: validated, nothing launched
     else:
         assert status == 1 and b"local_len >= tokens" in lib.lkv_last_error()
+
+
+@pytest.mark.parametrize("batch,splits,workspace,message", [(64, 16, 0, b"static scratch"), (1, 2, 64, b"workspace must be NULL")])
+def test_noalloc_decode_rejections_before_any_launch(batch, splits, workspace, message):
+    lib = _lib.load()
+    a = _lib.DecodeArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim, a.num_splits = batch, 64, 8, 128, splits
+    a.q = a.out = 16
+    a.workspace, a.workspace_bytes = (16, workspace) if workspace else (None, 0)
+    assert lib.lkv_decode_attn_noalloc(ctypes.byref(a), None) == 1
+    assert message in lib.lkv_last_error()
