@@ -22,6 +22,8 @@ Printed JSON line (one, from this single process):
                  the 2.5 PFLOP/s dense bf16 peak
   configs        the other BASELINE configs, measured in the same run:
                  config4_decode_128k  lkv_decode_attn at B=4, 131072-token context (split-K), GB/s
+                 config4_prefill_128k the last 4096-token prefill call of the 128K prompt (4 chunk
+                                      pieces of 1024 queries), MFMA %
                  config5_wan          Wan-1.3B block attention over its full history structure,
                                       30 layers, MFMA %
                  config3_e2e_8b       the 8B-shape model: chunked prefill of 32 x 8192 tokens,
@@ -61,12 +63,16 @@ def parse_args():
     ap.add_argument("--splits", type=int, default=None, help="key splits per (sequence, kv head); default: heuristic")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-configs", action="store_true",
+                    help="time only config 2 on the CPU (skip the configs 2-fp32 / 3 / 4 / 5 CPU samples)")
+    ap.add_argument("--cpu-model-step", action="store_true",
+                    help="also time full 8B-shape decode steps of the reference model on the CPU (slow)")
     ap.add_argument("--sweep-splits", action="store_true", help="print the kernel time for several split counts")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA measurement")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 4 (128K decode), config 5 (Wan) and config 3 (8B end to end) measurements")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy decode steps of the config 3 model run")
-    ap.add_argument("--only", choices=["prefill", "short", "config4", "config5", "config3"], default=None,
+    ap.add_argument("--only", choices=["prefill", "short", "config4", "config4p", "config5", "config3"], default=None,
                     help="run one secondary measurement alone and print its JSON (for profiling); "
                          "this is not the bench line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -153,6 +159,52 @@ def decode_long_measurement(ops, torch, dev, layers: int = 32) -> dict:
         "bytes_per_call": nbytes, "num_splits": splits, "kernel_us_per_call": round(us, 2),
         "attn_hbm_gbps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "attn_step_tok_s": round(Bl / (us * layers * 1e-6), 1),
+    }
+
+
+def prefill_long_measurement(ops, torch, dev, reps: int = 3) -> dict:
+    """BASELINE config 4's chunked prefill at the end of the 128K prompt: the final 4096-token call
+    (positions [126976, 131072)), which the model's chunk loop cuts into 4 chunk pieces of 1024
+    query tokens (modeling.py:196-208); each piece attends to the older shared segment (rec tokens,
+    V scale on) and the ring (blended previous chunk + its own chunk, bottom-right causal).  B=4,
+    Hq=32, Hkv=8: 32 (sequence, kv head) pairs x 32 query tiles per piece."""
+
+    Bl, Tl, C, call = 4, 131072, CHUNK, 4096
+    R = ops.ring_tokens_for_chunk(C)
+    g = torch.Generator(device=dev).manual_seed(7)
+    store = ops.TiledKV(torch.randn((Bl, HKV, Tl // 32, 4096), generator=g, device=dev).bfloat16(),
+                        torch.randn((Bl, HKV, Tl // 32, 4096), generator=g, device=dev).bfloat16())
+    ring = ops.TiledKV(torch.randn((Bl, HKV, R // 32, 4096), generator=g, device=dev).bfloat16(),
+                       torch.randn((Bl, HKV, R // 32, 4096), generator=g, device=dev).bfloat16())
+    q = torch.randn((Bl, C, HQ, D), generator=g, device=dev).bfloat16()
+    out = torch.empty_like(q)
+    vscale = torch.full((HKV,), 0.5, device=dev)
+    workspace = torch.empty(ops.prefill_workspace_bytes(Bl, HKV, Tl - 2 * C, 2 * C, 0), dtype=torch.uint8, device=dev)
+    pieces, pairs = [], 0
+    for cur in range(Tl - call, Tl, C):
+        rec = cur - C
+        pieces.append(dict(older=store, older_len=rec, vscale=vscale, local=ring, local_len=cur + C - rec,
+                           local_start=rec % R, causal=True, out=out, workspace=workspace))
+        pairs += C * rec + C * C + C * (C + 1) // 2
+    flops = 4 * D * HQ * Bl * pairs
+    for kw in pieces:
+        ops.prefill_attention(q, **kw)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for kw in pieces:
+            ops.prefill_attention(q, **kw)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    tflops = flops / (ms * 1e-3) / 1e12
+    del store, ring, workspace
+    return {
+        "workload": "config 4 prefill attention, one layer: the final 4096-token call of a 131072-token prompt "
+                    "(4 chunk pieces of 1024 queries at positions 126976-131071), B=4",
+        "flops_per_call": flops, "ms_per_call": round(ms, 3), "achieved_tflops": round(tflops, 1),
+        "peak_tflops": MFMA_PEAK_TFLOPS, "mfma_pct": round(100 * tflops / MFMA_PEAK_TFLOPS, 2),
     }
 
 
@@ -399,6 +451,102 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+def _cpu_time(fn, seconds: float, max_runs: int = 20) -> tuple[float, int]:
+    """Median wall time of fn() after one warm-up, over at least 3 runs and about ``seconds``."""
+
+    fn()
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < seconds and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline_configs(seconds: float, model_step: bool = False) -> dict:
+    """The rest of the CPU baseline plan, each a bounded sample of the torch
+    restatement of the reference path (torch.cat composition + SDPA, oracle/reference_path.py) on
+    this host's cores: config 2 in fp32; the attention layer-call of configs 3 and 4 at their decode
+    positions (older shared region with the V scale, blended recent chunk, current token); one Wan
+    layer's block attention (config 5); and, with ``model_step`` (tens of seconds per step), full
+    8B-shape decode steps of the reference model at B = 32, 8K context in fp32, the reference CPU
+    path's dtype (config 3; the 32 layers share one set of weights, which does not change the work).  Full 8B prefill at 8K / 128K on the CPU is infeasible and not attempted."""
+
+    import torch
+    from torch.nn import functional as F
+
+    from oracle import model as M
+    from oracle.reference_path import compose, lastkv_attention, sdpa_bottom_right
+
+    g = torch.Generator().manual_seed(11)
+    bf = torch.bfloat16
+    rnd = lambda *shape, dtype=bf: torch.randn(shape, generator=g).to(dtype)
+    res = {}
+
+    k, v, q = rnd(B, HKV, T, D, dtype=torch.float32), rnd(B, HKV, T, D, dtype=torch.float32), rnd(B, HQ, 1, D, dtype=torch.float32)
+    sec, n = _cpu_time(lambda: sdpa_bottom_right(q, k, v, native_gqa=True), seconds)
+    res["config2_fp32_layer_call"] = {"ms": round(sec * 1e3, 2), "runs": n, "gbps_bf16_bytes": round(BYTES_PER_CALL / sec / 1e9, 2),
+                                      "tok_s": round(B / (sec * LAYERS), 3)}
+    del k, v, q
+
+    alpha, vscale = torch.full((HKV,), -1.0), torch.linspace(0.6, 1.2, HKV)
+    for name, Bc, pos in (("config3_attn_decode_8k", B, 8192), ("config4_attn_decode_128k", 4, 131072)):
+        deep = (rnd(Bc, HKV, pos, D), rnd(Bc, HKV, pos, D))
+        prev = (rnd(Bc, HKV, CHUNK, D), rnd(Bc, HKV, CHUNK, D))
+        cur = (rnd(Bc, HKV, 1, D), rnd(Bc, HKV, 1, D))
+        qd = rnd(Bc, HQ, 1, D)
+        sec, n = _cpu_time(lambda: lastkv_attention(qd, deep, prev, cur, alpha, vscale, CHUNK), seconds)
+        nbytes = 2 * Bc * HKV * (pos + 1) * D * 2 + 2 * Bc * HQ * D * 2
+        res[name] = {"ms": round(sec * 1e3, 2), "runs": n, "gbps": round(nbytes / sec / 1e9, 2),
+                     "batch": Bc, "position": pos}
+        del deep, prev, cur, qd
+
+    S, keys, Hw = 4680, 37440, 12
+    qw, kw, vw = rnd(1, Hw, S, D), rnd(1, Hw, keys, D), rnd(1, Hw, keys, D)
+    sec, n = _cpu_time(lambda: F.scaled_dot_product_attention(qw, kw, vw), seconds, max_runs=5)
+    flops = 4 * Hw * D * S * keys
+    res["config5_wan_layer_attention"] = {"ms": round(sec * 1e3, 1), "runs": n, "tflops": round(flops / sec / 1e12, 3)}
+    del qw, kw, vw
+
+    if not model_step:
+        return res
+    # the reference's CPU path runs in fp32 (load_model's defaults, llm/src/lastkv/llm/__init__.py:13-14)
+    f32 = torch.float32
+    cfg = M.config_8b()
+    layer = M.DecoderLayer(cfg, 0).eval()
+    embed = torch.nn.Embedding(cfg.vocab_size, cfg.hidden_size)
+    lm_head = torch.nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
+    norm = M.RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+    with torch.no_grad():
+        for t in list(layer.parameters()) + [embed.weight, lm_head.weight]:
+            if t.dim() > 1:
+                t.uniform_(-0.02, 0.02, generator=g)
+    inv_freq, rope_scale = M.rope_inv_freq(cfg)
+    cache = M.Cache(cfg.num_hidden_layers, cfg.chunk_size)
+    cache.seen_tokens = T
+    cache.deep = (rnd(B, HKV, T, D, dtype=f32), rnd(B, HKV, T, D, dtype=f32))
+    prev = (rnd(B, HKV, CHUNK, D, dtype=f32), rnd(B, HKV, CHUNK, D, dtype=f32))
+    cache.previous = [prev] * cfg.num_hidden_layers
+    ids = torch.randint(0, cfg.vocab_size, (B, 1), generator=g)
+
+    def step():
+        with torch.no_grad():
+            pos = torch.full((1, 1), cache.seen_tokens)
+            pe = M.rotary_cos_sin(inv_freq, rope_scale, pos, f32)
+            h = embed(ids)
+            for l in range(cfg.num_hidden_layers):
+                layer.self_attn.layer_idx = l
+                h = layer(h, pe, cache)
+            lm_head(norm(h)).argmax(-1)
+            cache.seen_tokens += 1
+
+    sec, n = _cpu_time(step, seconds, max_runs=5)
+    res["config3_model_decode_step_8k_fp32"] = {"ms": round(sec * 1e3, 1), "runs": n, "tok_s": round(B / sec, 2),
+                                                "batch": B, "position": T}
+    return res
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -422,6 +570,8 @@ def main() -> int:
             res = short_prefill_measurement(ops, torch, cache, dev)
         elif args.only == "config4":
             res = decode_long_measurement(ops, torch, dev)
+        elif args.only == "config4p":
+            res = prefill_long_measurement(ops, torch, dev)
         elif args.only == "config5":
             res = wan_measurement(ops, torch, dev)
         else:
@@ -478,6 +628,7 @@ def main() -> int:
         del qs, outs
         configs = {"short_prefill_calls": short_prefill_measurement(ops, torch, cache, dev),
                    "config4_decode_128k": decode_long_measurement(ops, torch, dev),
+                   "config4_prefill_128k": prefill_long_measurement(ops, torch, dev),
                    "config5_wan": wan_measurement(ops, torch, dev)}
         del cache
         torch.cuda.empty_cache()
@@ -488,10 +639,12 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    traffic = None
+    traffic, traffic_source = None, None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
+        traffic_source = ("profile, not measured in this run: " + os.path.relpath(TRAFFIC_FILE, REPO)
+                          + " (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE per dispatch, scaled by a 1 GiB copy)")
     result = {
         "metric": METRIC,
         "value": round(B / (ms_per_step * 1e-3), 2),
@@ -519,11 +672,14 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
         "prefill": prefill,
         "configs": configs,
     }
+    if result["cpu_baseline"] is not None and not args.no_cpu_configs:
+        result["cpu_baseline"]["configs"] = cpu_baseline_configs(min(args.cpu_seconds, 5.0), args.cpu_model_step)
     print(json.dumps(result), flush=True)
     return 0
 
