@@ -277,7 +277,9 @@ class Decoder(nn.Module):
         self.layers = nn.ModuleList(DecoderLayer(config, i) for i in range(config.num_hidden_layers))
         self.norm = RMSNorm(config.hidden_size, config.rms_norm_eps)
         # kept out of the module's buffers so that casting the model to bf16 leaves it fp32
-        self.inv_freq, self.rope_scaling_factor = rope_inv_freq(config)
+        # (on the CPU whatever the default device, so a model built on "meta" keeps real tables)
+        with torch.device("cpu"):
+            self.inv_freq, self.rope_scaling_factor = rope_inv_freq(config)
 
     def forward(self, input_ids, cache: Cache | None = None):
         """modeling.py:173-212 (input validation :175-193, chunk loop :196-208)."""
