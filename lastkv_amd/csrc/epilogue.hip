@@ -1,8 +1,9 @@
 // Fused QKV epilogue (RoPE + q/k RMSNorm + tiled K/V cache append) and the chunk-boundary blend.
 //
-// Epilogue: one wave per (token, head) of the Hq + Hkv heads; lane l owns dims l and l + 64, the
-// two halves that rotate_half pairs, so RoPE needs no lane exchange and RMSNorm one wave sum.
-// Every intermediate is rounded to bf16 where the reference's bf16 torch ops round.
+// Epilogue, decode-sized calls: one wave per (token, head) of the Hq + Hkv heads; lane l owns dims
+// l and l + 64, the two halves that rotate_half pairs, so RoPE needs no lane exchange and RMSNorm
+// one wave sum.  Calls of many tokens: the block form below (16-byte accesses, V tiles written
+// through LDS).  Every intermediate is rounded to bf16 where the reference's bf16 torch ops round.
 #include "common.h"
 #include "runtime.h"
 
@@ -119,6 +120,166 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
       kb[k_tile_offset(wt, lane + 64)] = o1;
       vb[v_tile_offset(wt, lane)] = v0;
       vb[v_tile_offset(wt, lane + 64)] = v1;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Block form of the epilogue for calls of many tokens (prefill pieces): the same arithmetic with
+// 16-byte loads and stores.  Eight lanes own one 128-dim row; lane l of the eight holds dims
+// [8l, 8l + 8) and [64 + 8l, 64 + 8l + 8), the pairs rotate_half combines, so RoPE needs no lane
+// exchange and RMSNorm's sum three xor shuffles.  The first workgroups take one (sequence,
+// 32-position block, kv head) each: K goes to its tile row by row (64-byte runs), V is transposed
+// through LDS and written to its tile (d-major) with 16-byte stores, both to the ring block and, on
+// the final layer, to the shared-store block.  The others take query rows, four heads of one token
+// per 8-lane group.
+constexpr int kRowLanes = 8;
+constexpr int kVStride = 40;  // LDS row of one V dim: 32 tokens + 8 pad elements (80 bytes, 16-byte aligned)
+
+__device__ inline void unpack8(uint4 u, float (&x)[8]) {
+  x[0] = bf16_lo(u.x), x[1] = bf16_hi(u.x), x[2] = bf16_lo(u.y), x[3] = bf16_hi(u.y);
+  x[4] = bf16_lo(u.z), x[5] = bf16_hi(u.z), x[6] = bf16_lo(u.w), x[7] = bf16_hi(u.w);
+}
+
+__device__ inline uint4 pack8(const float (&x)[8]) {
+  return make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
+}
+
+// RoPE then RMSNorm of the row held by an 8-lane group (lane l: dims 8l.. in a / 64 + 8l.. in b).
+__device__ inline void rope_norm_row(uint4& a, uint4& b, uint4 ca, uint4 cb, uint4 sa, uint4 sb, const uint16_t* w,
+                                     int l, float eps) {
+  float x0[8], x1[8], c0[8], c1[8], s0[8], s1[8], r0[8], r1[8];
+  unpack8(a, x0), unpack8(b, x1), unpack8(ca, c0), unpack8(cb, c1), unpack8(sa, s0), unpack8(sb, s1);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    r0[j] = rb(rb(x0[j] * c0[j]) + rb(-x1[j] * s0[j]));
+    r1[j] = rb(rb(x1[j] * c1[j]) + rb(x0[j] * s1[j]));
+  }
+  if (w != nullptr) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += r0[j] * r0[j] + r1[j] * r1[j];
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHeadDim) + eps);
+    float w0[8], w1[8];
+    unpack8(*reinterpret_cast<const uint4*>(w + 8 * l), w0);
+    unpack8(*reinterpret_cast<const uint4*>(w + 64 + 8 * l), w1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      r0[j] = rb(w0[j] * rb(r0[j] * inv));
+      r1[j] = rb(w1[j] * rb(r1[j] * inv));
+    }
+  }
+  a = pack8(r0);
+  b = pack8(r1);
+}
+
+__device__ inline void load_row(const uint16_t* row, int l, uint4& a, uint4& b) {
+  a = *reinterpret_cast<const uint4*>(row + 8 * l);
+  b = *reinterpret_cast<const uint4*>(row + 64 + 8 * l);
+}
+
+// Projection rows are read once and outputs written once per call: non-temporal accesses keep them
+// from displacing the cos / sin rows and norm weights that every head rereads.
+__device__ inline void load_row_nt(const uint16_t* row, int l, uint4& a, uint4& b) {
+  a = load_nt(row + 8 * l);
+  b = load_nt(row + 64 + 8 * l);
+}
+
+__device__ inline void store_nt(uint16_t* dst, uint4 v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
+}
+
+constexpr int kQRows = 4;  // query heads of one token per 8-lane group (one cos / sin load for all)
+
+// Workgroups [0, kv_wgs) take one (sequence, 32-position block, kv head) each; the rest 32 groups of
+// kQRows query rows (heads [kQRows j, kQRows j + kQRows) of one token, j < ceil(Hq / kQRows)).
+__global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32_t kv_wgs, int32_t kv_blocks) {
+  __shared__ uint16_t sv[kHeadDim * kVStride];
+  const int t = threadIdx.x, l = t & (kRowLanes - 1);
+  if (static_cast<int>(blockIdx.x) >= kv_wgs) {
+    const int hgroups = (p.hq + kQRows - 1) / kQRows;
+    const int64_t grp = (static_cast<int64_t>(blockIdx.x) - kv_wgs) * 32 + (t >> 3);  // (b, i, head group)
+    if (grp >= static_cast<int64_t>(p.batch) * p.tokens * hgroups) return;
+    const int h0 = static_cast<int>(grp % hgroups) * kQRows;
+    const int64_t tok = grp / hgroups;
+    const int i = static_cast<int>(tok % p.tokens), b = static_cast<int>(tok / p.tokens);
+    uint4 xa[kQRows], xb[kQRows], ca, cb, sa, sb;
+    const uint16_t* qrow = p.q + b * p.q_sb + i * p.q_st + static_cast<int64_t>(h0) * kHeadDim;
+#pragma unroll
+    for (int r = 0; r < kQRows; ++r)
+      if (h0 + r < p.hq) load_row_nt(qrow + r * kHeadDim, l, xa[r], xb[r]);
+    load_row(p.cos + b * p.cs_sb + i * p.cs_st, l, ca, cb);
+    load_row(p.sin + b * p.cs_sb + i * p.cs_st, l, sa, sb);
+    uint16_t* dst = p.q_out + b * p.qo_sb + i * p.qo_st + static_cast<int64_t>(h0) * kHeadDim;
+#pragma unroll
+    for (int r = 0; r < kQRows; ++r) {
+      if (h0 + r >= p.hq) break;
+      rope_norm_row(xa[r], xb[r], ca, cb, sa, sb, p.qw, l, p.eps);
+      store_nt(dst + r * kHeadDim + 8 * l, xa[r]);
+      store_nt(dst + r * kHeadDim + 64 + 8 * l, xb[r]);
+    }
+    return;
+  }
+  const int kv = static_cast<int>(blockIdx.x);
+  const int jr = kv % kv_blocks, g = (kv / kv_blocks) % p.hkv, b = kv / (kv_blocks * p.hkv);
+  const int p0 = p.pos ? p.pos[b] : p.pos_c;
+  if (p0 < 0) return;  // (uniform over the workgroup)
+  const int blk = (p0 >> 5) + jr;             // positions [32 blk, 32 blk + 32)
+  const int w = t >> 3;                       // this thread's token of the block
+  const int i = blk * kBlockTokens + w - p0;  // its index in the call
+  const bool valid = i >= 0 && i < p.tokens;
+  const int rslot = p.r_tab ? 0 : (p.ring_slot ? p.ring_slot[b] : b);
+  const bool ring_ok = rslot >= 0 && rslot < p.ring_slots;
+  const int dslot = p.d_tab ? 0 : (p.deep_slot ? p.deep_slot[b] : b);
+  const bool deep_ok = p.dk != nullptr && dslot >= 0 && dslot < p.deep_slots && blk * kBlockTokens < p.deep_cap;
+  const int rblk = ((blk * kBlockTokens) % p.ring_tokens) >> 5;
+  const int64_t roff = ring_ok ? rslot * p.r_ss + g * p.r_hs + write_block(p.r_tab, p.r_tab_stride, p.r_page, p.r_npages, b, rblk) : 0;
+  const int64_t doff = deep_ok ? dslot * p.d_ss + g * p.d_hs + write_block(p.d_tab, p.d_tab_stride, p.d_page, p.d_npages, b, blk) : 0;
+  if (valid) {
+    uint4 ka, kb, ca, cb, sa, sb, va, vb;
+    load_row_nt(p.k + b * p.k_sb + i * p.k_st + static_cast<int64_t>(g) * kHeadDim, l, ka, kb);
+    load_row_nt(p.v + b * p.v_sb + i * p.v_st + static_cast<int64_t>(g) * kHeadDim, l, va, vb);
+    load_row(p.cos + b * p.cs_sb + i * p.cs_st, l, ca, cb);
+    load_row(p.sin + b * p.cs_sb + i * p.cs_st, l, sa, sb);
+    rope_norm_row(ka, kb, ca, cb, sa, sb, p.kw, l, p.eps);
+    // dims [8l, 8l + 8) and [64 + 8l, 64 + 8l + 8) of token w are 16 contiguous bytes each in a K tile
+    const int ko0 = k_tile_offset(w, 8 * l), ko1 = k_tile_offset(w, 64 + 8 * l);
+    if (ring_ok) {
+      store_nt(p.rk + roff + ko0, ka);
+      store_nt(p.rk + roff + ko1, kb);
+    }
+    if (deep_ok) {
+      store_nt(p.dk + doff + ko0, ka);
+      store_nt(p.dk + doff + ko1, kb);
+    }
+    const uint16_t* ea = reinterpret_cast<const uint16_t*>(&va);
+    const uint16_t* eb = reinterpret_cast<const uint16_t*>(&vb);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sv[(8 * l + e) * kVStride + w] = ea[e];
+      sv[(64 + 8 * l + e) * kVStride + w] = eb[e];
+    }
+  }
+  __syncthreads();
+  // V tile: element (token w, dim d) at d * 32 + w; 512 runs of 8 tokens of one dim
+  const int lo = max(0, p0 - blk * kBlockTokens), hi = min(kBlockTokens, p0 + p.tokens - blk * kBlockTokens);
+#pragma unroll
+  for (int run = t; run < kHeadDim * 4; run += 256) {
+    const int d = run >> 2, w0 = 8 * (run & 3);
+    if (w0 + 8 <= lo || w0 >= hi) continue;
+    const uint4 x = *reinterpret_cast<const uint4*>(sv + d * kVStride + w0);
+    if (w0 >= lo && w0 + 8 <= hi) {
+      if (ring_ok) store_nt(p.rv + roff + d * kBlockTokens + w0, x);
+      if (deep_ok) store_nt(p.dv + doff + d * kBlockTokens + w0, x);
+    } else {  // a block edge of the call: only its own tokens
+      const uint16_t* e = reinterpret_cast<const uint16_t*>(&x);
+      for (int j = max(lo - w0, 0); j < min(hi - w0, 8); ++j) {
+        if (ring_ok) p.rv[roff + d * kBlockTokens + w0 + j] = e[j];
+        if (deep_ok) p.dv[doff + d * kBlockTokens + w0 + j] = e[j];
+      }
     }
   }
 }
@@ -275,8 +436,36 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
   p.d_tab_stride = a->deep_table_stride;
   p.d_page = a->deep_page_stride;
   p.d_npages = a->deep_num_pages;
-  const int blocks = static_cast<int>((items + 3) / 4);
-  qkv_epilogue_kernel<<<blocks, 256, 0, as_stream(stream)>>>(p);
+  // Calls of many tokens with 16-byte-aligned rows take the block form (16-byte accesses, V tiles
+  // written through LDS), provided the call's 32-position blocks do not wrap onto each other in the
+  // ring; decode-sized calls keep one wave per (token, head).
+  auto aligned = [](const void* ptr, int64_t s0, int64_t s1) {
+    return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0 && s0 % 8 == 0 && s1 % 8 == 0;
+  };
+  // 32-position blocks one sequence's tokens span (exact for host-constant positions)
+  const int64_t kv_blocks = a->positions != nullptr
+                                ? (a->tokens + kBlockTokens - 1) / kBlockTokens + 1
+                                : (a->position_const + a->tokens - 1) / kBlockTokens - a->position_const / kBlockTokens + 1;
+  const bool block_form = a->tokens >= 16 && kv_blocks <= a->ring_tokens / kBlockTokens &&
+                          aligned(a->q, a->q_stride_b, a->q_stride_t) && aligned(a->k, a->k_stride_b, a->k_stride_t) &&
+                          aligned(a->v, a->v_stride_b, a->v_stride_t) && aligned(a->cos, a->cs_stride_b, a->cs_stride_t) &&
+                          aligned(a->sin, a->cs_stride_b, a->cs_stride_t) &&
+                          aligned(a->q_out, a->q_out_stride_b, a->q_out_stride_t) && aligned(a->q_norm_w, 0, 0) &&
+                          aligned(a->k_norm_w, 0, 0) && aligned(a->ring_k, a->ring_seq_stride, a->ring_head_stride) &&
+                          aligned(a->ring_v, a->ring_page_stride, 0) &&
+                          aligned(a->deep_k, a->deep_seq_stride, a->deep_head_stride) &&
+                          aligned(a->deep_v, a->deep_page_stride, 0);
+  if (block_form) {
+    const int64_t q_groups = static_cast<int64_t>(a->batch) * a->tokens * ((a->num_q_heads + kQRows - 1) / kQRows);
+    const int64_t kv_wgs = static_cast<int64_t>(a->batch) * a->num_kv_heads * kv_blocks;
+    const int64_t wgs = kv_wgs + (q_groups + 31) / 32;
+    LKV_REQUIRE(wgs < (1LL << 31), "too many tokens in one call");
+    qkv_block_kernel<<<static_cast<unsigned>(wgs), 256, 0, as_stream(stream)>>>(p, static_cast<int32_t>(kv_wgs),
+                                                                              static_cast<int32_t>(kv_blocks));
+  } else {
+    const int blocks = static_cast<int>((items + 3) / 4);
+    qkv_epilogue_kernel<<<blocks, 256, 0, as_stream(stream)>>>(p);
+  }
   return check_launch("lkv_qkv_epilogue");
 }
 

@@ -233,10 +233,15 @@ def _ulp_stats(actual: np.ndarray, expected: np.ndarray):
     return mism / diff.size, int(np.max(np.abs(diff >> 16))) if mism else 0
 
 
-@pytest.mark.parametrize("B,L,p0,last", [(2, 1, 37, False), (3, 17, 100, True), (1, 64, 0, True)])
-def test_qkv_epilogue_matches_reference_ops(B, L, p0, last):
+@pytest.mark.parametrize("B,L,p0,last,C", [(2, 1, 37, False, 32), (3, 17, 100, True, 32), (1, 64, 0, True, 32),
+                                          (2, 300, 1000, True, 1024), (2, 200, 1950, True, 1024), (1, 1024, 3072, False, 1024)])
+def test_qkv_epilogue_matches_reference_ops(B, L, p0, last, C):
+    """Decode-sized calls take one wave per (token, head); calls of 16 tokens or more the block form
+    (16-byte accesses, V tiles through LDS), here with partial blocks at both ends of the call and a
+    ring that wraps inside it (positions 1950-2149 in a 2048-token ring)."""
+
     rng = np.random.default_rng(B * 100 + L)
-    Hq, Hkv, C = 8, 2, 32
+    Hq, Hkv = 8, 2
     q = _bf(rng, (B, L, Hq * 128))
     k = _bf(rng, (B, L, Hkv * 128))
     v = _bf(rng, (B, L, Hkv * 128))
@@ -247,7 +252,7 @@ def test_qkv_epilogue_matches_reference_ops(B, L, p0, last):
     qw = torch.linspace(0.7, 1.3, 128).bfloat16()
     kw = torch.linspace(1.2, 0.8, 128).bfloat16()
     ring = ops.TiledKV.zeros(B, Hkv, ops.ring_tokens_for_chunk(C), DEV)
-    deep = ops.TiledKV.zeros(B, Hkv, 256, DEV) if last else None
+    deep = ops.TiledKV.zeros(B, Hkv, -(-(p0 + L) // 32) * 32, DEV) if last else None
     q_out = ops.qkv_epilogue(_t(q), _t(k), _t(v), cos.to(DEV), sin.to(DEV), num_q_heads=Hq, num_kv_heads=Hkv,
                              q_norm_weight=qw.to(DEV), k_norm_weight=kw.to(DEV), eps=1e-5, positions=p0, ring=ring, deep=deep)
     # the reference's ops in bf16 on the CPU (modeling.py:100-106)
