@@ -458,7 +458,7 @@ typedef struct lkv_append_args {
   int64_t v_stride_b;
   int64_t v_stride_t;
   int64_t v_stride_h;
-  void *pool_k; /* [pages, heads, 4096] bf16 */
+  void *pool_k; /* bf16 pool: page p of head h at p * page_stride + h * head_stride (4096 each) */
   void *pool_v;
   int64_t page_stride;
   int64_t head_stride;

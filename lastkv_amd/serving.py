@@ -3,7 +3,7 @@ decode fast path (``vllm/src/lastkv/vllm/backends/rmarin_flashinfer/fastpath.py`
 slab pool (``batching.py:1971-2122``) and the model runner that calls it per layer
 (``vllm_model.py``, ``vllm_backend.py:637-664``).
 
-``LastKVPagePool`` holds every sequence's K/V in 32-token pages of one ``[pages, Hkv, 4096]`` pool
+``LastKVPagePool`` holds every sequence's K/V in 32-token pages of one head-major ``[Hkv, pages, 4096]`` pool
 (K and V): per slot, the shared last-layer pages of its positions (handed out as the sequence
 grows, like vLLM blocks) and, per layer, a fixed ring of ``ring_tokens_for_chunk(C)`` tokens (the
 recent + current chunk, the reference's per-layer ring pages).  ``LastKVFastPath.prepare`` is the
@@ -139,7 +139,7 @@ class PageAllocator:
 
 
 class LastKVPagePool:
-    """One ``[pages, Hkv, 4096]`` K/V pool: shared last-layer pages (handed out per slot on demand)
+    """One head-major ``[Hkv, pages, 4096]`` K/V pool: shared last-layer pages (handed out per slot on demand)
     and per-layer ring pages (fixed per slot), plus one scratch page that padded rows and unused
     table entries name.  Device copies of the page tables sit beside the host bookkeeping."""
 

@@ -157,8 +157,8 @@ class WanKVCache:
         koff = ((((w[:, None] >> 2) & 1) * 4 + (d[None, :] >> 5)) * 16 + (((w[:, None] >> 3) << 2) | (w[:, None] & 3))) * 32 \
             + (d[None, :] & 31)
         voff = d[None, :] * 32 + w[:, None]
-        kp = self.pool.k[pages]  # [B, T, H, 4096]
-        vp = self.pool.v[pages]
+        kp = self.pool.kp[pages]  # [B, T, H, 4096]
+        vp = self.pool.vp[pages]
         idx_k = koff[None, :, None, :].expand(kp.shape[0], -1, kp.shape[2], -1)
         idx_v = voff[None, :, None, :].expand(vp.shape[0], -1, vp.shape[2], -1)
         return kp.gather(3, idx_k), vp.gather(3, idx_v)

@@ -26,8 +26,8 @@ def _scatter(cache: ops.TiledKV, pool: ops.PagedKV, pages: torch.Tensor) -> torc
 
     S, H, nb, _ = cache.k.shape
     flat = pages.reshape(-1).long()
-    pool.k[flat] = cache.k.permute(0, 2, 1, 3).reshape(S * nb, H, 4096)
-    pool.v[flat] = cache.v.permute(0, 2, 1, 3).reshape(S * nb, H, 4096)
+    pool.kp[flat] = cache.k.permute(0, 2, 1, 3).reshape(S * nb, H, 4096)
+    pool.vp[flat] = cache.v.permute(0, 2, 1, 3).reshape(S * nb, H, 4096)
     return pages.to(torch.int32).contiguous()
 
 
@@ -113,8 +113,8 @@ def _gather(pool: ops.PagedKV, table: torch.Tensor) -> tuple[torch.Tensor, torch
 
     S, nb = table.shape
     idx = table.reshape(-1).long()
-    k = pool.k[idx].view(S, nb, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
-    v = pool.v[idx].view(S, nb, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
+    k = pool.kp[idx].reshape(S, nb, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
+    v = pool.vp[idx].reshape(S, nb, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
     return k, v
 
 

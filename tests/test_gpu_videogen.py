@@ -39,8 +39,8 @@ def _read(pool: ops.PagedKV, table: torch.Tensor, tokens: int):
 
     B, Wd = table.shape
     idx = table.reshape(-1).long()
-    tk = pool.k[idx].view(B, Wd, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
-    tv = pool.v[idx].view(B, Wd, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
+    tk = pool.kp[idx].reshape(B, Wd, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
+    tv = pool.vp[idx].reshape(B, Wd, pool.heads, 4096).permute(0, 2, 1, 3).contiguous()
     k = ops.cache_unpack(tk, ops.KIND_K, 0, tokens)
     v = ops.cache_unpack(tv, ops.KIND_V, 0, tokens)
     return k.transpose(1, 2), v.transpose(1, 2)
