@@ -16,7 +16,7 @@
 //     four 16-lane rows with VALU lane swaps, O rescaled (a branch taken only when some row's
 //     offset moved) with the factor each lane already holds;
 //   - O^T += V^T * P^T with 16x16x32 fp16 MFMAs, and the row sums as P times a tile of ones on
-//     the same pipe: P in (0, 2) carries 11 mantissa bits (bf16 would carry 8, a 1.7e-3 relative
+//     the same pipe: P in (0, 512) carries 11 mantissa bits (bf16 would carry 8, a 1.7e-3 relative
 //     error the rel-L2 1e-3 bound does not allow); the 2-wave instance adds the fp16 residual of
 //     P (hi + lo, ~22 bits).  bf16 V converts to fp16 exactly for 2^-17 <= |V| <= 65280 and 0;
 //     smaller magnitudes are truncated toward zero (absolute error < 2^-24), larger ones
@@ -154,15 +154,16 @@ __device__ inline float max8(const float (&s)[8]) {
 // Online-softmax state of one 16-row column group: m = the row's score reference (raw scores),
 // mc = m * c, the exp2 offset (0 while m = -inf).
 // Probabilities are P = 2^(s c - mc).  m is the exact row maximum after the first block; later it
-// is raised only when some P reaches 2 (a new maximum more than 1 / c above m), so P < 2 always
-// and fp16 keeps its full 11-bit precision.  O / l does not depend on the offset.
+// is raised only when some P reaches 2^9 (a new maximum more than 9 / c above m), so P < 512
+// always: fp16 keeps its full 11-bit precision (P V and the row sums accumulate in fp32), and
+// later blocks rarely pay for a rescale.  O / l does not depend on the offset.
 struct RowState {
   float m, mc;
 };
 
 // Raises each row's reference to its maximum over this block (lm = lane maxima) and rescales O
 // and the row sums by 2^(mc_old - mc_new).  Runs for the first block and in a wave-uniform branch
-// taken whenever some P reached 2.
+// taken whenever some P reached 2^9.
 __device__ inline void raise_rows(RowState& rs, float lm, float c, f32x4 (&o)[8], f32x4& ol) {
   const float bm = wave_max_across_rows(lm);
   const bool up = bm > rs.m;  // m = -inf: true for the first finite maximum
@@ -198,10 +199,16 @@ __device__ inline void probs_lo(const float (&pr)[8], const uint32_t (&w)[4], ui
   }
 }
 
-// Nonzero when some packed fp16 probability is >= 2 (exponent field >= 16), infinite or NaN.
-__device__ inline uint32_t probs_overflow(const uint32_t (&w)[4]) {
-  return (w[0] | w[1] | w[2] | w[3]) & 0x40004000u;
+// The lane's largest packed fp16 probabilities of a block (one per half, NaN-propagating).
+__device__ inline uint32_t probs_max(uint32_t a, uint32_t b, uint32_t c) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 x = __builtin_elementwise_maximum(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_maximum(x, __builtin_bit_cast(h2, c)));
 }
+
+// A rescale is due when some probability of the block is >= 2^9 (fp16 exponent field >= 24:
+// bits 14 and 13 of a half both set), infinite or NaN; pm = probs_max over the block's words.
+__device__ inline bool probs_overflow(uint32_t pm) { return (pm & (pm << 1) & 0x40004000u) != 0; }
 
 template <int N>
 struct IC {
@@ -408,11 +415,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
           sc[cg][1] = mfma_bf16(kf[4 + kb], qf[cg][kb], sc[cg][1]);
         }
       uint32_t pw[CG][4], pl[CG][4];
+      uint32_t pmax;  // the lane's largest probabilities of this block (packed fp16)
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) {
         float pr[8];
         probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
         if (kSplitP) probs_lo(pr, pw[cg], pl[cg]);
+        pmax = cg == 0 ? probs_max(pw[cg][0], pw[cg][1], probs_max(pw[cg][2], pw[cg][3], pw[cg][3]))
+                       : probs_max(pmax, probs_max(pw[cg][0], pw[cg][1], pw[cg][2]), pw[cg][3]);
       }
       uint4 vf[8];
 #pragma unroll
@@ -429,10 +439,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
         __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);  // exp
       }
       // a new row maximum: exact maxima, rescale, recompute this block's P
-      uint32_t ovf = 0;
-#pragma unroll
-      for (int cg = 0; cg < CG; ++cg) ovf |= probs_overflow(pw[cg]);
-      if (__builtin_amdgcn_ballot_w64(ovf != 0)) {
+      if (__builtin_amdgcn_ballot_w64(probs_overflow(pmax))) {
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
           raise_rows(rs[cg], max8(s[cg]), c, o[cg], ol[cg]);
