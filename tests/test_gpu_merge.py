@@ -87,10 +87,12 @@ def test_merge_vllm_and_flashinfer_orders():
 
 def test_merged_passes_equal_single_pass_over_union():
     """Older segment and local segment attended separately (each with its LSE) and merged, as the
-    reference's two-pass serving path does.  The merge is checked against the oracle merge of the
-    two bf16-rounded partial outputs (standard bar); against one pass over [older | local] the two
-    intermediate bf16 roundings add up to about one bf16 ulp, so that comparison allows rel-L2
-    4e-3 (the same holds for the reference's own two-pass FA3 path)."""
+    reference's two-pass serving path does.  Each partial output is checked against the oracle's
+    partial (standard bar), and the merge against the oracle merge of the same two bf16 partials
+    the kernel merged (standard bar; comparing with the merge of the oracle's partials instead
+    would count each partial's bf16 rounding flips twice).  Against one pass over [older | local]
+    the two intermediate bf16 roundings add up to about one bf16 ulp, so that comparison allows
+    rel-L2 4e-3 (the same holds for the reference's own two-pass FA3 path)."""
 
     rng = np.random.default_rng(23)
     B, L, Hq, Hkv, T0, n_local = 2, 48, 8, 2, 300, 96
@@ -122,8 +124,12 @@ def test_merged_passes_equal_single_pass_over_union():
     pl, pll = A.attention(qt, lk, lv, causal_bottom_right=True)
     np.testing.assert_allclose(lse_o.cpu().numpy(), plo.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
     np.testing.assert_allclose(lse_l.cpu().numpy(), pll.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
-    want_m, _ = A.merge_states(bf16.round_bf16(po.astype(np.float32)), plo, bf16.round_bf16(pl.astype(np.float32)), pll)
-    _close(merged, bf16.round_bf16(want_m.transpose(0, 2, 1, 3).astype(np.float32)), "merged vs oracle merge of bf16 partials")
+    _close(out_o, bf16.round_bf16(po.transpose(0, 2, 1, 3).astype(np.float32)), "older partial vs oracle")
+    _close(out_l, bf16.round_bf16(pl.transpose(0, 2, 1, 3).astype(np.float32)), "local partial vs oracle")
+    go = out_o.float().cpu().numpy().transpose(0, 2, 1, 3)
+    gl = out_l.float().cpu().numpy().transpose(0, 2, 1, 3)
+    want_m, _ = A.merge_states(go, lse_o.cpu().numpy().transpose(0, 2, 1), gl, lse_l.cpu().numpy().transpose(0, 2, 1))
+    _close(merged, bf16.round_bf16(want_m.transpose(0, 2, 1, 3).astype(np.float32)), "merged vs oracle merge of the same partials")
     want, _ = A.attention(qt, np.concatenate([ok, lk], 2), np.concatenate([sv, lv], 2), causal_bottom_right=True)
     want = bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32))
     _close(single, want, "single pass vs oracle")
