@@ -72,7 +72,8 @@ def parse_args():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 4 (128K decode), config 5 (Wan) and config 3 (8B end to end) measurements")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy decode steps of the config 3 model run")
-    ap.add_argument("--only", choices=["prefill", "short", "config4", "config4p", "config5", "config3"], default=None,
+    ap.add_argument("--only", choices=["prefill", "short", "config4", "config4p", "config5", "config3", "epilogue"],
+                    default=None,
                     help="run one secondary measurement alone and print its JSON (for profiling); "
                          "this is not the bench line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -233,6 +234,57 @@ def short_prefill_measurement(ops, torch, cache, dev, reps: int = 20) -> dict:
         res[key] = {"us_per_call": round(us, 2), "kv_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
                     "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     return res
+
+
+def epilogue_measurement(ops, torch, dev, reps: int = 20) -> dict:
+    """lkv_qkv_epilogue at config 3's prefill call shape: B=32 x 2048 new tokens (65536 tokens),
+    32 query + 8 kv heads: RoPE and q/k RMSNorm of q and k, q written back, k and v appended to the
+    layer's tiled ring (bf16).  Algorithmic bytes: q/k/v read once, q written once, k/v written once,
+    the cos/sin rows read once; compared with a device copy of the same number of bytes."""
+
+    B, L = 32, 2048
+    g = torch.Generator(device=dev).manual_seed(8)
+    q = torch.randn((B, L, HQ * D), generator=g, device=dev).bfloat16()
+    k = torch.randn((B, L, HKV * D), generator=g, device=dev).bfloat16()
+    v = torch.randn((B, L, HKV * D), generator=g, device=dev).bfloat16()
+    cos = torch.rand((B, L, D), generator=g, device=dev).bfloat16()
+    sin = torch.rand((B, L, D), generator=g, device=dev).bfloat16()
+    w = (torch.rand(D, generator=g, device=dev) + 0.5).bfloat16()
+    ring = ops.TiledKV.zeros(B, HKV, ops.ring_tokens_for_chunk(CHUNK), dev)
+    q_out = torch.empty((B, L, HQ, D), dtype=torch.bfloat16, device=dev)
+    kw = dict(num_q_heads=HQ, num_kv_heads=HKV, q_norm_weight=w, k_norm_weight=w, eps=1e-5, positions=0, ring=ring,
+              q_out=q_out)
+    for _ in range(3):
+        ops.qkv_epilogue(q, k, v, cos, sin, **kw)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ops.qkv_epilogue(q, k, v, cos, sin, **kw)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    T = B * L
+    nbytes = T * (HQ + 2 * HKV) * D * 2 + T * HQ * D * 2 + T * 2 * HKV * D * 2 + T * 2 * D * 2
+    src = torch.empty(nbytes // 4, dtype=torch.bfloat16, device=dev)  # half read, half written
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_us = e0.elapsed_time(e1) * 1e3 / reps
+    del src, dst
+    return {
+        "workload": "lkv_qkv_epilogue, config 3 prefill call: B=32 x 2048 tokens, 32 q + 8 kv heads, tiled ring append",
+        "bytes_per_call": nbytes, "us_per_call": round(us, 1), "gbps": round(nbytes / us / 1e3, 1),
+        "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+        "same_bytes_device_copy_us": round(copy_us, 1), "copy_gbps": round(nbytes / copy_us / 1e3, 1),
+        "frac_of_copy": round(copy_us / us, 4),
+    }
 
 
 def wan_measurement(ops, torch, dev) -> dict:
@@ -574,6 +626,8 @@ def main() -> int:
             res = prefill_long_measurement(ops, torch, dev)
         elif args.only == "config5":
             res = wan_measurement(ops, torch, dev)
+        elif args.only == "epilogue":
+            res = epilogue_measurement(ops, torch, dev)
         else:
             res = e2e_8b_measurement(torch, dev, args.decode_steps)
         print(json.dumps({"only": args.only, **res}), flush=True)
