@@ -152,10 +152,13 @@ __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, con
 template <bool kVScale, bool kNT, bool kMulti, int CG = 1, bool kPairs = false>
 __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p) {
   constexpr int kCols = (kPairs ? 32 : 16) * CG;
+  constexpr int kWaveCols = 16 * CG;  // columns one wave holds (a pair's share with kPairs)
   constexpr int kStride = kPairs ? 2 : kWaves;  // block stride of one wave
-  __shared__ float sm_m[kWaves][kCols];
-  __shared__ float sm_l[kWaves][kCols];
-  __shared__ float sm_o[kWaves][kCols][kHeadDim];
+  // indexed by the column inside the wave's own range: with kPairs each wave pair stages only its
+  // half of the columns, so the staging takes 64 KiB at most and two workgroups fit on a CU
+  __shared__ float sm_m[kWaves][kWaveCols];
+  __shared__ float sm_l[kWaves][kWaveCols];
+  __shared__ float sm_o[kWaves][kWaveCols][kHeadDim];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -236,15 +239,15 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
     if (g4 == 0 && 16 * (cg0 + cg) + n16 < cols) {
-      sm_m[wave][16 * (cg0 + cg) + n16] = st[cg].m;
-      sm_l[wave][16 * (cg0 + cg) + n16] = st[cg].l;
+      sm_m[wave][16 * cg + n16] = st[cg].m;
+      sm_l[wave][16 * cg + n16] = st[cg].l;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int h = 16 * (cg0 + cg) + 4 * g4 + i;
-      if (h < cols) {
+      const int hl = 16 * cg + 4 * g4 + i;  // column 16 * cg0 + hl
+      if (16 * cg0 + hl < cols) {
 #pragma unroll
-        for (int nb = 0; nb < 8; ++nb) sm_o[wave][h][16 * nb + n16] = st[cg].o[nb][i];
+        for (int nb = 0; nb < 8; ++nb) sm_o[wave][hl][16 * nb + n16] = st[cg].o[nb][i];
       }
     }
   }
@@ -254,17 +257,18 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     const int tq = kMulti ? h / G : 0, hh = h - tq * G;
     const int64_t row_q = (static_cast<int64_t>(b) * (kMulti ? p.L : 1) + tq) * p.hq + kvh * G + hh;  // [B, L, Hq] row
     // the waves that hold column h: all four, or the pair of its column group
-    const int w0 = kPairs ? 2 * (h / (16 * CG)) : 0;
+    const int pair = kPairs ? h / kWaveCols : 0;
+    const int w0 = 2 * pair, hl = h - pair * kWaveCols;  // its waves and its column inside their range
     constexpr int kMergeWaves = kPairs ? 2 : kWaves;
-    float M = sm_m[w0][h];
+    float M = sm_m[w0][hl];
 #pragma unroll
-    for (int w = w0 + 1; w < w0 + kMergeWaves; ++w) M = fmaxf(M, sm_m[w][h]);
+    for (int w = w0 + 1; w < w0 + kMergeWaves; ++w) M = fmaxf(M, sm_m[w][hl]);
     float L = 0.f, O = 0.f;
 #pragma unroll
     for (int w = w0; w < w0 + kMergeWaves; ++w) {
-      const float f = sm_m[w][h] == kNegInf ? 0.f : fast_exp2(sm_m[w][h] - M);
-      L += f * sm_l[w][h];
-      O += f * sm_o[w][h][d];
+      const float f = sm_m[w][hl] == kNegInf ? 0.f : fast_exp2(sm_m[w][hl] - M);
+      L += f * sm_l[w][hl];
+      O += f * sm_o[w][hl][d];
     }
     if (p.splits == 1) {
       p.out[b * p.out_sb + (kMulti ? tq * p.out_st : 0) + static_cast<int64_t>(kvh * G + hh) * kHeadDim + d] =
