@@ -360,6 +360,42 @@ def test_silu_mul_bit_exact():
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_prefill_lazy_rescale_threshold_regimes(causal):
+    """The tile kernel keeps block 0's exact row maximum and rescales only when a later
+    probability reaches 2^9.  Rows here see near-zero scores in block 0 and one later key (older
+    block 2) whose exp2 argument jumps by d: d from 0.5 to 80 across the rows, so some rows keep the
+    old reference with probabilities up to 2^8.99 in fp16, some sit just past the threshold and
+    rescale once, some jump far beyond it.  A second key (local block 1) jumps further still on
+    half the rows (a second rescale).  Tile kernel (automatic / 4 / 8 waves) against the fp64
+    oracle; causal runs put the second key inside every row's visible range."""
+
+    rng = np.random.default_rng(91)
+    B, Hkv, G, L, T0, n_local = 1, 2, 4, 64, 96, 128
+    Hq = G * Hkv
+    c = 128 ** -0.5 * 1.4426950408889634  # exp2 argument per unit of raw score
+    jumps = np.array([0.5, 2.0, 5.0, 8.5, 8.95, 9.05, 9.5, 12.0, 20.0, 40.0, 80.0, 1.0, 8.8, 9.2, 30.0, 0.0])
+    a = (jumps / (128 * c)).astype(np.float32)  # q = a * ones: the special key (k = ones) scores 128 a
+    rows = (np.arange(L)[:, None] * Hq + np.arange(Hq)[None, :]) % len(jumps)
+    q = a[rows][None, :, :, None] * np.ones((1, 1, 1, 128), np.float32)
+    q = bf16.round_bf16((q + 0.002 * rng.standard_normal((B, L, Hq, 128))).astype(np.float32))
+    keys = T0 + n_local
+    k = bf16.round_bf16((0.05 * rng.standard_normal((B, Hkv, keys, 128))).astype(np.float32))
+    k[:, :, 70] = 1.0  # older block 2
+    k[:, :, T0 + 40, :] = bf16.round_bf16(np.where(np.arange(128) < 64, 1.5, 1.0).astype(np.float32))  # local block 1
+    v = _bf(rng, (B, Hkv, keys, 128))
+    older = ops.TiledKV.zeros(B, Hkv, 128, DEV)
+    ops.pack_kv(_t(k[:, :, :T0]), _t(v[:, :, :T0]), older)
+    ring = ops.TiledKV.zeros(B, Hkv, n_local, DEV)
+    ops.pack_kv(_t(k[:, :, T0:]), _t(v[:, :, T0:]), ring)
+    kw = dict(older=older, older_len=T0, local=ring, local_len=n_local, causal=causal)
+    want, _ = A.attention(q.transpose(0, 2, 1, 3), k, v, causal_bottom_right=causal)
+    want = bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32))
+    for tw in (0, 4, 8):
+        out = ops.prefill_attention(_t(q), tile_waves=tw, **kw)
+        _close(out, want, f"rescale regimes causal={causal} tile_waves={tw}")
+
+
 @pytest.mark.parametrize("L,G", [(160, 4), (12, 4)])
 def test_prefill_extreme_score_ranges(L, G):
     """Regression: rows whose first visible scores are all far below zero (scaled scores near -180,
