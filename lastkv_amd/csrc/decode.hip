@@ -24,6 +24,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr float kNegInf = -__builtin_inff();
+constexpr float kLazyRaise = 8.f;  // exp2 units a block maximum may exceed m before m is raised
 
 struct DecodeParams {
   const uint16_t* q;
@@ -94,28 +95,34 @@ __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, con
 #pragma unroll
   for (int j = 1; j < 8; ++j) mx = fmaxf(mx, s[j]);
   mx = wave_max_across_rows(mx);
-  const float m_new = fmaxf(st.m, mx);
+  // Lazy reference: a column's m moves (and O and l are rescaled) only in a wave-uniform branch
+  // taken when some column's block maximum exceeds its m by more than kLazyRaise (exp2 units), the
+  // first block with a visible key included (m = -inf).  Otherwise P = 2^(s - m) stays below
+  // 2^kLazyRaise; its bf16 hi + lo split keeps ~16 bits at any magnitude and O, l are fp32.
   float alpha = 1.f;
+  if (__builtin_amdgcn_ballot_w64(mx > st.m + kLazyRaise)) {
+    const float m_new = fmaxf(st.m, mx);
+    alpha = m_new == kNegInf ? 1.f : fast_exp2(st.m - m_new);
+    st.m = m_new;
+    // rows of this lane's O accumulators are heads 4*g4 + i; their factors live in lanes 4*g4 + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = __shfl(alpha, 4 * g4 + i);
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) st.o[nb][i] *= a;
+    }
+  }
   float p[8];
-  if (m_new == kNegInf) {
+  if (st.m == kNegInf) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) p[j] = 0.f;
   } else {
-    alpha = fast_exp2(st.m - m_new);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) p[j] = fast_exp2(s[j] - m_new);
+    for (int j = 0; j < 8; ++j) p[j] = fast_exp2(s[j] - st.m);
   }
   float rs = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
   rs = wave_sum_across_rows(rs);
   st.l = st.l * alpha + rs;
-  st.m = m_new;
-  // rows of this lane's O accumulators are heads 4*g4 + i; their factors live in lanes 4*g4 + i
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float a = __shfl(alpha, 4 * g4 + i);
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) st.o[nb][i] *= a;
-  }
   uint4 phi, plo;
   float hi[8];
   phi.x = pack_bf16x2(p[0], p[1]);
