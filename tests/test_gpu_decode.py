@@ -212,6 +212,43 @@ def test_config2_split_invariance_and_power_of_two_vscale_linearity(config2):
         assert torch.equal(ops.decode_attention(q, older=cache, older_len=8192, num_splits=1, kv_cache_hint=hint), base)
 
 
+@pytest.mark.parametrize("tokens", [1, 4, 40])
+@pytest.mark.parametrize("bf16_scale", [True, False])
+def test_older_vscale_equals_prescaled_cache_bitwise(tokens, bf16_scale):
+    """The older segment's V scale gives the same bits as a cache whose V holds bf16(V * s)
+    (torch: fp32 product, one round to bf16), for bf16-valued and other fp32 scales; 1 and 4
+    tokens run the decode kernel, 40 tokens the tile kernel's V pre-pass.  The local segment
+    stays unscaled."""
+
+    rng = np.random.default_rng(11 + tokens)
+    B, Hq, Hkv, T0, n1 = 3, 16, 4, 1000, 77
+    ok, ov = _bf(rng, (B, Hkv, T0, 128)), _bf(rng, (B, Hkv, T0, 128), 3.0)
+    lk, lv = _bf(rng, (B, Hkv, n1, 128)), _bf(rng, (B, Hkv, n1, 128))
+    s = rng.uniform(0.3, 1.7, Hkv).astype(np.float32)
+    s[0] = 1.0
+    if bf16_scale:
+        s = bf16.round_bf16(s)
+    else:
+        s[1:] = np.where(bf16.round_bf16(s[1:]) == s[1:], s[1:] * (1 + 2.0 ** -12), s[1:])
+        assert not np.any(bf16.round_bf16(s[1:]) == s[1:])
+    older = ops.TiledKV.zeros(B, Hkv, 1024, DEV)
+    ops.pack_kv(_t(ok), _t(ov), older)
+    vs = torch.from_numpy(s).to(DEV)
+    pre = ops.TiledKV(older.k.clone(), (older.v.float() * vs.view(1, Hkv, 1, 1)).bfloat16())
+    ring = ops.TiledKV.zeros(B, Hkv, 128, DEV)
+    ops.pack_kv(_t(lk), _t(lv), ring)
+    seg = dict(older_len=T0, local=ring, local_len=n1)
+    if tokens == 1:
+        q = _t(_bf(rng, (B, Hq, 128)))
+        got = ops.decode_attention(q, older=older, vscale=vs, num_splits=2, **seg)
+        want = ops.decode_attention(q, older=pre, num_splits=2, **seg)
+    else:
+        q = _t(_bf(rng, (B, tokens, Hq, 128)))
+        got = ops.prefill_attention(q, older=older, vscale=vs, causal=True, **seg)
+        want = ops.prefill_attention(q, older=pre, causal=True, **seg)
+    assert torch.equal(got, want)
+
+
 def _two_segments(rng, B, Hkv, T0, n1, start, ring_blocks):
     """Older segment of T0 tokens and a ring of ring_blocks blocks holding n1 tokens from ring token
     `start` (wrapping), with a bf16 older V scale; returns the caches and the composed fp32 K/V the
