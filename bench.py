@@ -240,7 +240,9 @@ def epilogue_measurement(ops, torch, dev, reps: int = 20) -> dict:
     """lkv_qkv_epilogue at config 3's prefill call shape: B=32 x 2048 new tokens (65536 tokens),
     32 query + 8 kv heads: RoPE and q/k RMSNorm of q and k, q written back, k and v appended to the
     layer's tiled ring (bf16).  Algorithmic bytes: q/k/v read once, q written once, k/v written once,
-    the cos/sin rows read once; compared with a device copy of the same number of bytes."""
+    the cos/sin rows read once; compared with a device copy of the same number of bytes.  Timed with
+    q, k, v as separate tensors (the HF module's three projections) and as row views of one fused
+    projection output (the serving path's layout)."""
 
     B, L = 32, 2048
     g = torch.Generator(device=dev).manual_seed(8)
@@ -264,6 +266,19 @@ def epilogue_measurement(ops, torch, dev, reps: int = 20) -> dict:
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / reps
+    # the serving path's layout: q, k and v are row views of one fused projection output
+    qkv = torch.cat((q, k, v), dim=-1)
+    fq, fk, fv = qkv.split([HQ * D, HKV * D, HKV * D], dim=-1)
+    for _ in range(3):
+        ops.qkv_epilogue(fq, fk, fv, cos, sin, **kw)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        ops.qkv_epilogue(fq, fk, fv, cos, sin, **kw)
+    e1.record()
+    torch.cuda.synchronize()
+    us_fused = e0.elapsed_time(e1) * 1e3 / reps
+    del qkv, fq, fk, fv
     T = B * L
     nbytes = T * (HQ + 2 * HKV) * D * 2 + T * HQ * D * 2 + T * 2 * HKV * D * 2 + T * 2 * D * 2
     src = torch.empty(nbytes // 4, dtype=torch.bfloat16, device=dev)  # half read, half written
@@ -282,6 +297,8 @@ def epilogue_measurement(ops, torch, dev, reps: int = 20) -> dict:
         "workload": "lkv_qkv_epilogue, config 3 prefill call: B=32 x 2048 tokens, 32 q + 8 kv heads, tiled ring append",
         "bytes_per_call": nbytes, "us_per_call": round(us, 1), "gbps": round(nbytes / us / 1e3, 1),
         "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+        "fused_projection_us_per_call": round(us_fused, 1),
+        "fused_projection_hbm_frac": round(nbytes / us_fused / 1e3 / HBM_PEAK_GBS, 4),
         "same_bytes_device_copy_us": round(copy_us, 1), "copy_gbps": round(nbytes / copy_us / 1e3, 1),
         "frac_of_copy": round(copy_us / us, 4),
     }

@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
 // exchange and RMSNorm's sum three xor shuffles.  The first workgroups take one (sequence,
 // 32-position block, kv head) each: K goes to its tile row by row (64-byte runs), V is transposed
 // through LDS and written to its tile (d-major) with 16-byte stores, both to the ring block and, on
-// the final layer, to the shared-store block.  The others take query rows, four heads of one token
+// the final layer, to the shared-store block.  The others take query rows, two heads of one token
 // per 8-lane group.
 constexpr int kRowLanes = 8;
 constexpr int kVStride = 40;  // LDS row of one V dim: 32 tokens + 8 pad elements (80 bytes, 16-byte aligned)
@@ -145,17 +145,60 @@ __device__ inline uint4 pack8(const float (&x)[8]) {
   return make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
 }
 
-// RoPE then RMSNorm of the row held by an 8-lane group (lane l: dims 8l.. in a / 64 + 8l.. in b).
-__device__ inline void rope_norm_row(uint4& a, uint4& b, uint4 ca, uint4 cb, uint4 sa, uint4 sb, const uint16_t* w,
-                                     int l, float eps) {
-  float x0[8], x1[8], c0[8], c1[8], s0[8], s1[8], r0[8], r1[8];
-  unpack8(a, x0), unpack8(b, x1), unpack8(ca, c0), unpack8(cb, c1), unpack8(sa, s0), unpack8(sb, s1);
+// The norm weights of lane l's dims as floats (loaded once per thread, ahead of its row loads: a
+// load issued after them would make each row's s_waitcnt wait for every row load in flight).
+struct NormW {
+  float w0[8], w1[8];
+  bool on;
+};
+
+__device__ inline NormW norm_weights(const uint16_t* w, int l) {
+  NormW r;
+  r.on = w != nullptr;
+  uint4 a = make_uint4(0, 0, 0, 0), b = a;
+  if (w != nullptr) {
+    a = *reinterpret_cast<const uint4*>(w + 8 * l);
+    b = *reinterpret_cast<const uint4*>(w + 64 + 8 * l);
+  }
+  unpack8(a, r.w0);
+  unpack8(b, r.w1);
+  return r;
+}
+
+// One token's cos / sin values of lane l's dims, shared by every head of the token.
+struct RopeCS {
+  float c0[8], c1[8], s0[8], s1[8];
+};
+
+__device__ inline RopeCS rope_cs(uint4 ca, uint4 cb, uint4 sa, uint4 sb) {
+  RopeCS r;
+  unpack8(ca, r.c0), unpack8(cb, r.c1), unpack8(sa, r.s0), unpack8(sb, r.s1);
+  return r;
+}
+
+// Rounds a and b to bf16 with one v_cvt_pk_bf16_f32 (round to nearest even, as rb).
+__device__ inline void rb2(float& a, float& b) {
+  const uint32_t u = pack_bf16x2(a, b);
+  a = bf16_lo(u);
+  b = bf16_hi(u);
+}
+
+// RoPE then RMSNorm of the row held by an 8-lane group (lane l: dims 8l.. in a / 64 + 8l.. in b),
+// every bf16 operation of the reference rounded in the same order (two roundings per
+// v_cvt_pk_bf16_f32; the last one is the packing of the output).
+__device__ inline void rope_norm_row(uint4& a, uint4& b, const RopeCS& cs, const NormW& w, float eps) {
+  float x0[8], x1[8], r0[8], r1[8];
+  unpack8(a, x0), unpack8(b, x1);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    r0[j] = rb(rb(x0[j] * c0[j]) + rb(-x1[j] * s0[j]));
-    r1[j] = rb(rb(x1[j] * c1[j]) + rb(x0[j] * s1[j]));
+    float p0 = x0[j] * cs.c0[j], p1 = -x1[j] * cs.s0[j], p2 = x1[j] * cs.c1[j], p3 = x0[j] * cs.s1[j];
+    rb2(p0, p1);
+    rb2(p2, p3);
+    r0[j] = p0 + p1;
+    r1[j] = p2 + p3;
+    rb2(r0[j], r1[j]);
   }
-  if (w != nullptr) {
+  if (w.on) {
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss += r0[j] * r0[j] + r1[j] * r1[j];
@@ -163,13 +206,12 @@ __device__ inline void rope_norm_row(uint4& a, uint4& b, uint4 ca, uint4 cb, uin
     ss += __shfl_xor(ss, 2);
     ss += __shfl_xor(ss, 4);
     const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHeadDim) + eps);
-    float w0[8], w1[8];
-    unpack8(*reinterpret_cast<const uint4*>(w + 8 * l), w0);
-    unpack8(*reinterpret_cast<const uint4*>(w + 64 + 8 * l), w1);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      r0[j] = rb(w0[j] * rb(r0[j] * inv));
-      r1[j] = rb(w1[j] * rb(r1[j] * inv));
+      float u0 = r0[j] * inv, u1 = r1[j] * inv;
+      rb2(u0, u1);
+      r0[j] = w.w0[j] * u0;  // rounded by the packing below
+      r1[j] = w.w1[j] * u1;
     }
   }
   a = pack8(r0);
@@ -192,7 +234,47 @@ __device__ inline void store_nt(uint16_t* dst, uint4 v) {
   __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
 }
 
-constexpr int kQRows = 4;  // query heads of one token per 8-lane group (one cos / sin load for all)
+// query heads of one token per 8-lane group (one cos / sin load for all; measured at config 3's
+// prefill call shape: 2 heads 310 us, 4 heads 313 us, 8 heads 335 us per call)
+constexpr int kQRows = 2;
+
+// The query rows of one 8-lane group: kQRows heads of one token and the token's cos / sin rows.
+struct QItem {
+  uint4 xa[kQRows], xb[kQRows], ca, cb, sa, sb;
+};
+
+// grp = (b, i, head group).  The loads are unconditional (a group past the end rereads the last
+// one, heads past Hq the last head) so that the compiler can count them for s_waitcnt and the next
+// group's loads stay in flight while this one is computed.
+__device__ inline void q_item_load(const QkvParams& p, int32_t grp, int32_t groups, int hgroups, int l, QItem& it) {
+  grp = grp < groups ? grp : groups - 1;
+  const int h0 = grp % hgroups * kQRows;
+  const int tok = grp / hgroups;
+  const int i = tok % p.tokens, b = tok / p.tokens;
+  const uint16_t* qrow = p.q + b * p.q_sb + i * p.q_st;
+#pragma unroll
+  for (int r = 0; r < kQRows; ++r)
+    load_row_nt(qrow + static_cast<int64_t>(min(h0 + r, p.hq - 1)) * kHeadDim, l, it.xa[r], it.xb[r]);
+  load_row(p.cos + b * p.cs_sb + i * p.cs_st, l, it.ca, it.cb);
+  load_row(p.sin + b * p.cs_sb + i * p.cs_st, l, it.sa, it.sb);
+}
+
+__device__ inline void q_item_store(const QkvParams& p, int32_t grp, int32_t groups, int hgroups, int l, const NormW& w,
+                                    QItem& it) {
+  if (grp >= groups) return;
+  const int h0 = grp % hgroups * kQRows;
+  const int tok = grp / hgroups;
+  const int i = tok % p.tokens, b = tok / p.tokens;
+  uint16_t* dst = p.q_out + b * p.qo_sb + i * p.qo_st + static_cast<int64_t>(h0) * kHeadDim;
+  const RopeCS cs = rope_cs(it.ca, it.cb, it.sa, it.sb);
+#pragma unroll
+  for (int r = 0; r < kQRows; ++r) {
+    if (h0 + r >= p.hq) break;
+    rope_norm_row(it.xa[r], it.xb[r], cs, w, p.eps);
+    store_nt(dst + r * kHeadDim + 8 * l, it.xa[r]);
+    store_nt(dst + r * kHeadDim + 64 + 8 * l, it.xb[r]);
+  }
+}
 
 // Workgroups [0, kv_wgs) take one (sequence, 32-position block, kv head) each; the rest 32 groups of
 // kQRows query rows (heads [kQRows j, kQRows j + kQRows) of one token, j < ceil(Hq / kQRows)).
@@ -201,26 +283,13 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
   const int t = threadIdx.x, l = t & (kRowLanes - 1);
   if (static_cast<int>(blockIdx.x) >= kv_wgs) {
     const int hgroups = (p.hq + kQRows - 1) / kQRows;
-    const int64_t grp = (static_cast<int64_t>(blockIdx.x) - kv_wgs) * 32 + (t >> 3);  // (b, i, head group)
-    if (grp >= static_cast<int64_t>(p.batch) * p.tokens * hgroups) return;
-    const int h0 = static_cast<int>(grp % hgroups) * kQRows;
-    const int64_t tok = grp / hgroups;
-    const int i = static_cast<int>(tok % p.tokens), b = static_cast<int>(tok / p.tokens);
-    uint4 xa[kQRows], xb[kQRows], ca, cb, sa, sb;
-    const uint16_t* qrow = p.q + b * p.q_sb + i * p.q_st + static_cast<int64_t>(h0) * kHeadDim;
-#pragma unroll
-    for (int r = 0; r < kQRows; ++r)
-      if (h0 + r < p.hq) load_row_nt(qrow + r * kHeadDim, l, xa[r], xb[r]);
-    load_row(p.cos + b * p.cs_sb + i * p.cs_st, l, ca, cb);
-    load_row(p.sin + b * p.cs_sb + i * p.cs_st, l, sa, sb);
-    uint16_t* dst = p.q_out + b * p.qo_sb + i * p.qo_st + static_cast<int64_t>(h0) * kHeadDim;
-#pragma unroll
-    for (int r = 0; r < kQRows; ++r) {
-      if (h0 + r >= p.hq) break;
-      rope_norm_row(xa[r], xb[r], ca, cb, sa, sb, p.qw, l, p.eps);
-      store_nt(dst + r * kHeadDim + 8 * l, xa[r]);
-      store_nt(dst + r * kHeadDim + 64 + 8 * l, xb[r]);
-    }
+    const int32_t groups = p.batch * p.tokens * hgroups;  // < 2^31 (checked by the host)
+    const int32_t grp = (static_cast<int32_t>(blockIdx.x) - kv_wgs) * 32 + (t >> 3);
+    if (grp >= groups) return;
+    const NormW w = norm_weights(p.qw, l);
+    QItem it;
+    q_item_load(p, grp, groups, hgroups, l, it);
+    q_item_store(p, grp, groups, hgroups, l, w, it);
     return;
   }
   const int kv = static_cast<int>(blockIdx.x);
@@ -238,13 +307,14 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
   const int rblk = ((blk * kBlockTokens) % p.ring_tokens) >> 5;
   const int64_t roff = ring_ok ? rslot * p.r_ss + g * p.r_hs + write_block(p.r_tab, p.r_tab_stride, p.r_page, p.r_npages, b, rblk) : 0;
   const int64_t doff = deep_ok ? dslot * p.d_ss + g * p.d_hs + write_block(p.d_tab, p.d_tab_stride, p.d_page, p.d_npages, b, blk) : 0;
+  const NormW kw = norm_weights(p.kw, l);
   if (valid) {
     uint4 ka, kb, ca, cb, sa, sb, va, vb;
     load_row_nt(p.k + b * p.k_sb + i * p.k_st + static_cast<int64_t>(g) * kHeadDim, l, ka, kb);
     load_row_nt(p.v + b * p.v_sb + i * p.v_st + static_cast<int64_t>(g) * kHeadDim, l, va, vb);
     load_row(p.cos + b * p.cs_sb + i * p.cs_st, l, ca, cb);
     load_row(p.sin + b * p.cs_sb + i * p.cs_st, l, sa, sb);
-    rope_norm_row(ka, kb, ca, cb, sa, sb, p.kw, l, p.eps);
+    rope_norm_row(ka, kb, rope_cs(ca, cb, sa, sb), kw, p.eps);
     // dims [8l, 8l + 8) and [64 + 8l, 64 + 8l + 8) of token w are 16 contiguous bytes each in a K tile
     const int ko0 = k_tile_offset(w, 8 * l), ko1 = k_tile_offset(w, 64 + 8 * l);
     if (ring_ok) {
@@ -459,7 +529,7 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
     const int64_t q_groups = static_cast<int64_t>(a->batch) * a->tokens * ((a->num_q_heads + kQRows - 1) / kQRows);
     const int64_t kv_wgs = static_cast<int64_t>(a->batch) * a->num_kv_heads * kv_blocks;
     const int64_t wgs = kv_wgs + (q_groups + 31) / 32;
-    LKV_REQUIRE(wgs < (1LL << 31), "too many tokens in one call");
+    LKV_REQUIRE(wgs < (1LL << 31) && q_groups < (1LL << 31) - 32, "too many tokens in one call");
     qkv_block_kernel<<<static_cast<unsigned>(wgs), 256, 0, as_stream(stream)>>>(p, static_cast<int32_t>(kv_wgs),
                                                                               static_cast<int32_t>(kv_blocks));
   } else {
