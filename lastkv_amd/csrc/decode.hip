@@ -215,10 +215,22 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   // (the compiler then counts them exactly for s_waitcnt); the last one or two blocks follow it.
   const int first = blk_begin + (kPairs ? (wave & 1) : wave);
   if (first < blk_end) {
-    const int nw = (blk_end - 1 - first) / kStride + 1;
-    BlockFrags fa, fb;
-    BlockRef ra = block_ref(sv, first);
+    int nw = (blk_end - 1 - first) / kStride + 1;
+    // A wave with one block more than the workgroup's last wave (the split's block count is not a
+    // multiple of the waves) fetches that last block together with its first one and computes it
+    // after the loop, so its extra block adds compute but no round trip to memory: the loop, whose
+    // iterations are bound by load latency, then runs as many iterations in every wave.
+    const int last_first = blk_begin + (kPairs ? 1 : kWaves - 1);
+    const int nw_last = last_first < blk_end ? (blk_end - 1 - last_first) / kStride + 1 : 0;
+    const bool fold = nw > nw_last && nw >= 2;
+    BlockFrags fa, fb, fc;
+    BlockRef ra = block_ref(sv, first), rc{};
     load_block<kNT>(fa, ra, n16, g4);
+    if (fold) {
+      rc = block_ref(sv, first + kStride * (nw - 1));
+      load_block<kNT>(fc, rc, n16, g4);
+      --nw;
+    }
     int t = 0;
     // (the scheduling barriers keep the block being computed from moving above the next block's
     // loads, where reusing its registers would make the loads wait for it)
@@ -240,6 +252,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     } else {
       compute(fa, ra);
     }
+    if (fold) compute(fc, rc);
   }
 
   // merge the four waves' states
