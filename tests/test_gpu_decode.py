@@ -57,9 +57,14 @@ def test_pack_unpack_bit_exact_against_layout_oracle():
         assert np.array_equal(ops.cache_unpack(cache, kind, 100, 10).float().cpu().numpy(), x[:, :, :10])
 
 
-@pytest.mark.parametrize("tokens", [1, 31, 32, 33, 100, 1000])
+@pytest.mark.parametrize("tokens", [1, 31, 32, 33, 100, 161, 193, 1000, 8193])
 @pytest.mark.parametrize("splits", [1, 3])
 def test_shared_only_decode_matches_oracle(tokens, splits):
+    """Block counts 1-257 per sequence: 161 and 193 tokens (6 and 7 blocks) leave two and three of
+    a workgroup's four waves one block more than the last wave (the extra block is fetched with
+    the wave's first one and computed after its loop), 8193 tokens one wave (257 blocks, a 1-token
+    last block)."""
+
     rng = np.random.default_rng(tokens * 7 + splits)
     B, Hq, Hkv = 3, 8, 2
     q = _bf(rng, (B, Hq, 1, 128))

@@ -251,6 +251,58 @@ def test_8b_geometry_greedy_64_steps():
     _margin_aware_greedy(oracle, ours, prompt, 64, prefill_chunk=1024)
 
 
+def test_8b_full_shape_prompt_logits_no_worse_than_reference_bf16():
+    """Config 3's model at its full shape: 32 layers, the 128256-token vocabulary, random N(0, 0.02)
+    bf16 weights, per-layer blend alphas and V scales drawn at random (bf16 values), B = 4 prompts of
+    8192 tokens at C = 1024.  The logits of the last 64 prompt positions from the drop-in model
+    (2048-token prefill calls) and the last position's logits from the serving path (1024-token
+    steps on the paged pool) against the reference path with fp32 attention (o32): no further
+    from it than the reference path's own bf16 evaluation (o16), with as many argmax matches."""
+
+    from lastkv_amd.serving import LastKVServingModel
+
+    cfg = M.config_8b()
+    B, P, keep = 4, 8192, 64
+    default = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(DEV):
+            oracle = M.ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(default)
+    g = torch.Generator(device=DEV).manual_seed(0)
+    oracle = oracle.to(DEV, torch.bfloat16).init_weights(g).eval()
+    with torch.no_grad():
+        for layer in oracle.model.layers:
+            att = layer.self_attn
+            att.prev_chunk_alphas.copy_(torch.randn(att.prev_chunk_alphas.shape, generator=g, device=DEV))
+            att.deep_v_scale.copy_(torch.rand(att.deep_v_scale.shape, generator=g, device=DEV) * 1.2 + 0.3)
+    ours = Model(LastKVConfig.from_dict(dict(cfg.__dict__))).to(DEV, torch.bfloat16).eval()
+    ours.load_state_dict(oracle.state_dict(), strict=True)
+    prompt = torch.randint(0, cfg.vocab_size, (B, P), generator=torch.Generator().manual_seed(1)).to(DEV)
+    with torch.inference_mode():
+        l32 = _o32(oracle)(prompt, logits_to_keep=keep)[0].float()
+        l16 = _o16(oracle)(prompt, logits_to_keep=keep)[0].float()
+        cache = LastKVCache(cfg.num_hidden_layers, cfg.chunk_size, capacity_tokens=P)
+        for s in range(0, P, 2048):
+            out = ours(prompt[:, s:s + 2048], past_key_values=cache, logits_to_keep=keep)
+        got = out.logits.float()
+        del cache, out
+    del oracle
+    torch.cuda.empty_cache()
+    _no_worse_than_reference_bf16(got, l32, l16, "8B full shape, last 64 prompt positions, drop-in")
+    runner = LastKVServingModel(ours, max_batch=B, max_tokens_per_slot=P)
+    slots = [runner.add_sequence() for _ in range(B)]
+    with torch.inference_mode():
+        for s in range(0, P, 1024):
+            served = runner.step([(slot, prompt[b, s:s + 1024]) for b, slot in enumerate(slots)]).float()
+    ours_d, ref_d = _rel(served, l32[:, -1]), _rel(l16[:, -1], l32[:, -1])
+    agree = (served.argmax(-1) == l32[:, -1].argmax(-1)).sum().item()
+    print(f"8B full shape, last prompt position, serving: rel_l2 vs o32 {ours_d:.2e} / o16 {ref_d:.2e}; "
+          f"argmax matches {agree} of {B}", flush=True)
+    assert ours_d <= 1.5 * ref_d + 1e-3
+
+
 def _decisive_pair(cfg, prompt_len, seed=0):
     """The decisive-by-construction model (tests/decisive_model.py) as the oracle model (bf16)
     and the drop-in model holding the same weights."""
