@@ -447,6 +447,31 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
     # per sequence: how many leading generated tokens (the prefill's argmax first) the paths share
     prefix = (ids_hf[:, :n] == ids_served[:, :n]).int().cumprod(1).sum(1).cpu()
     rel_l2 = float((sv_logits - hf_logits).norm() / hf_logits.norm())
+    del runner, graph
+    torch.cuda.empty_cache()
+
+    # The same serving path on the reference's vLLM rounding contract (rings of V / s, raw shared V,
+    # output rescale, the fused QKV kernel's rounding): the decode attention reads V as stored.
+    runner = LastKVServingModel(model, max_batch=Bm, max_tokens_per_slot=prompt + decode_steps + 1, contract="vllm")
+    slots = [runner.add_sequence() for _ in range(Bm)]
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(0, prompt, CHUNK):
+            logits = runner.step([(slot, ids[b, s:s + CHUNK]) for b, slot in enumerate(slots)])
+        torch.cuda.synchronize()
+        t_vprefill = time.perf_counter() - t0
+        v_logits = logits.float()
+        tok = logits.argmax(-1)
+        graph = runner.decode_graph(slots)
+        _, tok = graph.step(tok)  # capture + first replay, untimed
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(decode_steps - 1):
+            _, tok = graph.step(tok)
+        torch.cuda.synchronize()
+        t_vdecode = time.perf_counter() - t0
+    v_rel = float((v_logits - hf_logits).norm() / hf_logits.norm())
     del runner, graph, model
     torch.cuda.empty_cache()
     return {
@@ -464,6 +489,14 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
             "prefill_s": round(t_sprefill, 3), "prefill_tok_s": round(Bm * prompt / t_sprefill, 1),
             "decode_ms_per_step": round(t_sdecode * 1e3 / (decode_steps - 1), 3),
             "decode_tok_s": round(Bm * (decode_steps - 1) / t_sdecode, 1),
+        },
+        "serving_path_vllm_contract": {
+            "how": "the serving path with the reference's vLLM rounding contract (V / s rings, raw shared V, "
+                   "output rescale, fused-QKV rounding)",
+            "prefill_s": round(t_vprefill, 3), "prefill_tok_s": round(Bm * prompt / t_vprefill, 1),
+            "decode_ms_per_step": round(t_vdecode * 1e3 / (decode_steps - 1), 3),
+            "decode_tok_s": round(Bm * (decode_steps - 1) / t_vdecode, 1),
+            "prefill_logits_rel_l2_vs_hf_path": round(v_rel, 5),
         },
         # The serving path's fused RMSNorm sums its squares in another order than torch's norm
         # (about 1 element in 1e5 differs by one bf16 ulp; with torch's norm in its place the two

@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 7
+#define LKV_ABI_VERSION 8
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -142,6 +142,12 @@ typedef struct lkv_decode_args {
    * keep for the next layer's call over the same shared cache), 1 = default policy, 2 =
    * non-temporal.  Results do not depend on it. */
   int32_t kv_cache_hint;
+  /* Optional output scale, fp32 [Hkv] (bf16-valued) or NULL: the output of query head h becomes
+   * bf16(bf16(o) * out_scale[h / group]), the serving path's per-head rescale of an attention over
+   * rings that hold V / s (fastpath.py:650 _head_scale / :690 output.mul_(out_scale),
+   * fused_qkv.py:130-156 head_scale_: the bf16 output times s in fp32, one rounding).  lse is not
+   * scaled. */
+  const float *out_scale;
 } lkv_decode_args;
 
 int64_t lkv_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_splits);
@@ -243,6 +249,8 @@ typedef struct lkv_prefill_args {
    * count.  4 / 8: always the tile kernel, with that many waves (32 rows each) above 64 rows per
    * kv head and 2 waves at or below. */
   int32_t tile_waves;
+  /* Optional output scale, fp32 [Hkv] (bf16-valued) or NULL, as in lkv_decode_args. */
+  const float *out_scale;
 } lkv_prefill_args;
 
 /* Workspace bytes lkv_prefill_attn needs for these args: the fp16 V of every key block of every
@@ -257,9 +265,10 @@ int32_t lkv_prefill_attn(const lkv_prefill_args *args, lkv_stream_t stream);
  *
  * Replaces modeling.py:103-108 (apply_rotary_pos_emb, q_norm / k_norm, append of the new K/V to
  * current[l]) and, on the serving path, fused_qkv.py:58-126 (_fused_qkv_kernel: rotary + RMSNorm
- * + ring / slab K,V writes).  Arithmetic follows the torch op order of the reference's bf16
- * model: rope = bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)); norm = bf16(w * bf16(x * r)) with
- * r = 1 / sqrt(mean(x^2) + eps) in fp32 (transformers LlamaRMSNorm, modeling.py:90-91).
+ * + ring / slab K,V writes).  With rounding = 0 the arithmetic follows the torch op order of the
+ * reference's bf16 model: rope = bf16(bf16(x*cos) + bf16(rotate_half(x)*sin)); norm =
+ * bf16(w * bf16(x * r)) with r = 1 / sqrt(mean(x^2) + eps) in fp32 (transformers LlamaRMSNorm,
+ * modeling.py:90-91); rounding = 1 follows the fused_qkv kernel instead (see the field).
  * For new token i of sequence b at cache position p = pos(b) + i (pos(b) = positions[b], or
  * position_const when positions is NULL):
  *   q_out[b, i, h, :] = norm_q(rope(q[b, i, h, :]))                  for h < Hq
@@ -325,6 +334,18 @@ typedef struct lkv_qkv_args {
   int64_t deep_table_stride;
   int64_t deep_page_stride;
   int32_t deep_num_pages;
+  /* Rounding contract of RoPE and RMSNorm: 0 = the torch op order above (the HF model); 1 = the
+   * vLLM fused_qkv kernel (fused_qkv.py:24-55): rope = (bf16(fma(x, c, -(y * s))), bf16(fma(y, c,
+   * x * s))) over the halves x = dims [0, 64), y = dims [64, 128) with c, s the cos / sin of dims
+   * [0, 64); RMSNorm sums the squares as 16 groups of 8 consecutive dims, each accumulated in order
+   * with fused multiply-adds, then adjacent groups pairwise (16 -> 8 -> 4 -> 2 -> 1), and writes
+   * bf16(x * r * w) with fp32 products.  r = 1 / sqrt(sum / 128 + eps) in both contracts (fp32,
+   * correctly rounded square root and division; the reference's rsqrt.approx is hardware-specific). */
+  int32_t rounding;
+  /* Optional fp32 [Hkv] or NULL: the ring receives V as bf16(v * ring_v_mul[g]) (the vLLM path's
+   * rings of V / s with ring_v_mul = fp32(1 / s), fused_qkv.py:84-86); the deep write keeps the
+   * raw V (fused_qkv.py:87-90). */
+  const float *ring_v_mul;
 } lkv_qkv_args;
 
 int32_t lkv_qkv_epilogue(const lkv_qkv_args *args, lkv_stream_t stream);

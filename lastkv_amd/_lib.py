@@ -11,7 +11,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class LastKVNativeError(RuntimeError):
@@ -73,6 +73,7 @@ class DecodeArgs(ctypes.Structure):
         ("local_page_stride", c_i64),
         ("local_num_pages", c_i32),
         ("kv_cache_hint", c_i32),
+        ("out_scale", c_ptr),
     ]
 
 
@@ -128,6 +129,7 @@ class PrefillArgs(ctypes.Structure):
         ("local_page_stride", c_i64),
         ("local_num_pages", c_i32),
         ("tile_waves", c_i32),
+        ("out_scale", c_ptr),
     ]
 
 
@@ -244,6 +246,8 @@ class QkvArgs(ctypes.Structure):
         ("deep_table_stride", c_i64),
         ("deep_page_stride", c_i64),
         ("deep_num_pages", c_i32),
+        ("rounding", c_i32),
+        ("ring_v_mul", c_ptr),
     ]
 
 

@@ -34,12 +34,20 @@ struct DecodeParams {
   float* lse;
   SegParams seg;
   const float* vscale;
+  const float* out_scale;  // [Hkv] or nullptr: out = bf16(bf16(o) * out_scale[kvh])
   float* ws_o;
   float* ws_ml;
   int32_t hq, group, splits;
   int32_t L, causal;  // query tokens per sequence (1 for decode calls) and bottom-right causality
   float scale_log2;
 };
+
+// The bf16 output of a normalised fp32 value x of kv head kvh: bf16(x), or bf16(bf16(x) * s) with
+// an output scale (the reference rescales its bf16 attention output by s in fp32).
+__device__ inline uint16_t out_bits(float x, const float* out_scale, int kvh) {
+  if (out_scale == nullptr) return f32_to_bf16_bits(x);
+  return f32_to_bf16_bits(bf16_bits_to_f32(f32_to_bf16_bits(x)) * out_scale[kvh]);
+}
 
 struct BlockFrags {
   uint4 k[2][4];
@@ -292,7 +300,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     }
     if (p.splits == 1) {
       p.out[b * p.out_sb + (kMulti ? tq * p.out_st : 0) + static_cast<int64_t>(kvh * G + hh) * kHeadDim + d] =
-          f32_to_bf16_bits(L > 0.f ? O / L : 0.f);
+          out_bits(L > 0.f ? O / L : 0.f, p.out_scale, kvh);
       if (p.lse != nullptr && d == 0) p.lse[row_q] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
     } else {
       const int64_t row = row_q * p.splits + split;
@@ -353,7 +361,8 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const D
   }
   for (; s < S; ++s) O[0] += sm_w[s] * o[s * kHeadDim + d];
   const float Ot = (O[0] + O[1]) + (O[2] + O[3]);
-  p.out[b * p.out_sb + tq * p.out_st + static_cast<int64_t>(h) * kHeadDim + d] = f32_to_bf16_bits(L > 0.f ? Ot / L : 0.f);
+  p.out[b * p.out_sb + tq * p.out_st + static_cast<int64_t>(h) * kHeadDim + d] =
+      out_bits(L > 0.f ? Ot / L : 0.f, p.out_scale, h / p.group);
   if (p.lse != nullptr && d == 0) p.lse[bh] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
 }
 
@@ -427,6 +436,7 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   p.out_st = a->out_stride_t;
   p.lse = a->lse;
   p.vscale = a->vscale;
+  p.out_scale = a->out_scale;
   p.hq = a->num_q_heads;
   p.group = group;
   p.L = a->tokens;
@@ -503,6 +513,7 @@ int32_t run_decode(const lkv_decode_args* a, void* ws, int64_t ws_bytes, hipStre
   p.causal = 0;
   p.lse = a->lse;
   p.vscale = a->vscale;
+  p.out_scale = a->out_scale;
   p.ws_o = static_cast<float*>(ws);
   p.ws_ml = need > 0 ? p.ws_o + static_cast<int64_t>(a->batch) * a->num_q_heads * a->num_splits * kHeadDim : nullptr;
   p.hq = a->num_q_heads;

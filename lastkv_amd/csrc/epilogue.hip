@@ -3,7 +3,9 @@
 // Epilogue, decode-sized calls: one wave per (token, head) of the Hq + Hkv heads; lane l owns dims
 // l and l + 64, the two halves that rotate_half pairs, so RoPE needs no lane exchange and RMSNorm
 // one wave sum.  Calls of many tokens: the block form below (16-byte accesses, V tiles written
-// through LDS).  Every intermediate is rounded to bf16 where the reference's bf16 torch ops round.
+// through LDS).  Two rounding contracts: the torch op order of the HF model (every intermediate
+// rounded to bf16 where the reference's bf16 torch ops round) and the vLLM fused_qkv kernel's
+// (fused multiply-adds, one rounding per output, a fixed RMSNorm summation order).
 #include "common.h"
 #include "runtime.h"
 
@@ -46,6 +48,8 @@ struct QkvParams {
   const int32_t* d_tab;
   int64_t d_tab_stride, d_page;
   int32_t d_npages;
+  int32_t rounding;      // 0: torch op order (HF model), 1: vLLM fused_qkv order
+  const float* rv_mul;   // ring V := bf16(v * rv_mul[g]) (the vLLM path's V / s rings), or nullptr
 };
 
 // Element offset of block blk of sequence b: contiguous per slot, or a clamped page of a pool.
@@ -53,6 +57,36 @@ __device__ inline int64_t write_block(const int32_t* tab, int64_t tab_stride, in
                                       int blk) {
   if (tab == nullptr) return static_cast<int64_t>(blk) * kBlockElems;
   return static_cast<int64_t>(min(max(tab[b * tab_stride + blk], 0), npages - 1)) * page;
+}
+
+// vLLM fused_qkv arithmetic (fused_qkv.py:24-55) of one row, lane l holding dims l and l + 64:
+// r = (bf16(fma(x0, c, -(x1 * s))), bf16(fma(x1, c, x0 * s))); the RMSNorm sum runs over the 16
+// groups of 8 consecutive dims (lanes 8j..8j+7 of each half), the squares of a group accumulated
+// in order with fused multiply-adds, then adjacent groups added pairwise (lane xor 8, 16, 32, then
+// the two halves); out = bf16(r * inv * w) with fp32 products.  No contraction: every product and
+// sum rounds where the reference's does.
+__device__ inline void rope_norm_vllm_lane(float x0, float x1, float c, float s, const uint16_t* w, int lane,
+                                           float eps, float& r0, float& r1) {
+#pragma clang fp contract(off)
+  r0 = rb(__builtin_fmaf(x0, c, -(x1 * s)));
+  r1 = rb(__builtin_fmaf(x1, c, x0 * s));
+  if (w == nullptr) return;
+  const int base = lane & ~7;
+  float sa = 0.f, sb = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float ua = __shfl(r0, base + e), ub = __shfl(r1, base + e);
+    sa = __builtin_fmaf(ua, ua, sa);
+    sb = __builtin_fmaf(ub, ub, sb);
+  }
+#pragma unroll
+  for (int off = 8; off <= 32; off <<= 1) {
+    sa += __shfl_xor(sa, off);
+    sb += __shfl_xor(sb, off);
+  }
+  const float inv = 1.0f / sqrtf((sa + sb) / static_cast<float>(kHeadDim) + eps);
+  r0 = rb(r0 * inv * bf16_bits_to_f32(w[lane]));
+  r1 = rb(r1 * inv * bf16_bits_to_f32(w[lane + 64]));
 }
 
 __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
@@ -74,15 +108,20 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
   const uint16_t* sp = p.sin + b * p.cs_sb + i * p.cs_st;
   const float c0 = bf16_bits_to_f32(cp[lane]), c1 = bf16_bits_to_f32(cp[lane + 64]);
   const float s0 = bf16_bits_to_f32(sp[lane]), s1 = bf16_bits_to_f32(sp[lane + 64]);
-  // q * cos + rotate_half(q) * sin, rotate_half(q) = cat(-q[64:], q[:64]); three bf16 roundings
-  float r0 = rb(rb(x0 * c0) + rb(-x1 * s0));
-  float r1 = rb(rb(x1 * c1) + rb(x0 * s1));
   const uint16_t* w = is_q ? p.qw : p.kw;
-  if (w != nullptr) {
-    const float ss = wave_sum64(r0 * r0 + r1 * r1);
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHeadDim) + p.eps);
-    r0 = rb(bf16_bits_to_f32(w[lane]) * rb(r0 * inv));
-    r1 = rb(bf16_bits_to_f32(w[lane + 64]) * rb(r1 * inv));
+  float r0, r1;
+  if (p.rounding == 0) {
+    // q * cos + rotate_half(q) * sin, rotate_half(q) = cat(-q[64:], q[:64]); three bf16 roundings
+    r0 = rb(rb(x0 * c0) + rb(-x1 * s0));
+    r1 = rb(rb(x1 * c1) + rb(x0 * s1));
+    if (w != nullptr) {
+      const float ss = wave_sum64(r0 * r0 + r1 * r1);
+      const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHeadDim) + p.eps);
+      r0 = rb(bf16_bits_to_f32(w[lane]) * rb(r0 * inv));
+      r1 = rb(bf16_bits_to_f32(w[lane + 64]) * rb(r1 * inv));
+    }
+  } else {
+    rope_norm_vllm_lane(x0, x1, c0, s0, w, lane, p.eps, r0, r1);
   }
   const uint16_t o0 = f32_to_bf16_bits(r0), o1 = f32_to_bf16_bits(r1);
   if (is_q) {
@@ -96,6 +135,10 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
   const uint16_t* vrow = p.v + b * p.v_sb + i * p.v_st + static_cast<int64_t>(g) * kHeadDim;
   const uint16_t v0 = vrow[lane], v1 = vrow[lane + 64];
   {
+    // the ring's V, scaled for the vLLM path (fp32 product, one rounding); the deep write is raw
+    const float m = p.rv_mul != nullptr ? p.rv_mul[g] : 1.f;
+    const uint16_t rv0 = p.rv_mul != nullptr ? f32_to_bf16_bits(bf16_bits_to_f32(v0) * m) : v0;
+    const uint16_t rv1 = p.rv_mul != nullptr ? f32_to_bf16_bits(bf16_bits_to_f32(v1) * m) : v1;
     const int slot = p.r_tab ? 0 : (p.ring_slot ? p.ring_slot[b] : b);
     if (slot >= 0 && slot < p.ring_slots) {
       const int rt = position % p.ring_tokens;
@@ -105,8 +148,8 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
       const int wt = rt & 31;
       kb[k_tile_offset(wt, lane)] = o0;
       kb[k_tile_offset(wt, lane + 64)] = o1;
-      vb[v_tile_offset(wt, lane)] = v0;
-      vb[v_tile_offset(wt, lane + 64)] = v1;
+      vb[v_tile_offset(wt, lane)] = rv0;
+      vb[v_tile_offset(wt, lane + 64)] = rv1;
     }
   }
   if (p.dk != nullptr && position < p.deep_cap) {
@@ -218,6 +261,60 @@ __device__ inline void rope_norm_row(uint4& a, uint4& b, const RopeCS& cs, const
   b = pack8(r1);
 }
 
+// The vLLM fused_qkv order (fused_qkv.py:24-55) of the row held by an 8-lane group: lane l holds
+// dims [8l, 8l + 8) and [64 + 8l, 64 + 8l + 8), i.e. groups l and 8 + l of the 16 groups of 8 dims
+// whose squares the reference accumulates in order with fused multiply-adds; adjacent groups are
+// then added pairwise (lane xor 1, 2, 4) and the two halves last.  cos / sin of dims [0, 64) rotate
+// both halves.
+__device__ inline void rope_norm_row_vllm(uint4& a, uint4& b, const RopeCS& cs, const NormW& w, float eps) {
+#pragma clang fp contract(off)
+  float x0[8], x1[8], r0[8], r1[8];
+  unpack8(a, x0), unpack8(b, x1);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    r0[j] = __builtin_fmaf(x0[j], cs.c0[j], -(x1[j] * cs.s0[j]));
+    r1[j] = __builtin_fmaf(x1[j], cs.c0[j], x0[j] * cs.s0[j]);
+    rb2(r0[j], r1[j]);
+  }
+  if (w.on) {
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sa = __builtin_fmaf(r0[j], r0[j], sa);
+      sb = __builtin_fmaf(r1[j], r1[j], sb);
+    }
+#pragma unroll
+    for (int off = 1; off <= 4; off <<= 1) {
+      sa += __shfl_xor(sa, off);
+      sb += __shfl_xor(sb, off);
+    }
+    const float inv = 1.0f / sqrtf((sa + sb) / static_cast<float>(kHeadDim) + eps);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      r0[j] = r0[j] * inv * w.w0[j];  // rounded by the packing below
+      r1[j] = r1[j] * inv * w.w1[j];
+    }
+  }
+  a = pack8(r0);
+  b = pack8(r1);
+}
+
+__device__ inline void rope_norm_row_any(uint4& a, uint4& b, const RopeCS& cs, const NormW& w, float eps, int rounding) {
+  if (rounding == 0)
+    rope_norm_row(a, b, cs, w, eps);
+  else
+    rope_norm_row_vllm(a, b, cs, w, eps);
+}
+
+// 8 bf16 values times m (fp32 products, one rounding each).
+__device__ inline uint4 scale8(uint4 x, float m) {
+  float f[8];
+  unpack8(x, f);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] *= m;
+  return pack8(f);
+}
+
 __device__ inline void load_row(const uint16_t* row, int l, uint4& a, uint4& b) {
   a = *reinterpret_cast<const uint4*>(row + 8 * l);
   b = *reinterpret_cast<const uint4*>(row + 64 + 8 * l);
@@ -270,7 +367,7 @@ __device__ inline void q_item_store(const QkvParams& p, int32_t grp, int32_t gro
 #pragma unroll
   for (int r = 0; r < kQRows; ++r) {
     if (h0 + r >= p.hq) break;
-    rope_norm_row(it.xa[r], it.xb[r], cs, w, p.eps);
+    rope_norm_row_any(it.xa[r], it.xb[r], cs, w, p.eps, p.rounding);
     store_nt(dst + r * kHeadDim + 8 * l, it.xa[r]);
     store_nt(dst + r * kHeadDim + 64 + 8 * l, it.xb[r]);
   }
@@ -314,7 +411,7 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
     load_row_nt(p.v + b * p.v_sb + i * p.v_st + static_cast<int64_t>(g) * kHeadDim, l, va, vb);
     load_row(p.cos + b * p.cs_sb + i * p.cs_st, l, ca, cb);
     load_row(p.sin + b * p.cs_sb + i * p.cs_st, l, sa, sb);
-    rope_norm_row(ka, kb, rope_cs(ca, cb, sa, sb), kw, p.eps);
+    rope_norm_row_any(ka, kb, rope_cs(ca, cb, sa, sb), kw, p.eps, p.rounding);
     // dims [8l, 8l + 8) and [64 + 8l, 64 + 8l + 8) of token w are 16 contiguous bytes each in a K tile
     const int ko0 = k_tile_offset(w, 8 * l), ko1 = k_tile_offset(w, 64 + 8 * l);
     if (ring_ok) {
@@ -334,20 +431,24 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
     }
   }
   __syncthreads();
-  // V tile: element (token w, dim d) at d * 32 + w; 512 runs of 8 tokens of one dim
+  // V tile: element (token w, dim d) at d * 32 + w; 512 runs of 8 tokens of one dim.  The ring
+  // takes bf16(v * rv_mul[g]) on the vLLM path, the deep store the raw V.
   const int lo = max(0, p0 - blk * kBlockTokens), hi = min(kBlockTokens, p0 + p.tokens - blk * kBlockTokens);
+  const float vm = p.rv_mul != nullptr ? p.rv_mul[g] : 1.f;
 #pragma unroll
   for (int run = t; run < kHeadDim * 4; run += 256) {
     const int d = run >> 2, w0 = 8 * (run & 3);
     if (w0 + 8 <= lo || w0 >= hi) continue;
     const uint4 x = *reinterpret_cast<const uint4*>(sv + d * kVStride + w0);
+    const uint4 xr = p.rv_mul != nullptr ? scale8(x, vm) : x;
     if (w0 >= lo && w0 + 8 <= hi) {
-      if (ring_ok) store_nt(p.rv + roff + d * kBlockTokens + w0, x);
+      if (ring_ok) store_nt(p.rv + roff + d * kBlockTokens + w0, xr);
       if (deep_ok) store_nt(p.dv + doff + d * kBlockTokens + w0, x);
     } else {  // a block edge of the call: only its own tokens
       const uint16_t* e = reinterpret_cast<const uint16_t*>(&x);
+      const uint16_t* er = reinterpret_cast<const uint16_t*>(&xr);
       for (int j = max(lo - w0, 0); j < min(hi - w0, 8); ++j) {
-        if (ring_ok) p.rv[roff + d * kBlockTokens + w0 + j] = e[j];
+        if (ring_ok) p.rv[roff + d * kBlockTokens + w0 + j] = er[j];
         if (deep_ok) p.dv[doff + d * kBlockTokens + w0 + j] = e[j];
       }
     }
@@ -454,6 +555,8 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
     LKV_REQUIRE(a->deep_slot != nullptr || a->deep_num_slots >= a->batch, "deep cache has fewer slots than sequences");
   }
   LKV_REQUIRE(a->positions != nullptr || a->position_const >= 0, "negative position");
+  LKV_REQUIRE(a->rounding == 0 || a->rounding == 1, "rounding must be 0 (torch op order) or 1 (vLLM fused_qkv), got %d",
+              a->rounding);
   const int64_t items = static_cast<int64_t>(a->batch) * a->tokens * (a->num_q_heads + a->num_kv_heads);
   if (items == 0) return LKV_OK;
   LKV_REQUIRE(items / 4 + 1 < (1LL << 31), "too many tokens in one call");
@@ -506,6 +609,8 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
   p.d_tab_stride = a->deep_table_stride;
   p.d_page = a->deep_page_stride;
   p.d_npages = a->deep_num_pages;
+  p.rounding = a->rounding;
+  p.rv_mul = a->ring_v_mul;
   // Calls of many tokens with 16-byte-aligned rows take the block form (16-byte accesses, V tiles
   // written through LDS), provided the call's 32-position blocks do not wrap onto each other in the
   // ring; decode-sized calls keep one wave per (token, head).

@@ -40,6 +40,7 @@ struct PrefillParams {
   float* lse;
   SegParams seg;
   const float* vscale;
+  const float* out_scale;  // [Hkv] or nullptr: out = bf16(bf16(o) * out_scale[kvh])
   int32_t L, hq, hkv, group, causal, tiles;
   float scale_log2;
   int32_t vscale_mode;
@@ -491,6 +492,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   }
 
   // normalise and write: lane (n16, g4) holds dims 16 * nb + 4 * g4 + i of row n16 of each group
+  const float os = p.out_scale != nullptr ? p.out_scale[kvh] : 1.f;
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
     const float lt = ol[cg][0];
@@ -502,7 +504,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) {
         const f32x4 x = o[cg][nb] * linv;
-        *reinterpret_cast<uint2*>(orow + 16 * nb + 4 * g4) = make_uint2(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]));
+        uint32_t w01 = pack_bf16x2(x[0], x[1]), w23 = pack_bf16x2(x[2], x[3]);
+        if (p.out_scale != nullptr) {  // bf16(bf16(o) * s), the reference's rescale of its bf16 output
+          w01 = pack_bf16x2(bf16_lo(w01) * os, bf16_hi(w01) * os);
+          w23 = pack_bf16x2(bf16_lo(w23) * os, bf16_hi(w23) * os);
+        }
+        *reinterpret_cast<uint2*>(orow + 16 * nb + 4 * g4) = make_uint2(w01, w23);
       }
       if (p.lse != nullptr && g4 == 0)
         p.lse[(static_cast<int64_t>(b) * p.L + tok) * p.hq + kvh * G + h] =
@@ -591,6 +598,7 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.out_st = a->out_stride_t;
   p.lse = a->lse;
   p.vscale = a->vscale;
+  p.out_scale = a->out_scale;
   p.L = a->tokens;
   p.hq = a->num_q_heads;
   p.group = group;

@@ -303,6 +303,13 @@ def _fill_segments(a, B: int, device: torch.device, older, older_len, older_slot
     return Hkv
 
 
+def _out_scale_arg(a, out_scale: torch.Tensor | None, Hkv: int, device: torch.device) -> None:
+    if out_scale is not None:
+        _require(out_scale.dtype == torch.float32 and out_scale.numel() == Hkv and out_scale.is_contiguous()
+                 and out_scale.device == device, "out_scale must be a contiguous fp32 [Hkv] tensor on the query's device")
+    a.out_scale = _ptr(out_scale)
+
+
 def decode_attention(
     q: torch.Tensor,
     *,
@@ -324,11 +331,14 @@ def decode_attention(
     workspace: torch.Tensor | None = None,
     kv_cache_hint: int = 0,
     no_alloc: bool = False,
+    out_scale: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """One-token-per-sequence attention over ``[older shared segment | local ring segment]``.
 
     ``q`` is ``[B, Hq, 128]`` bf16 (or ``[B, Hq, 1, 128]``).  ``vscale`` ``[Hkv]`` fp32 switches
-    the older segment's V to ``bf16(V * vscale[h])``.  Returns ``out`` ``[B, Hq, 128]`` bf16.
+    the older segment's V to ``bf16(V * vscale[h])``.  ``out_scale`` ``[Hkv]`` fp32 (bf16 values)
+    makes the output ``bf16(bf16(o) * out_scale[h])``, the vLLM path's rescale of an attention over
+    rings of V / s.  Returns ``out`` ``[B, Hq, 128]`` bf16.
     ``kv_cache_hint`` selects the cache policy of the K/V loads (0 = by the call's K/V size,
     1 = default, 2 = non-temporal); the results do not depend on it.  ``no_alloc`` calls
     ``lkv_decode_attn_noalloc``: the split states go to the library's static per-GPU scratch
@@ -377,6 +387,7 @@ def decode_attention(
     a.batch, a.num_q_heads, a.num_kv_heads, a.head_dim = B, Hq, Hkv, HEAD_DIM
     a.num_splits = num_splits
     a.kv_cache_hint = int(kv_cache_hint)
+    _out_scale_arg(a, out_scale, Hkv, device)
     a.sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
     a.q, a.q_stride_b = q.data_ptr(), q.stride(0)
     a.out, a.out_stride_b = out.data_ptr(), out.stride(0)
@@ -410,6 +421,7 @@ def prefill_attention(
     lse: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     tile_waves: int = 0,
+    out_scale: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention of ``q`` ``[B, L, Hq, 128]`` (L query tokens per sequence, the last L tokens of
     the local segment) over ``[older | local]``; the local segment is bottom-right causal
@@ -418,7 +430,7 @@ def prefill_attention(
     ``workspace`` (uint8, 16-byte aligned, at least ``prefill_workspace_bytes`` of the same
     arguments) receives the fp16 V of every key block; without it one is allocated per call.
     ``tile_waves`` (0, 4 or 8) fixes the workgroup size of the tile kernel; 0 lets the library
-    choose from the grid size and the device's CU count."""
+    choose from the grid size and the device's CU count.  ``out_scale`` as in ``decode_attention``."""
 
     _require_bf16_cuda("q", q)
     _require(q.dim() == 4 and q.shape[-1] == HEAD_DIM, "q must be [B, L, Hq, 128]")
@@ -442,6 +454,7 @@ def prefill_attention(
     a.sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
     a.causal = 1 if causal else 0
     a.tile_waves = int(tile_waves)
+    _out_scale_arg(a, out_scale, Hkv, device)
     a.q, a.q_stride_b, a.q_stride_t = q.data_ptr(), q.stride(0), q.stride(1)
     a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
     a.lse = _ptr(lse)
@@ -548,6 +561,10 @@ def _rows(name: str, t: torch.Tensor, heads: int) -> tuple[int, int, int]:
     return t.data_ptr(), t.stride(0), t.stride(1)
 
 
+# rounding contracts of lkv_qkv_epilogue (lkv_qkv_args.rounding)
+ROUNDINGS = {"torch": 0, "vllm": 1}
+
+
 def qkv_epilogue(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -569,11 +586,18 @@ def qkv_epilogue(
     ring_table: torch.Tensor | None = None,
     ring_tokens: int | None = None,
     deep_table: torch.Tensor | None = None,
+    rounding: str = "torch",
+    ring_v_mul: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """RoPE + q/k RMSNorm of the projections and the append of K/V to the layer ring (and, for
     the final layer, the shared cache) at positions ``positions + i``; returns the normalised
     queries ``[B, L, Hq, 128]``.  A PagedKV ring / deep store takes an int32 page table ``[B, W]``
-    (``ring_tokens``: the ring length, default ``32 * W``)."""
+    (``ring_tokens``: the ring length, default ``32 * W``).
+
+    ``rounding``: ``"torch"``, the HF model's bf16 op order, or ``"vllm"``, the reference's fused
+    QKV kernel (single-FMA rotary, fixed RMSNorm summation order).  ``ring_v_mul`` ``[Hkv]`` fp32
+    writes the ring's V as ``bf16(v * ring_v_mul[g])`` (the vLLM path's V / s rings); the shared
+    cache keeps the raw V."""
 
     B, L = int(q.shape[0]), int(q.shape[1])
     qp, qsb, qst = _rows("q", q, num_q_heads)
@@ -594,9 +618,15 @@ def qkv_epilogue(
     if q_out is None:
         q_out = torch.empty((B, L, num_q_heads, HEAD_DIM), dtype=torch.bfloat16, device=device)
     _require(q_out.is_contiguous() and tuple(q_out.shape) == (B, L, num_q_heads, HEAD_DIM), "q_out must be contiguous [B, L, Hq, 128]")
+    _require(rounding in ROUNDINGS, f"rounding must be one of {sorted(ROUNDINGS)}, got {rounding!r}")
+    if ring_v_mul is not None:
+        _require(ring_v_mul.dtype == torch.float32 and ring_v_mul.numel() == num_kv_heads and ring_v_mul.is_contiguous()
+                 and ring_v_mul.device == device, "ring_v_mul must be a contiguous fp32 [Hkv] tensor on the query's device")
     a = _lib.QkvArgs()
     a.struct_size = ctypes.sizeof(_lib.QkvArgs)
     a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = B, L, num_q_heads, num_kv_heads, HEAD_DIM
+    a.rounding = ROUNDINGS[rounding]
+    a.ring_v_mul = _ptr(ring_v_mul)
     a.eps = float(eps)
     a.positions, a.position_const = _len_arg(positions, B, "positions", device)
     a.q, a.q_stride_b, a.q_stride_t = qp, qsb, qst

@@ -15,10 +15,16 @@ shared append on the final layer) and one attention pass over [shared older page
 written into ``output``.  For a decode step every per-layer call reads only device-resident
 metadata and preallocated buffers.
 
-Rounding contract: the HF bf16 one (older V used as bf16(V * s_l) inside the attention kernel,
-the recent chunk blended once per boundary in bf16), i.e. the numbers of ``lastkv_amd.llm``.  The
-reference's vLLM path instead keeps V / s_l in the rings and rescales the output
-(``fastpath.py:652-690``); that variant's extra roundings are not reproduced.
+Two rounding contracts (``contract=``):
+  - ``"hf"`` (default): the numbers of ``lastkv_amd.llm`` -- RoPE and RMSNorm in the torch op order,
+    the older segment's V used as bf16(V * s_l) inside the attention kernel, the recent chunk
+    blended once per boundary in bf16;
+  - ``"vllm"``: the reference's merged serving path (``fastpath.py:619-651``, ``fused_qkv.py``) --
+    RoPE with one FMA and one rounding per output and RMSNorm in the fused kernel's summation order,
+    rings holding bf16(V * fp32(1 / s_l)) next to the raw V of the shared pages, one attention pass
+    over both, the bf16 output rescaled by s_l (``_head_scale``), and the boundary blend of the rings
+    with the unscaled shared V (``batching.py:1124-1140``).  The attention then reads every V as
+    stored, with no per-element scaling of the older segment.
 """
 
 from __future__ import annotations
@@ -209,10 +215,11 @@ class LastKVFastPath:
     fp32 [Hkv] or None); ``blend`` = (alpha, one_minus_alpha, vscale-or-None), fp32 ``[L * Hkv]``
     as ``blend_chunk`` takes them; ``rotary(positions [B, n]) -> (cos, sin)`` bf16 ``[B, n, 128]``.
     ``from_model`` takes all three from a ``lastkv_amd.llm`` model.  ``num_splits`` fixes the
-    decode split count (default: chosen per step from the longest row)."""
+    decode split count (default: chosen per step from the longest row).  ``contract`` selects the
+    rounding contract (module docstring): ``"hf"`` or ``"vllm"``."""
 
     def __init__(self, pool: LastKVPagePool, *, num_q_heads: int, layer_params, blend, rotary, max_batch: int,
-                 num_splits: int | None = None):
+                 num_splits: int | None = None, contract: str = "hf"):
         self.pool = pool
         self.num_q_heads = num_q_heads
         self.layer_params = list(layer_params)
@@ -220,6 +227,19 @@ class LastKVFastPath:
             raise ValueError("one parameter tuple per layer is required")
         if num_q_heads % pool.kv_heads:
             raise ValueError("num_q_heads must be a multiple of the pool's kv heads")
+        if contract not in ("hf", "vllm"):
+            raise ValueError(f"contract must be 'hf' or 'vllm', got {contract!r}")
+        self.contract = contract
+        # vLLM contract: per layer the ring's V multiplier fp32(1 / s) and the output scale s
+        # (fastpath.py:254-267: scales must be finite and non-zero)
+        self._ring_v_mul: list[torch.Tensor | None] = [None] * pool.num_layers
+        if contract == "vllm":
+            for l, (_, _, _, vs) in enumerate(self.layer_params):
+                if vs is None:
+                    continue
+                if not bool(torch.isfinite(vs).all()) or bool((vs == 0).any()):
+                    raise ValueError("value scales must be finite and non-zero for the vLLM contract")
+                self._ring_v_mul[l] = (1.0 / vs.float()).contiguous()
         self.blend = blend
         self.rotary = rotary
         self.max_batch = max_batch
@@ -247,7 +267,8 @@ class LastKVFastPath:
         self._row_splits: list[int] = []
 
     @classmethod
-    def from_model(cls, model, pool: LastKVPagePool, *, max_batch: int, num_splits: int | None = None) -> "LastKVFastPath":
+    def from_model(cls, model, pool: LastKVPagePool, *, max_batch: int, num_splits: int | None = None,
+                   contract: str = "hf") -> "LastKVFastPath":
         """Parameters of a ``lastkv_amd.llm`` decoder: its layers' q/k norms, V scales and blend gates."""
 
         inner = getattr(model, "model", model)
@@ -266,7 +287,7 @@ class LastKVFastPath:
             return cos, sin
 
         return cls(pool, num_q_heads=cfg.num_attention_heads, layer_params=params, blend=inner._blend_params(),
-                   rotary=rotary, max_batch=max_batch, num_splits=num_splits)
+                   rotary=rotary, max_batch=max_batch, num_splits=num_splits, contract=contract)
 
     # -------------------------------------------------------------- sequences
     def add_sequence(self) -> int:
@@ -380,6 +401,8 @@ class LastKVFastPath:
 
         P = self.pool
         alpha, om, s = self.blend
+        if self.contract == "vllm":  # rings hold V / s: blend with the unscaled shared V
+            s = None
         ops.blend_chunk(P.pool.k, P.pool.v, P.pool, batch=1, chunk_start=boundary - P.chunk_size, chunk_len=P.chunk_size,
                         alpha=alpha, one_minus_alpha=om, vscale=s, ring_table=P.ring_table[:, slot:slot + 1],
                         ring_tokens=P.ring_tokens, deep_table=P.src_table[slot:slot + 1])
@@ -398,6 +421,13 @@ class LastKVFastPath:
         if min(query.shape[0], key.shape[0], value.shape[0], output.shape[0]) < T:
             raise ValueError(f"this step has {T} query tokens")
         qn_w, kn_w, eps, vs = self.layer_params[layer_index]
+        # vLLM contract: rings of V / s (the epilogue scales the ring's V), attention over V as stored,
+        # output rescaled by s; HF contract: the older segment's V scaled inside the attention
+        vllm = self.contract == "vllm"
+        epi = dict(rounding="vllm", ring_v_mul=self._ring_v_mul[layer_index]) if vllm else {}
+        out_scale = vs if vllm else None
+        if vllm:
+            vs = None
         top = layer_index == P.num_layers - 1
         ring_tab = self._ring_table[layer_index]
         pos, older_len, local_len, local_start = self._meta
@@ -409,10 +439,10 @@ class LastKVFastPath:
                 cos, sin, num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=qn_w, k_norm_weight=kn_w, eps=eps,
                 positions=pos[:B], ring=P.pool, ring_table=ring_tab[:B], ring_tokens=P.ring_tokens,
                 deep=P.pool if top else None, deep_table=self._older_table[:B] if top else None,
-                q_out=self._q_out[:T].view(B, n, Hq, 128))
+                q_out=self._q_out[:T].view(B, n, Hq, 128), **epi)
             seg = dict(older=P.pool, older_table=self._older_table[:B], older_len=older_len[:B], vscale=vs, local=P.pool,
                        local_table=ring_tab[:B], local_ring_blocks=P.ring_blocks, local_len=local_len[:B],
-                       local_start=local_start[:B])
+                       local_start=local_start[:B], out_scale=out_scale)
             if n == 1:
                 ops.decode_attention(q_out.view(B, Hq, 128), out=output[:T].view(B, Hq, 128), num_splits=self.splits,
                                      workspace=self._decode_ws, **seg)
@@ -432,11 +462,11 @@ class LastKVFastPath:
                 cos, sin, num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=qn_w, k_norm_weight=kn_w, eps=eps,
                 positions=r.position, ring=P.pool, ring_table=ring_tab[b:b + 1], ring_tokens=P.ring_tokens,
                 deep=P.pool if top else None, deep_table=self._older_table[b:b + 1] if top else None,
-                q_out=self._q_out[sl].view(1, n, Hq, 128))
+                q_out=self._q_out[sl].view(1, n, Hq, 128), **epi)
             width = max(1, -(-r.older // BLOCK))
             seg = dict(older=P.pool, older_table=self._older_table[b:b + 1, :width], older_len=r.older, vscale=vs,
                        local=P.pool, local_table=ring_tab[b:b + 1], local_ring_blocks=P.ring_blocks, local_len=r.local,
-                       local_start=r.older % P.ring_tokens)
+                       local_start=r.older % P.ring_tokens, out_scale=out_scale)
             if n == 1:
                 ops.decode_attention(q_out.view(1, Hq, 128), out=output[sl].view(1, Hq, 128), num_splits=self._row_splits[b],
                                      workspace=self._decode_ws, **seg)
@@ -455,7 +485,7 @@ class LastKVServingModel:
     own torch modules applied to the step's ``[T, hidden]`` rows."""
 
     def __init__(self, model, *, max_batch: int, max_tokens_per_slot: int, source_pages: int | None = None,
-                 num_splits: int | None = None, device=None):
+                 num_splits: int | None = None, device=None, contract: str = "hf"):
         self.model = model
         inner = model.model
         cfg = inner.config
@@ -467,7 +497,8 @@ class LastKVServingModel:
                                    chunk_size=cfg.chunk_size, max_slots=max_batch,
                                    source_pages=source_pages or max_batch * per_slot,
                                    max_tokens_per_slot=max_tokens_per_slot, device=device)
-        self.fast = LastKVFastPath.from_model(model, self.pool, max_batch=max_batch, num_splits=num_splits)
+        self.fast = LastKVFastPath.from_model(model, self.pool, max_batch=max_batch, num_splits=num_splits,
+                                              contract=contract)
         self.config = cfg
 
     def add_sequence(self) -> int:

@@ -42,19 +42,23 @@ def decode_attention(q: Tensor, older_k: Optional[Tensor], older_v: Optional[Ten
                      older_len_const: int, older_table: Optional[Tensor], vscale: Optional[Tensor],
                      local_k: Optional[Tensor], local_v: Optional[Tensor], local_len: Optional[Tensor],
                      local_len_const: int, local_start: Optional[Tensor], local_start_const: int,
-                     local_table: Optional[Tensor], local_ring_blocks: int, sm_scale: float, num_splits: int) -> Tensor:
-    """``lkv_decode_attn``: q ``[B, Hq, 128]`` -> out ``[B, Hq, 128]`` over [older | local]."""
+                     local_table: Optional[Tensor], local_ring_blocks: int, sm_scale: float, num_splits: int,
+                     out_scale: Optional[Tensor] = None) -> Tensor:
+    """``lkv_decode_attn``: q ``[B, Hq, 128]`` -> out ``[B, Hq, 128]`` over [older | local]
+    (``out_scale`` [Hkv]: out = bf16(bf16(o) * s), the vLLM path's output rescale)."""
 
     return ops.decode_attention(
         q, older=_seg(older_k, older_v, older_table), older_len=_len(older_len, older_len_const), vscale=vscale,
         local=_seg(local_k, local_v, local_table), local_len=_len(local_len, local_len_const),
         local_start=_len(local_start, local_start_const), older_table=older_table, local_table=local_table,
-        local_ring_blocks=local_ring_blocks or None, sm_scale=sm_scale or None, num_splits=num_splits or None)
+        local_ring_blocks=local_ring_blocks or None, sm_scale=sm_scale or None, num_splits=num_splits or None,
+        out_scale=out_scale)
 
 
 @decode_attention.register_fake
 def _(q, older_k, older_v, older_len, older_len_const, older_table, vscale, local_k, local_v, local_len,
-      local_len_const, local_start, local_start_const, local_table, local_ring_blocks, sm_scale, num_splits):
+      local_len_const, local_start, local_start_const, local_table, local_ring_blocks, sm_scale, num_splits,
+      out_scale=None):
     return q.new_empty((q.shape[0], q.shape[1], ops.HEAD_DIM))
 
 
@@ -63,7 +67,8 @@ def prefill_attention(q: Tensor, older_k: Optional[Tensor], older_v: Optional[Te
                       older_len_const: int, older_table: Optional[Tensor], vscale: Optional[Tensor],
                       local_k: Optional[Tensor], local_v: Optional[Tensor], local_len: Optional[Tensor],
                       local_len_const: int, local_start: Optional[Tensor], local_start_const: int,
-                      local_table: Optional[Tensor], local_ring_blocks: int, causal: bool, sm_scale: float) -> Tensor:
+                      local_table: Optional[Tensor], local_ring_blocks: int, causal: bool, sm_scale: float,
+                      out_scale: Optional[Tensor] = None) -> Tensor:
     """``lkv_prefill_attn``: q ``[B, L, Hq, 128]`` (the last L tokens of the local segment) ->
     out ``[B, L, Hq, 128]``; bottom-right causal over the local segment when ``causal``."""
 
@@ -71,12 +76,13 @@ def prefill_attention(q: Tensor, older_k: Optional[Tensor], older_v: Optional[Te
         q, older=_seg(older_k, older_v, older_table), older_len=_len(older_len, older_len_const), vscale=vscale,
         local=_seg(local_k, local_v, local_table), local_len=_len(local_len, local_len_const),
         local_start=_len(local_start, local_start_const), older_table=older_table, local_table=local_table,
-        local_ring_blocks=local_ring_blocks or None, causal=causal, sm_scale=sm_scale or None)
+        local_ring_blocks=local_ring_blocks or None, causal=causal, sm_scale=sm_scale or None, out_scale=out_scale)
 
 
 @prefill_attention.register_fake
 def _(q, older_k, older_v, older_len, older_len_const, older_table, vscale, local_k, local_v, local_len,
-      local_len_const, local_start, local_start_const, local_table, local_ring_blocks, causal, sm_scale):
+      local_len_const, local_start, local_start_const, local_table, local_ring_blocks, causal, sm_scale,
+      out_scale=None):
     return q.new_empty(q.shape)
 
 
@@ -101,20 +107,23 @@ def qkv_epilogue(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, num_
                  q_norm_weight: Optional[Tensor], k_norm_weight: Optional[Tensor], eps: float,
                  positions: Optional[Tensor], positions_const: int, q_out: Tensor, ring_k: Tensor, ring_v: Tensor,
                  ring_table: Optional[Tensor], ring_tokens: int, deep_k: Optional[Tensor], deep_v: Optional[Tensor],
-                 deep_table: Optional[Tensor]) -> None:
+                 deep_table: Optional[Tensor], rounding: int = 0, ring_v_mul: Optional[Tensor] = None) -> None:
     """``lkv_qkv_epilogue``: RoPE + q/k RMSNorm, q written to ``q_out`` ``[B, L, Hq, 128]``, K/V
-    appended to the ring (and to the shared cache ``deep_*`` when given) at ``positions + i``."""
+    appended to the ring (and to the shared cache ``deep_*`` when given) at ``positions + i``;
+    ``rounding`` 0 = the HF torch op order, 1 = the vLLM fused_qkv order; ``ring_v_mul`` [Hkv]
+    scales the ring's V (the vLLM path's V / s rings)."""
 
     ops.qkv_epilogue(q, k, v, cos, sin, num_q_heads=num_q_heads, num_kv_heads=num_kv_heads,
                      q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight, eps=eps,
                      positions=_len(positions, positions_const), ring=_seg(ring_k, ring_v, ring_table),
                      deep=_seg(deep_k, deep_v, deep_table), q_out=q_out, ring_table=ring_table,
-                     ring_tokens=ring_tokens or None, deep_table=deep_table)
+                     ring_tokens=ring_tokens or None, deep_table=deep_table,
+                     rounding={v: k for k, v in ops.ROUNDINGS.items()}[rounding], ring_v_mul=ring_v_mul)
 
 
 @qkv_epilogue.register_fake
 def _(q, k, v, cos, sin, num_q_heads, num_kv_heads, q_norm_weight, k_norm_weight, eps, positions, positions_const,
-      q_out, ring_k, ring_v, ring_table, ring_tokens, deep_k, deep_v, deep_table):
+      q_out, ring_k, ring_v, ring_table, ring_tokens, deep_k, deep_v, deep_table, rounding=0, ring_v_mul=None):
     return None
 
 

@@ -15,6 +15,9 @@ Modules:
                      eager transcription of the reference's own test (test_llm_inference.py:39-93)
   wan             -- the Wan video model's shared-history cache, previous-block blend and
                      bidirectional block attention (videogen/.../cache.py, model.py:153-272)
+  vllm_path       -- the reference's vLLM serving-path rounding contract: the fused QKV kernel's
+                     single-FMA rotary and RMSNorm summation order, V / s rings, the output
+                     rescale and the merged per-layer op sequence (fused_qkv.py, fastpath.py:619-651)
 
 Each function cites the reference file:line it restates; how each is pinned is stated in the
 function's docstring ("pinned by: ...").

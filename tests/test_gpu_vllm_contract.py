@@ -1,0 +1,281 @@
+"""GPU parity of the vLLM serving-path rounding contract (oracle/vllm_path.py).
+
+1. ``lkv_qkv_epilogue`` with ``rounding = vllm`` against the oracle's restatement of the reference's
+   fused QKV kernel (fused_qkv.py:24-91), bit for bit: normalised queries, ring K, ring V as
+   bf16(v * fp32(1 / s)), raw shared K / V; per-token and block forms, norms on and off.
+2. ``out_scale`` of the decode and prefill kernels: bf16(bf16(o) * s) of the unscaled call, bit for bit
+   (decode with one and several splits, the tile kernel and short calls on the decode kernel).
+3. ``LastKVFastPath(contract="vllm")`` over ragged steps that cross chunk boundaries against the
+   oracle's merged path (``MergedSequence``): ring and shared pages bit-exact (V / s rings, raw
+   shared V, blends in the V / s domain), outputs within max-abs 2e-2 and rel-L2 1e-3.
+4. The serving model on the vLLM contract: HIP-graph decode replays equal eager steps and stay
+   close to the HF-contract path's logits; ragged prefill + decode logits no further from the fp32
+   reference model than the reference's own bf16 path (the two contracts are the same model in
+   exact arithmetic).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from lastkv_amd import ops
+from lastkv_amd.serving import LastKVFastPath, LastKVPagePool, LastKVServingModel
+from oracle import attention as A
+from oracle import bf16
+from oracle import layout as LY
+from oracle import vllm_path as VP
+
+from test_gpu_llm import _no_worse_than_reference_bf16, _o16, _o32, _tiny
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+MAX_ABS = 2e-2
+REL_L2 = 1e-3
+
+
+def _bf(rng, shape, scale=1.0):
+    return bf16.round_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def _t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV, torch.bfloat16)
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _rotary_np(pos):
+    inv = 1.0 / (10000.0 ** (np.arange(0, 128, 2) / 128))
+    f = np.asarray(pos, np.float64)[..., None] * inv
+    return bf16.round_bf16(np.cos(f).astype(np.float32)), bf16.round_bf16(np.sin(f).astype(np.float32))
+
+
+def _rotary(positions: torch.Tensor):
+    """HF-style bf16 tables [.., 128] (halves repeated) of the same angles as ``_rotary_np``."""
+
+    c, s = _rotary_np(positions.cpu().numpy())
+    return _t(np.concatenate([c, c], -1)), _t(np.concatenate([s, s], -1))
+
+
+@pytest.mark.parametrize("L", [1, 3, 15, 16, 45])
+@pytest.mark.parametrize("norms", [True, False])
+def test_epilogue_vllm_rounding_bit_exact(L, norms):
+    rng = np.random.default_rng(100 + L)
+    B, Hq, Hkv, p0 = 2, 8, 2, 37
+    q, k, v = _bf(rng, (B, L, Hq, 128), 2.0), _bf(rng, (B, L, Hkv, 128), 2.0), _bf(rng, (B, L, Hkv, 128), 2.0)
+    c, s = _rotary_np(p0 + np.arange(L))
+    qw = bf16.round_bf16((rng.random(128) + 0.5).astype(np.float32)) if norms else None
+    kw = bf16.round_bf16((rng.random(128) + 0.5).astype(np.float32)) if norms else None
+    scale = bf16.round_bf16(rng.uniform(0.3, 1.7, Hkv).astype(np.float32))
+    inv = VP.inv_scale(scale)
+    ring = ops.TiledKV.zeros(B, Hkv, 128, DEV)
+    deep = ops.TiledKV.zeros(B, Hkv, 128, DEV)
+    cos = _t(np.concatenate([c, c], -1))[None]
+    sin = _t(np.concatenate([s, s], -1))[None]
+    q_out = ops.qkv_epilogue(_t(q.reshape(B, L, -1)), _t(k.reshape(B, L, -1)), _t(v.reshape(B, L, -1)), cos, sin,
+                             num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=_t(qw) if norms else None,
+                             k_norm_weight=_t(kw) if norms else None, eps=1e-5, positions=p0, ring=ring, deep=deep,
+                             rounding="vllm", ring_v_mul=torch.from_numpy(inv).to(DEV))
+    torch.cuda.synchronize()
+    cq, sq = c[None, :, None], s[None, :, None]
+    want_q = VP.rope_rms(q, cq, sq, qw, 1e-5)
+    want_k = VP.rope_rms(k, cq, sq, kw, 1e-5)
+    assert np.array_equal(_np(q_out), want_q), f"q L={L}"
+    rk, rv = ops.unpack_kv(ring, p0, L)
+    dk, dv = ops.unpack_kv(deep, p0, L)
+    assert np.array_equal(_np(rk), want_k.transpose(0, 2, 1, 3)), f"ring K L={L}"
+    assert np.array_equal(_np(dk), want_k.transpose(0, 2, 1, 3)), f"deep K L={L}"
+    assert np.array_equal(_np(rv), VP.ring_value(v, inv).transpose(0, 2, 1, 3)), f"ring V / s L={L}"
+    assert np.array_equal(_np(dv), v.transpose(0, 2, 1, 3)), f"deep raw V L={L}"
+    # the two contracts differ (other rounding points), the torch-order call leaves the ring V raw
+    ring2 = ops.TiledKV.zeros(B, Hkv, 128, DEV)
+    q2 = ops.qkv_epilogue(_t(q.reshape(B, L, -1)), _t(k.reshape(B, L, -1)), _t(v.reshape(B, L, -1)), cos, sin,
+                          num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=_t(qw) if norms else None,
+                          k_norm_weight=_t(kw) if norms else None, eps=1e-5, positions=p0, ring=ring2)
+    assert not torch.equal(q2, q_out)
+    assert np.array_equal(_np(ops.unpack_kv(ring2, p0, L)[1]), v.transpose(0, 2, 1, 3))
+
+
+def _history_caches(rng, B, Hkv, older_len, local_len):
+    older = ops.TiledKV.zeros(B, Hkv, max(32, -(-older_len // 32) * 32), DEV)
+    if older_len:
+        ops.pack_kv(_t(_bf(rng, (B, Hkv, older_len, 128))), _t(_bf(rng, (B, Hkv, older_len, 128))), older)
+    ring = ops.TiledKV.zeros(B, Hkv, -(-local_len // 32) * 32, DEV)
+    ops.pack_kv(_t(_bf(rng, (B, Hkv, local_len, 128))), _t(_bf(rng, (B, Hkv, local_len, 128))), ring)
+    return older, ring
+
+
+@pytest.mark.parametrize("splits", [1, 3])
+def test_decode_out_scale_is_rounded_rescale(splits):
+    rng = np.random.default_rng(7)
+    B, Hq, Hkv = 3, 16, 4
+    older, ring = _history_caches(rng, B, Hkv, 300, 70)
+    q = _t(_bf(rng, (B, Hq, 128)))
+    s = torch.from_numpy(bf16.round_bf16(rng.uniform(0.3, 1.7, Hkv).astype(np.float32))).to(DEV)
+    seg = dict(older=older, older_len=300, local=ring, local_len=70, num_splits=splits)
+    plain = ops.decode_attention(q, **seg)
+    scaled = ops.decode_attention(q, out_scale=s, **seg)
+    want = (plain.float() * s.repeat_interleave(Hq // Hkv)[None, :, None]).bfloat16()
+    assert torch.equal(scaled, want)
+
+
+@pytest.mark.parametrize("L,tile_waves", [(4, 0), (40, 0), (40, 4), (200, 8)])
+def test_prefill_out_scale_is_rounded_rescale(L, tile_waves):
+    rng = np.random.default_rng(8 + L)
+    B, Hq, Hkv = 2, 8, 2
+    older, ring = _history_caches(rng, B, Hkv, 96, L + 20)
+    q = _t(_bf(rng, (B, L, Hq, 128)))
+    s = torch.from_numpy(bf16.round_bf16(rng.uniform(0.3, 1.7, Hkv).astype(np.float32))).to(DEV)
+    seg = dict(older=older, older_len=96, local=ring, local_len=L + 20, causal=True, tile_waves=tile_waves)
+    plain = ops.prefill_attention(q, **seg)
+    scaled = ops.prefill_attention(q, out_scale=s, **seg)
+    want = (plain.float() * s.repeat_interleave(Hq // Hkv)[None, None, :, None]).bfloat16()
+    assert torch.equal(scaled, want)
+
+
+def _page_tokens(pool: LastKVPagePool, pages: torch.Tensor, first: int, count: int, kind: int, ring: bool):
+    """[Hkv, count, 128] of positions [first, first + count) read from the pool through a page list."""
+
+    arr = (pool.pool.k if kind == 0 else pool.pool.v).float().cpu().numpy()
+    tab = pages.cpu().numpy()
+    out = np.empty((pool.kv_heads, count, 128), np.float32)
+    d = np.arange(128)
+    for i, t in enumerate(range(first, first + count)):
+        slot_tok = t % pool.ring_tokens if ring else t
+        page = tab[slot_tok // 32]
+        off = (LY.k_offset if kind == 0 else LY.v_offset)(slot_tok % 32, d)
+        out[:, i] = arr[:, page, off]
+    return out
+
+
+def test_fast_path_vllm_contract_matches_merged_oracle():
+    rng = np.random.default_rng(9)
+    layers, Hq, Hkv, C, cap = 3, 8, 2, 48, 400
+    params, oparams = [], []
+    for l in range(layers):
+        w = bf16.round_bf16((rng.random(128) + 0.5).astype(np.float32))
+        s = bf16.round_bf16(rng.uniform(0.4, 1.4, Hkv).astype(np.float32))
+        params.append((_t(w), _t(w[::-1]), 1e-5, torch.from_numpy(s).to(DEV)))
+        oparams.append((w, w[::-1].copy(), 1e-5, s))
+    alpha = bf16.round_bf16(rng.random((layers, Hkv)).astype(np.float32))
+    om = bf16.rsub(alpha, 1.0)
+    blend = (torch.from_numpy(alpha.reshape(-1)).to(DEV), torch.from_numpy(om.reshape(-1)).to(DEV),
+             torch.cat([p[3] for p in params]))
+    pool = LastKVPagePool(num_layers=layers, kv_heads=Hkv, chunk_size=C, max_slots=3, source_pages=48,
+                          max_tokens_per_slot=cap, device=DEV)
+    fast = LastKVFastPath(pool, num_q_heads=Hq, layer_params=params, blend=blend, rotary=_rotary, max_batch=4,
+                          num_splits=2, contract="vllm")
+    slots = [fast.add_sequence() for _ in range(2)]
+    seqs = [VP.MergedSequence(layers, Hkv, C, oparams, alpha, _rotary_np) for _ in slots]
+    schedule = [[(0, 48), (1, 20)], [(1, 28), (0, 40)], [(0, 8), (1, 48)], [(0, 1), (1, 1)], [(0, 30), (1, 1)]]
+    schedule += [[(0, 1), (1, 1)]] * 12 + [[(1, 17)], [(0, 3), (1, 2)]]
+    worst = 0.0
+    for step, rows in enumerate(schedule):
+        fast.prepare([(slots[i], n) for i, n in rows])
+        for i, _ in rows:
+            seqs[i].begin_step()
+        T = fast.tokens
+        q = _bf(rng, (T, Hq, 128))
+        k = _bf(rng, (T, Hkv, 128))
+        v = _bf(rng, (T, Hkv, 128))
+        for l in range(layers):
+            out = torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=DEV)
+            fast.run_layer(l, _t(q.reshape(T, -1)), _t(k.reshape(T, -1)), _t(v.reshape(T, -1)), out)
+            got = _np(out)
+            start = 0
+            for i, n in rows:
+                sl = slice(start, start + n)
+                want = seqs[i].layer(l, q[sl], k[sl], v[sl], Hq)
+                ma, rl = A.max_abs(got[sl], want), A.rel_l2(got[sl], want)
+                worst = max(worst, rl)
+                assert ma <= MAX_ABS and rl <= REL_L2, f"step {step} layer {l} seq {i}: max_abs={ma} rel_l2={rl}"
+                start += n
+        for i, n in rows:
+            seqs[i].end_step(n)
+    torch.cuda.synchronize()
+    # cache contents: every layer's live ring window and the shared pages, bit for bit
+    for i, slot in enumerate(slots):
+        seen = fast.seen(slot)
+        rec = max(0, (seen - 1) // C * C - C)
+        for l in range(layers):
+            for kind, ring_ref in ((0, seqs[i].ring_k[l]), (1, seqs[i].ring_v[l])):
+                got = _page_tokens(pool, pool.ring_table[l, slot], rec, seen - rec, kind, ring=True)
+                want = np.stack([ring_ref[t] for t in range(rec, seen)], 1)
+                assert np.array_equal(got, want), f"seq {i} layer {l} ring {'KV'[kind]}"
+        for kind, slab in ((0, seqs[i].slab_k), (1, seqs[i].slab_v)):
+            got = _page_tokens(pool, pool.src_table[slot], 0, seen, kind, ring=False)
+            assert np.array_equal(got, np.stack([slab[t] for t in range(seen)], 1)), f"seq {i} shared {'KV'[kind]}"
+    print(f"{len(schedule)} steps, worst rel_l2 {worst:.2e}", flush=True)
+
+
+def test_serving_model_vllm_contract_graph_and_closeness():
+    oracle, ours = _tiny(chunk=8)
+    prompts = [torch.randint(3, 97, (n,), generator=torch.Generator().manual_seed(40 + n)).to(DEV) for n in (19, 30, 8)]
+    eager = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=96, num_splits=2, contract="vllm")
+    graphed = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=96, num_splits=2, contract="vllm")
+    hf = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=96, num_splits=2)
+    with torch.inference_mode():
+        ids = []
+        for runner in (eager, graphed, hf):
+            slots = [runner.add_sequence() for _ in prompts]
+            nxt = []
+            for slot, p in zip(slots, prompts):
+                fed = 0
+                while fed < p.numel():
+                    take = min(p.numel() - fed, 8 - runner.fast.seen(slot) % 8)
+                    logits = runner.step([(slot, p[fed:fed + take])])
+                    fed += take
+                nxt.append(logits[0].argmax())
+            ids.append((slots, torch.stack(nxt)))
+        (es, etok), (gs, gtok), (hs, htok) = ids
+        graph = graphed.decode_graph(gs)
+        tok_e, tok_g, tok_h = etok, gtok, htok
+        dist_v, dist_h = [], []
+        for step in range(30):
+            le = eager.step([(s, t.view(1)) for s, t in zip(es, tok_e)])
+            lg, tg = graph.step(tok_g)
+            lh = hf.step([(s, t.view(1)) for s, t in zip(hs, tok_e)])
+            assert torch.equal(lg, le), f"graph replay {step}"
+            # the vLLM and HF contracts run the same model with different rounding points
+            ref = le.float()
+            dist_v.append(A.rel_l2(_np(lh), _np(ref)))
+            tok_e, tok_g = le.argmax(-1), tg.clone()
+            assert torch.equal(tok_e, tok_g)
+        print(f"vllm vs hf contract logits rel_l2: median {np.median(dist_v):.2e} max {max(dist_v):.2e}", flush=True)
+        assert max(dist_v) < 0.05
+
+
+def test_serving_model_vllm_contract_ragged_matches_oracle():
+    oracle, ours = _tiny(chunk=8)
+    seqs = [torch.randint(3, 97, (n,), generator=torch.Generator().manual_seed(60 + n)).to(DEV) for n in (37, 22, 50)]
+    runner = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=64, contract="vllm")
+    slots = [runner.add_sequence() for _ in seqs]
+    fed = [0] * len(seqs)
+    got = [[] for _ in seqs]
+    pieces = [5, 3, 8, 1, 8, 2, 7]
+    step = 0
+    with torch.inference_mode():
+        while any(f < len(x) for f, x in zip(fed, seqs)):
+            rows, owners = [], []
+            for i, x in enumerate(seqs):
+                if fed[i] >= len(x):
+                    continue
+                p = runner.fast.seen(slots[i])
+                take = min(len(x) - fed[i], 8 - p % 8, pieces[(step + i) % len(pieces)] if fed[i] < 24 else 1)
+                rows.append((slots[i], x[fed[i]:fed[i] + take]))
+                owners.append((i, fed[i] + take - 1))
+                fed[i] += take
+            logits = runner.step(rows)
+            for (i, pos), row in zip(owners, logits):
+                got[i].append((pos, row.float()))
+            step += 1
+        for i, x in enumerate(seqs):
+            want, _ = _o32(oracle)(x[None])
+            ref16, _ = _o16(oracle)(x[None])
+            pos = [p for p, _ in got[i]]
+            mine = torch.stack([r for _, r in got[i]])[None]
+            _no_worse_than_reference_bf16(mine, want[:, pos].float(), ref16[:, pos].float(),
+                                          f"vLLM-contract serving sequence {i} ({len(pos)} steps)")
