@@ -211,7 +211,8 @@ def test_decode_graph_replays_match_eager_steps():
     assert graphed.fast.seen(sg[0]) == eager.fast.seen(se[0]) == prompts[0].numel() + 40
 
 
-def test_vllm_impl_adapter_runs_the_fast_path():
+@pytest.mark.parametrize("contract", ["hf", "vllm"])
+def test_vllm_impl_adapter_runs_the_fast_path(contract):
     """lastkv_amd.vllm_backend.LastKVAttentionImpl.forward (the reference's Impl contract,
     vllm_backend.py:637-717) over steps prepared on the current fast path: a ragged prefill step,
     a uniform prefill step and padded decode steps crossing a chunk boundary.  vLLM hands it padded
@@ -225,7 +226,7 @@ def test_vllm_impl_adapter_runs_the_fast_path():
     _, ours = _tiny(chunk=8)
     cfg = ours.config
     Hq, Hkv, L = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.num_hidden_layers
-    runner = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=64)
+    runner = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=64, contract=contract)
     fast = runner.fast
     slots = [runner.add_sequence() for _ in range(3)]
     impl = VB.LastKVAttentionImpl(Hq, 128, 128 ** -0.5, Hkv, None, None, "auto")

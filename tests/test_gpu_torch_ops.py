@@ -55,6 +55,16 @@ def test_attention_ops_equal_the_ctypes_calls():
             pool.vp[perm[b, j]] = older.v[b, :, j]
     got = L.decode_attention(q, pool.k, pool.v, None, T0, perm, vs, None, None, None, 0, None, 0, None, 0, 0.0, 0)
     assert torch.equal(got, ops.decode_attention(q, older=older, older_len=T0, vscale=vs))
+    # the vLLM contract's output scale
+    s = (torch.rand(Hkv, generator=g, device=DEV) + 0.5).bfloat16().float()
+    got = L.decode_attention(q, older.k, older.v, None, T0, None, None, ring.k, ring.v, None, n1, None, start, None, 0,
+                             0.0, 0, s)
+    assert torch.equal(got, ops.decode_attention(q, older=older, older_len=T0, local=ring, local_len=n1,
+                                                 local_start=start, out_scale=s))
+    got = L.prefill_attention(qp, older.k, older.v, None, T0, None, None, ring.k, ring.v, None, n1, None, start, None, 0,
+                              True, 0.0, s)
+    assert torch.equal(got, ops.prefill_attention(qp, older=older, older_len=T0, local=ring, local_len=n1,
+                                                  local_start=start, causal=True, out_scale=s))
 
 
 def test_epilogue_merge_norm_ops_equal_the_ctypes_calls():
@@ -73,6 +83,15 @@ def test_epilogue_merge_norm_ops_equal_the_ctypes_calls():
     assert torch.equal(q_outs[0], q_outs[1])
     for a, b in ((rings[0], rings[1]), (deeps[0], deeps[1])):
         assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v)
+    # the vLLM contract: fused-QKV rounding and V / s rings
+    inv = 1.0 / (torch.rand(Hkv, generator=g, device=DEV) + 0.5).bfloat16().float()
+    rings = [ops.TiledKV.zeros(B, Hkv, 64, DEV) for _ in range(2)]
+    ops.qkv_epilogue(q, k, v, cos, sin, num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=w, k_norm_weight=w, eps=1e-6,
+                     positions=5, ring=rings[0], q_out=q_outs[0], rounding="vllm", ring_v_mul=inv)
+    L.qkv_epilogue(q, k, v, cos, sin, Hq, Hkv, w, w, 1e-6, None, 5, q_outs[1], rings[1].k, rings[1].v, None, 0,
+                   None, None, None, 1, inv)
+    assert torch.equal(q_outs[0], q_outs[1])
+    assert torch.equal(rings[0].k, rings[1].k) and torch.equal(rings[0].v, rings[1].v)
     T, H = 33, 8
     o1, o2 = _r(g, (T, H, 128)), _r(g, (T, H, 128))
     l1, l2 = torch.randn((T, H), generator=g, device=DEV), torch.randn((T, H), generator=g, device=DEV)
@@ -113,6 +132,11 @@ def test_opcheck():
     ring2 = ops.TiledKV.zeros(B, Hkv, 32, DEV)
     torch.library.opcheck(L.qkv_epilogue, (qq, kk, vv, cs, cs, Hq, Hkv, None, None, 1e-6, None, 0, q_out, ring2.k,
                                            ring2.v, None, 0, None, None, None))
+    s = torch.full((Hkv,), 0.75, device=DEV)
+    torch.library.opcheck(L.decode_attention, (q, older.k, older.v, None, T0, None, None, None, None, None, 0, None, 0,
+                                               None, 0, 0.0, 0, s))
+    torch.library.opcheck(L.qkv_epilogue, (qq, kk, vv, cs, cs, Hq, Hkv, None, None, 1e-6, None, 0, q_out, ring2.k,
+                                           ring2.v, None, 0, None, None, None, 1, 1.0 / s))
 
 
 def test_compiled_decode_fragment_equals_eager():
