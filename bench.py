@@ -20,6 +20,10 @@ Printed JSON line (one, from this single process):
                  query tokens against [older shared | recent blended | current causal]);
                  algorithmic FLOPs 4*128*Hq*B*sum(unmasked pairs) over the kernel time, against
                  the 2.5 PFLOP/s dense bf16 peak
+  peaks          achievable peaks of this part, measured in the same run (lkv_probe_read: 16-byte
+                 non-temporal loads over 1 GiB; lkv_probe_mfma: independent bf16 MFMA chains on
+                 changing operands); roofline.frac_of_achievable and prefill.frac_of_achievable_mfma
+                 put the kernels against them, beside the nominal-peak fractions
   configs        the other BASELINE configs, measured in the same run:
                  config4_decode_128k  lkv_decode_attn at B=4, 131072-token context (split-K), GB/s
                  config4_prefill_128k the last 4096-token prefill call of the 128K prompt (4 chunk
@@ -72,7 +76,8 @@ def parse_args():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the config 4 (128K decode), config 5 (Wan) and config 3 (8B end to end) measurements")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy decode steps of the config 3 model run")
-    ap.add_argument("--only", choices=["prefill", "short", "config4", "config4p", "config5", "config3", "epilogue"],
+    ap.add_argument("--only", choices=["prefill", "short", "config4", "config4p", "config5", "config3", "epilogue",
+                                       "peaks"],
                     default=None,
                     help="run one secondary measurement alone and print its JSON (for profiling); "
                          "this is not the bench line")
@@ -117,6 +122,43 @@ def prefill_measurement(ops, torch, cache, dev, reps: int = 3) -> dict:
         "workload": "config 3 prefill attention, one layer: 8 x 1024-token chunk pieces, B=32, 8K context",
         "flops_per_layer": flops, "ms_per_layer": round(ms, 3), "achieved_tflops": round(tflops, 1),
         "peak_tflops": MFMA_PEAK_TFLOPS, "mfma_pct": round(100 * tflops / MFMA_PEAK_TFLOPS, 2),
+    }
+
+
+def peaks_measurement(ops, torch, dev, reps: int = 5) -> dict:
+    """Achievable peaks of this part, measured in the same process: lkv_probe_read (16-byte
+    non-temporal loads over 1 GiB, 256 workgroups, the decode kernel's access pattern) and
+    lkv_probe_mfma (independent bf16 16x16x32 MFMA chains on changing pseudo-random operands,
+    two workgroups of 4 waves per CU, the prefill tile's occupancy)."""
+
+    buf = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).normal_()
+    nbytes = buf.numel() * buf.element_size()
+    sink = ops.probe_read(buf)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ops.probe_read(buf, sink=sink)
+    e1.record()
+    torch.cuda.synchronize()
+    read_gbps = nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del buf, sink
+    cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    wgs, iters = 2 * cu, 256
+    sink, flops = ops.probe_mfma(dev, wgs, iters)
+    torch.cuda.synchronize()
+    e0.record()
+    for r in range(reps):
+        ops.probe_mfma(dev, wgs, iters, seed=r + 2, sink=sink)
+    e1.record()
+    torch.cuda.synchronize()
+    mfma_tflops = flops * reps / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    return {
+        "hbm_read_gbps": round(read_gbps, 1), "hbm_read_frac_of_nominal": round(read_gbps / HBM_PEAK_GBS, 4),
+        "mfma_bf16_tflops": round(mfma_tflops, 1), "mfma_frac_of_nominal": round(mfma_tflops / MFMA_PEAK_TFLOPS, 4),
+        "how": "lkv_probe_read: 1 GiB of 16-byte non-temporal loads, 256 workgroups; lkv_probe_mfma: "
+               f"{wgs} workgroups x 4 waves x {iters} rounds of 8 independent 16x16x32 bf16 MFMA chains on "
+               "changing pseudo-random operands; HIP events over 5 launches each",
     }
 
 
@@ -678,6 +720,8 @@ def main() -> int:
             res = wan_measurement(ops, torch, dev)
         elif args.only == "epilogue":
             res = epilogue_measurement(ops, torch, dev)
+        elif args.only == "peaks":
+            res = peaks_measurement(ops, torch, dev)
         else:
             res = e2e_8b_measurement(torch, dev, args.decode_steps)
         print(json.dumps({"only": args.only, **res}), flush=True)
@@ -726,7 +770,10 @@ def main() -> int:
     kernel_ms = statistics.mean(e[0].elapsed_time(e[1]) for ev in events for e in ev)
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     achieved = BYTES_PER_CALL / (kernel_ms * 1e-3) / 1e9
+    peaks = peaks_measurement(ops, torch, dev)
     prefill = None if args.no_prefill else prefill_measurement(ops, torch, cache, dev)
+    if prefill is not None:
+        prefill["frac_of_achievable_mfma"] = round(prefill["achieved_tflops"] / peaks["mfma_bf16_tflops"], 4)
     configs = None
     if not args.no_configs:
         del qs, outs
@@ -777,7 +824,10 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_source,
+            "achievable_peak": peaks["hbm_read_gbps"],
+            "frac_of_achievable": round(achieved / peaks["hbm_read_gbps"], 4),
         },
+        "peaks": peaks,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds),
         "prefill": prefill,
         "configs": configs,

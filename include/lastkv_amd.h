@@ -524,6 +524,23 @@ int32_t lkv_rmsnorm(const lkv_rmsnorm_args *args, lkv_stream_t stream);
 int32_t lkv_silu_mul(const void *gate, int64_t gate_stride, const void *up, int64_t up_stride, void *out,
                      int64_t out_stride, int32_t rows, int32_t width, lkv_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Achievable-peak probes.  No counterpart in the reference: measurement support for the bench,
+ * which reports the kernels' rates against what these reach on the same part, beside the nominal
+ * 8 TB/s and 2.5 PFLOP/s.
+ *   lkv_probe_read: reads `bytes` (a positive multiple of 16, src 16-byte aligned) with 16-byte
+ *     non-temporal loads, 8 in flight per thread, `workgroups` x 256 threads in a grid-stride walk
+ *     (each load instruction of a wave one contiguous 1 KiB run), and writes one word per thread to
+ *     `sink` (workgroups * 256 uint32).
+ *   lkv_probe_mfma: `workgroups` x 4 waves, each running `iters` (a multiple of 8) rounds of 8 independent
+ *     16x16x32 bf16 MFMA chains whose operands change from one MFMA to the next (pseudo-random
+ *     bf16 values of magnitude [0.5, 1) with random signs, from `seed`); workgroups * 4 * iters *
+ *     8 * 16384 FLOP in total; one word per thread to `sink`.
+ * ------------------------------------------------------------------------------------- */
+int32_t lkv_probe_read(const void *src, int64_t bytes, uint32_t *sink, int32_t workgroups, lkv_stream_t stream);
+
+int32_t lkv_probe_mfma(uint32_t *sink, int32_t workgroups, int32_t iters, uint32_t seed, lkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -328,6 +328,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lkv_blend_chunk": (c_i32, [ctypes.POINTER(BlendArgs), c_ptr]),
     "lkv_rmsnorm": (c_i32, [ctypes.POINTER(NormArgs), c_ptr]),
     "lkv_silu_mul": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_i32, c_i32, c_ptr]),
+    "lkv_probe_read": (c_i32, [c_ptr, c_i64, c_ptr, c_i32, c_ptr]),
+    "lkv_probe_mfma": (c_i32, [c_ptr, c_i32, c_i32, ctypes.c_uint32, c_ptr]),
 }
 
 _lock = threading.Lock()

@@ -828,3 +828,36 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = No
     _lib.check(_lib.load().lkv_silu_mul(gate.data_ptr(), gs, up.data_ptr(), us, out.data_ptr(), os_, rows, width,
                                         _stream(gate.device)), "lkv_silu_mul")
     return out
+
+
+PROBE_THREADS = 256
+
+
+def probe_read(src: torch.Tensor, workgroups: int = 256, sink: torch.Tensor | None = None) -> torch.Tensor:
+    """One ``lkv_probe_read`` launch over the bytes of contiguous device tensor ``src`` (16-byte
+    non-temporal loads, the decode kernel's access pattern); returns the sink it wrote."""
+
+    _require(src.is_cuda and src.is_contiguous(), "src must be a contiguous device tensor")
+    nbytes = src.numel() * src.element_size()
+    if sink is None:
+        sink = torch.empty(workgroups * PROBE_THREADS, dtype=torch.int32, device=src.device)
+    _require(sink.numel() >= workgroups * PROBE_THREADS and sink.dtype == torch.int32, "sink too small")
+    lib = _lib.load()
+    _lib.check(lib.lkv_probe_read(src.data_ptr(), nbytes, sink.data_ptr(), workgroups, _stream(src.device)),
+               "lkv_probe_read")
+    return sink
+
+
+def probe_mfma(device: torch.device | str, workgroups: int, iters: int, seed: int = 1,
+               sink: torch.Tensor | None = None) -> tuple[torch.Tensor, int]:
+    """One ``lkv_probe_mfma`` launch (``workgroups`` x 4 waves of independent bf16 MFMA chains on
+    changing operands); returns (sink, FLOPs performed)."""
+
+    device = torch.device(device)
+    if sink is None:
+        sink = torch.empty(workgroups * PROBE_THREADS, dtype=torch.int32, device=device)
+    _require(sink.numel() >= workgroups * PROBE_THREADS and sink.dtype == torch.int32, "sink too small")
+    lib = _lib.load()
+    _lib.check(lib.lkv_probe_mfma(sink.data_ptr(), workgroups, iters, seed & 0xFFFFFFFF, _stream(device)),
+               "lkv_probe_mfma")
+    return sink, workgroups * 4 * iters * 8 * 16 * 16 * 32 * 2
