@@ -301,6 +301,18 @@ def test_8b_full_shape_prompt_logits_no_worse_than_reference_bf16():
     print(f"8B full shape, last prompt position, serving: rel_l2 vs o32 {ours_d:.2e} / o16 {ref_d:.2e}; "
           f"argmax matches {agree} of {B}", flush=True)
     assert ours_d <= 1.5 * ref_d + 1e-3
+    # the serving path on the reference's vLLM rounding contract: the same model in exact arithmetic
+    del runner
+    torch.cuda.empty_cache()
+    runner = LastKVServingModel(ours, max_batch=B, max_tokens_per_slot=P, contract="vllm")
+    slots = [runner.add_sequence() for _ in range(B)]
+    with torch.inference_mode():
+        for s in range(0, P, 1024):
+            served = runner.step([(slot, prompt[b, s:s + 1024]) for b, slot in enumerate(slots)]).float()
+    ours_d = _rel(served, l32[:, -1])
+    print(f"8B full shape, last prompt position, serving (vLLM contract): rel_l2 vs o32 {ours_d:.2e} / o16 {ref_d:.2e}",
+          flush=True)
+    assert ours_d <= 1.5 * ref_d + 1e-3
 
 
 def _decisive_pair(cfg, prompt_len, seed=0):
@@ -364,6 +376,12 @@ def test_8b_geometry_decisive_greedy_ids_identical_64_steps():
             graphed.append(token.clone())
     graphed = torch.stack(graphed, 1).cpu()
     assert torch.equal(graphed, o32), f"graph decode ids differ from o32 at {(graphed != o32).nonzero().tolist()[:8]}"
+    # the serving path on the reference's vLLM rounding contract gives the same 64 ids
+    del runner, graph
+    runner = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=P + 64, contract="vllm")
+    with torch.inference_mode():
+        served = torch.stack([r[P:] for r in runner.generate(list(prompt), 64, prefill_chunk=1024)])
+    assert torch.equal(served, o32), f"vLLM-contract ids differ from o32 at {(served != o32).nonzero().tolist()[:8]}"
 
 
 def test_reference_generate_example_call_sequence(tmp_path):
