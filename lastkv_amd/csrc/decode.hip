@@ -166,7 +166,6 @@ __device__ inline void compute_block(const BlockFrags& f, const BlockRef& r, con
 // the second time normally from L2), so no wave holds more than CG groups of state.
 template <bool kVScale, bool kNT, bool kMulti, int CG = 1, bool kPairs = false>
 __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p) {
-  constexpr int kCols = (kPairs ? 32 : 16) * CG;
   constexpr int kWaveCols = 16 * CG;  // columns one wave holds (a pair's share with kPairs)
   constexpr int kStride = kPairs ? 2 : kWaves;  // block stride of one wave
   // indexed by the column inside the wave's own range: with kPairs each wave pair stages only its
