@@ -477,12 +477,44 @@ class LastKVFastPath:
         return output
 
 
+def fuse_linears(mods) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """One ``[sum(out), in]`` weight (and bias) for ``nn.Linear`` modules that read the same input,
+    as vLLM's ``QKVParallelLinear`` / ``MergedColumnParallelLinear`` hold them: the modules' own
+    parameters are re-pointed to row ranges of the fused tensors (values unchanged, no second
+    copy), so one GEMM produces every module's output as a column range.  Modules already fused
+    this way (an earlier runner over the same model) keep their buffers."""
+
+    mods = list(mods)
+    have = getattr(mods[0], "_lkv_fused", None)
+    if have is not None and len(have[0]) == len(mods) and all(a is b for a, b in zip(have[0], mods)) and all(
+            m.weight.data_ptr() == have[1][r0:].data_ptr() for m, r0 in zip(mods, have[3])):
+        return have[1], have[2]
+    weight = torch.cat([m.weight.detach() for m in mods])
+    with_bias = [m.bias is not None for m in mods]
+    if any(with_bias) and not all(with_bias):
+        raise ValueError("fused projections must all have a bias or none")
+    bias = torch.cat([m.bias.detach() for m in mods]) if all(with_bias) else None
+    r0, starts = 0, []
+    for m in mods:
+        rows = m.weight.shape[0]
+        starts.append(r0)
+        m.weight.data = weight[r0:r0 + rows]
+        if bias is not None:
+            m.bias.data = bias[r0:r0 + rows]
+        r0 += rows
+    mods[0]._lkv_fused = (mods, weight, bias, starts)
+    return weight, bias
+
+
 class LastKVServingModel:
     """Continuous-batching runner of a ``lastkv_amd.llm`` causal LM over a LastKVFastPath: one
     ``step`` runs the decoder over ragged rows (prefill pieces and decode tokens of different
     sequences in one batch), the role of the reference's vLLM model class + backend forward
-    (``vllm_model.py``, ``vllm_backend.py:637-664``).  Projections, norms and MLP are the model's
-    own torch modules applied to the step's ``[T, hidden]`` rows."""
+    (``vllm_model.py``, ``vllm_backend.py:637-664``).  Norms and the MLP's down projection are the
+    model's own modules; q / k / v and gate / up run as one GEMM each over weights fused in place
+    (``fuse_linears``, the layout of vLLM's ``qkv_proj`` / ``gate_up_proj``): at decode (M = 32 rows)
+    hipBLASLt takes ~19 us per projection GEMM whatever its width, so three q / k / v GEMMs cost
+    59 us per layer against 19 us for the fused one."""
 
     def __init__(self, model, *, max_batch: int, max_tokens_per_slot: int, source_pages: int | None = None,
                  num_splits: int | None = None, device=None, contract: str = "hf"):
@@ -500,6 +532,8 @@ class LastKVServingModel:
         self.fast = LastKVFastPath.from_model(model, self.pool, max_batch=max_batch, num_splits=num_splits,
                                               contract=contract)
         self.config = cfg
+        self._qkv = [fuse_linears((l.self_attn.q_proj, l.self_attn.k_proj, l.self_attn.v_proj)) for l in inner.layers]
+        self._gate_up = [fuse_linears((l.mlp.gate_proj, l.mlp.up_proj)) for l in inner.layers]
 
     def add_sequence(self) -> int:
         return self.fast.add_sequence()
@@ -533,13 +567,18 @@ class LastKVServingModel:
         hidden = inner.embed_tokens(ids)  # the residual stream, updated in place
         Hq = self.config.num_attention_heads
         out = torch.empty((T, Hq, ops.HEAD_DIM), dtype=hidden.dtype, device=hidden.device)
+        widths = [Hq * ops.HEAD_DIM, self.config.num_key_value_heads * ops.HEAD_DIM]
+        widths.append(widths[1])
+        inter = self.config.intermediate_size
         h = ops.rmsnorm(hidden, layers[0].input_layernorm.weight, eps)
         for i, layer in enumerate(layers):
             att, mlp = layer.self_attn, layer.mlp
-            self.fast.run_layer(i, att.q_proj(h), att.k_proj(h), att.v_proj(h), out)
+            q, k, v = torch.nn.functional.linear(h, *self._qkv[i]).split(widths, dim=-1)
+            self.fast.run_layer(i, q, k, v, out)
             h = ops.rmsnorm(att.o_proj(out.view(T, Hq * ops.HEAD_DIM)), layer.post_attention_layernorm.weight, eps,
                             residual=hidden)
-            m = mlp.down_proj(ops.silu_mul(mlp.gate_proj(h), mlp.up_proj(h)))
+            gate_up = torch.nn.functional.linear(h, *self._gate_up[i])
+            m = mlp.down_proj(ops.silu_mul(gate_up[:, :inter], gate_up[:, inter:]))
             nxt = layers[i + 1].input_layernorm.weight if i + 1 < len(layers) else inner.norm.weight
             h = ops.rmsnorm(m, nxt, eps, residual=hidden)
         return h
