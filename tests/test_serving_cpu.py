@@ -72,3 +72,31 @@ def test_page_allocator_random_workload():
         for s, n in length.items():
             assert al.used[s] == -(-n // 32)
             assert (al.table[s, al.used[s]:] == scratch).all()
+
+
+def test_fuse_linears_aliases_weights_in_place():
+    """One fused [sum(out), in] weight / bias whose row ranges are the modules' own parameters:
+    same values, no copy, reused by a second call, written through by load_state_dict."""
+
+    import torch
+
+    from lastkv_amd.serving import fuse_linears
+
+    torch.manual_seed(3)
+    mods = [torch.nn.Linear(16, n, bias=True) for n in (8, 4, 4)]
+    before = [(m.weight.detach().clone(), m.bias.detach().clone()) for m in mods]
+    x = torch.randn(5, 16)
+    want = torch.cat([m(x) for m in mods], dim=-1).detach()
+    w, b = fuse_linears(mods)
+    assert w.shape == (16, 16) and b.shape == (16,)
+    for m, (w0, b0), r0 in zip(mods, before, (0, 8, 12)):
+        assert torch.equal(m.weight, w0) and torch.equal(m.bias, b0)
+        assert m.weight.data_ptr() == w[r0:].data_ptr() and m.bias.data_ptr() == b[r0:].data_ptr()
+    torch.testing.assert_close(torch.nn.functional.linear(x, w, b), want, rtol=0, atol=1e-6)
+    w2, b2 = fuse_linears(mods)
+    assert w2 is w and b2 is b
+    mods[1].load_state_dict({"weight": before[1][0] * 2, "bias": before[1][1] * 2})
+    assert torch.equal(w[8:12], before[1][0] * 2) and torch.equal(b[8:12], before[1][1] * 2)
+    mixed = [torch.nn.Linear(16, 4, bias=True), torch.nn.Linear(16, 4, bias=False)]
+    with pytest.raises(ValueError, match="bias"):
+        fuse_linears(mixed)
