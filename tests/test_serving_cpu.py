@@ -1,6 +1,7 @@
 """Host logic of the serving path on the CPU: the per-row segment plan against the oracle's
 region plan (itself pinned by enumeration against the reference test's cache invariants), and the
-page allocator's bookkeeping under a random open / grow / close workload."""
+page allocator's bookkeeping under a random open / grow / close workload, and the serving model's
+fused projection weights."""
 
 from __future__ import annotations
 
