@@ -245,6 +245,9 @@ __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
   }
 }
 
+constexpr int kTileRing = 4;       // LDS block buffers of the tile kernel
+constexpr int kTileBuf = 1024;     // uint4 per block buffer (16 KiB)
+
 // Workgroup = NW waves x 16 * CG query rows (CG 16-column groups per wave).  K (bf16, from the caches)
 // and V (fp16, from the pre-pass) blocks go through a ring of kRing LDS buffers; two register
 // stage sets keep the global loads two steps ahead of their LDS store.  Step i (block i in
@@ -253,23 +256,21 @@ __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
 // (i + 2) % 4, load block i + 4, one barrier.
 // The 2-wave instance (calls of at most 64 query rows per kv head, bound by HBM, not by the matrix
 // pipe) splits P into fp16 hi + lo and runs P V twice, so its probabilities carry ~22 bits
-// instead of 11.
-template <int NW, int CG, int WPE, bool kPaged>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_kernel(
-    const PrefillParams p) {
+// instead of 11.  prefill_tile runs one query tile (logical index = (sequence, kv head, tile)).
+template <int NW, int CG, bool kPaged>
+__device__ __attribute__((always_inline)) inline void prefill_tile(const PrefillParams& p, const int logical,
+                                                                   uint4* lds) {
   constexpr bool kSplitP = NW == 2;
   constexpr int kStages = 2;  // register stage sets (global loads run kStages steps ahead of their LDS store)
   constexpr int kDist = 2;    // step i stores block i + kDist into the LDS ring
-  constexpr int kRing = 4;
-  constexpr int kBuf = 1024;  // uint4 per block buffer (16 KiB)
-  __shared__ uint4 lds[kRing * kBuf];
+  constexpr int kRing = kTileRing;
+  constexpr int kBuf = kTileBuf;
   constexpr int kRowsPerWave = 16 * CG;
   constexpr int kRowsPerWg = NW * kRowsPerWave;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
-  const int logical = xcd_logical_index(blockIdx.x, gridDim.x);
   const int tile = logical % p.tiles;
   const int kvh = (logical / p.tiles) % p.hkv;
   const int b = logical / (p.tiles * p.hkv);
@@ -523,6 +524,20 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
             lt > 0.f ? (rs[cg].mc + __log2f(lt)) * kLn2 : kNegInf;
     }
   }
+}
+
+// One workgroup per query tile.  Workgroup ids map to tiles so that the tiles of one (sequence, kv
+// head) run on one XCD; in causal calls a tile's key count grows with its index, and the tiles are
+// dispatched longest first (largest index first), which shortens the tail of the last workgroups
+// (config-3 chunk pieces: 41.9 -> 43.1 % of the MFMA peak in a same-box A/B; the bidirectional Wan
+// block's tiles are all alike and keep their order).
+template <int NW, int CG, int WPE, bool kPaged>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_kernel(
+    const PrefillParams p) {
+  __shared__ uint4 lds[kTileRing * kTileBuf];
+  const int logical = xcd_logical_index(blockIdx.x, gridDim.x);
+  const int tile = logical % p.tiles;
+  prefill_tile<NW, CG, kPaged>(p, logical - tile + (p.causal ? p.tiles - 1 - tile : tile), lds);
 }
 
 }  // namespace
