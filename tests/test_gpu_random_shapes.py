@@ -10,9 +10,12 @@ sweep covers 300 shapes in six tests of 50 (``pytest -x`` stops at the first fai
 seeds 5039, 5049, 5114, 5139 and 5227 are the shapes on which the 2-wave tile instance exceeded
 rel-L2 1e-3 (1.02-1.08e-3) before it split P, kept as named regression cases.  A second sweep
 draws wide calls (65-600 query rows per kv head, up to 3K keys) on the default tile path and
-reports its worst margin.  Decode runs through one and several key splits."""
+reports its worst margin.  Decode runs through one and several key splits.  An opt-in long sweep
+(LKV_LONG_SWEEP=1) runs 2,000 more shapes and 100 wide calls through every tile choice."""
 
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -142,3 +145,29 @@ def test_random_decode_shapes_match_oracle(seed):
         out = ops.decode_attention(_t(q), num_splits=splits, lse=lse, **seg)
         _check(out, bf16.round_bf16(want[:, :, 0].astype(np.float32)), f"{label} splits={splits}", f"decode-s{splits}")
         np.testing.assert_allclose(lse.cpu().numpy(), want_lse[:, :, 0], rtol=1e-4, atol=1e-4)
+
+
+LONG_SWEEP_SEED0 = 20000
+LONG_SWEEP_SHAPES = 2000
+LONG_WIDE_SEED0 = 3000
+LONG_WIDE_SHAPES = 100
+
+
+@pytest.mark.skipif(os.environ.get("LKV_LONG_SWEEP") != "1", reason="long sweep (~2 minutes): set LKV_LONG_SWEEP=1")
+def test_long_random_prefill_sweep():
+    """2,000 more shapes of the same generator (automatic choice and tile_waves 4 and 8) and 100 wide
+    calls through all three tile choices: every call within the bar; prints the worst rel-L2 per
+    kernel path (the figures quoted for the tiles' margin)."""
+
+    for seed in range(LONG_SWEEP_SEED0, LONG_SWEEP_SEED0 + LONG_SWEEP_SHAPES):
+        _prefill_case(seed)
+    for seed in range(LONG_WIDE_SEED0, LONG_WIDE_SEED0 + LONG_WIDE_SHAPES):
+        rng, B, Hkv, G, L, T0, ring_blocks, n1, start, causal = _wide_case(seed)
+        seg, k, v = _two_segments(rng, B, Hkv, T0=max(T0, 1), n1=n1, start=start, ring_blocks=ring_blocks)
+        q = _bf(rng, (B, L, G * Hkv, 128))
+        want, _ = A.attention(q.transpose(0, 2, 1, 3), k, v, causal_bottom_right=causal)
+        want_out = bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32))
+        for tw in (0, 4, 8):
+            out = ops.prefill_attention(_t(q), causal=causal, tile_waves=tw, **seg)
+            _check(out, want_out, f"wide seed {seed} tile_waves={tw}", f"wide-tw{tw}")
+    print("worst rel_l2 by kernel: " + ", ".join(f"{k} {v:.3e}" for k, v in sorted(_worst.items())), flush=True)
