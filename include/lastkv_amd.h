@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 8
+#define LKV_ABI_VERSION 9
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -251,11 +251,30 @@ typedef struct lkv_prefill_args {
   int32_t tile_waves;
   /* Optional output scale, fp32 [Hkv] (bf16-valued) or NULL, as in lkv_decode_args. */
   const float *out_scale;
+  /* Optional ragged query rows (varlen; the cu_seqlens_q / max_seqlen_q of the FlashAttention varlen
+   * call the serving fast path makes for mixed prefill + decode steps, fastpath.py:643-648).  NULL:
+   * every sequence has `tokens` query tokens, q[b, i] at q + b * q_stride_b + i * q_stride_t.  Else a
+   * device int32 [batch + 1] array, non-decreasing from cu_seqlens_q[0] = 0: sequence b's query
+   * tokens are rows cu_seqlens_q[b] .. cu_seqlens_q[b + 1] - 1 of a [tokens, Hq, 128] q (row t at
+   * q + t * q_stride_t; q_stride_b and out_stride_b are unused; out and lse likewise by row, lse fp32
+   * [tokens, Hq]), `tokens` is the total row count and max_seqlen_q (>= 1) bounds every sequence's
+   * count.  Sequence b's L_b query tokens are the last L_b tokens of its local segment (causal).
+   * Entries are clamped into [0, tokens] and counts to max_seqlen_q, so corrupt offsets cannot
+   * address outside q / out.  With tile_waves 0, sequences of at most 64 query rows per kv head run
+   * on the decode kernel and the others on the tile kernel, in one call. */
+  const int32_t *cu_seqlens_q;
+  int32_t max_seqlen_q;
+  /* Key splits of the sequences that run on the decode kernel (at most 64 query rows per kv head):
+   * 0 chooses them from the grid and the workspace; n in [1, 1024] fixes n (the workspace must then
+   * also hold their split states, which lkv_prefill_workspace_bytes includes), so that a caller
+   * that fixes the split count gets the same arithmetic whatever the batch. */
+  int32_t num_splits;
 } lkv_prefill_args;
 
 /* Workspace bytes lkv_prefill_attn needs for these args: the fp16 V of every key block of every
- * (sequence, kv head), 8 KiB per 32-token block.  Exact when the lengths and the ring start are
- * host constants, else bounded by the capacities.  Takes the same filled-in struct. */
+ * (sequence, kv head), 8 KiB per 32-token block (exact when the lengths and the ring start are
+ * host constants, else bounded by the capacities), or with num_splits > 0 the decode kernel's
+ * split states if those are larger.  Takes the same filled-in struct. */
 int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args *args);
 
 int32_t lkv_prefill_attn(const lkv_prefill_args *args, lkv_stream_t stream);
@@ -346,6 +365,15 @@ typedef struct lkv_qkv_args {
    * rings of V / s with ring_v_mul = fp32(1 / s), fused_qkv.py:84-86); the deep write keeps the
    * raw V (fused_qkv.py:87-90). */
   const float *ring_v_mul;
+  /* Optional ragged rows (the fused QKV kernel's per-token form over a mixed step's flattened rows,
+   * fused_qkv.py:58-126).  NULL: `tokens` new tokens per sequence as above.  Else a device int32
+   * [batch + 1] array, non-decreasing from cu_seqlens[0] = 0: sequence b's new tokens are rows
+   * cu_seqlens[b] .. cu_seqlens[b + 1] - 1 (row t of q, k, v, cos, sin and q_out at t * *_stride_t;
+   * the *_stride_b fields are unused), its token i at position positions[b] + i (or position_const
+   * + i); `tokens` is the total row count and max_seqlen (>= 1) bounds every sequence's count.
+   * Offsets are clamped into [0, tokens] and counts to max_seqlen. */
+  const int32_t *cu_seqlens;
+  int32_t max_seqlen;
 } lkv_qkv_args;
 
 int32_t lkv_qkv_epilogue(const lkv_qkv_args *args, lkv_stream_t stream);

@@ -11,7 +11,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class LastKVNativeError(RuntimeError):
@@ -130,6 +130,9 @@ class PrefillArgs(ctypes.Structure):
         ("local_num_pages", c_i32),
         ("tile_waves", c_i32),
         ("out_scale", c_ptr),
+        ("cu_seqlens_q", c_ptr),
+        ("max_seqlen_q", c_i32),
+        ("num_splits", c_i32),
     ]
 
 
@@ -248,6 +251,8 @@ class QkvArgs(ctypes.Structure):
         ("deep_num_pages", c_i32),
         ("rounding", c_i32),
         ("ring_v_mul", c_ptr),
+        ("cu_seqlens", c_ptr),
+        ("max_seqlen", c_i32),
     ]
 
 

@@ -235,9 +235,11 @@ __device__ inline uint4 scale_frag(uint4 v, float s) {
   return r;
 }
 
-// A prefill call with group * tokens <= 64 query rows per kv head, run on the decode kernel with one
-// score column per (query token, head) (decode.hip).  The arguments have passed lkv_prefill_attn's
-// checks; seg was filled from them.
-int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, hipStream_t s);
+// The sequences of a prefill call with col_lo < group * tokens <= col_hi <= 64 query rows per kv head
+// (tokens: the call's count, or each sequence's own in a ragged call), run on the decode kernel with
+// one score column per (query token, head) (decode.hip).  The arguments have passed
+// lkv_prefill_attn's checks; seg was filled from them.
+int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, int32_t col_lo,
+                                 int32_t col_hi, hipStream_t s);
 
 }  // namespace lkv

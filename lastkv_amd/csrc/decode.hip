@@ -37,10 +37,33 @@ struct DecodeParams {
   const float* out_scale;  // [Hkv] or nullptr: out = bf16(bf16(o) * out_scale[kvh])
   float* ws_o;
   float* ws_ml;
-  int32_t hq, group, splits;
+  int32_t batch, hq, group, splits;
   int32_t L, causal;  // query tokens per sequence (1 for decode calls) and bottom-right causality
   float scale_log2;
+  // ragged query rows (short-prefill calls): sequence b's tokens are rows cu[b] .. cu[b + 1] - 1 of
+  // q / out (nullptr: L tokens per sequence); rows = the call's total row count.  Only sequences
+  // with col_lo < tokens * group <= col_hi run in this launch.
+  const int32_t* cu;
+  int32_t rows, col_lo, col_hi;
 };
+
+// Query tokens of sequence b (kMulti calls) and the flattened row of its token 0 (the q / out / lse
+// / split-state row index is row0 + token).
+struct MultiRows {
+  int L;
+  int64_t row0;
+};
+
+__device__ inline MultiRows multi_rows(const DecodeParams& p, int b) {
+  if (p.cu == nullptr) return MultiRows{p.L, static_cast<int64_t>(b) * p.L};
+  const int s0 = min(max(p.cu[b], 0), p.rows);
+  return MultiRows{min(min(max(p.cu[b + 1], s0), p.rows) - s0, p.L), s0};
+}
+
+__device__ inline bool in_column_class(const DecodeParams& p, int L) {
+  const int cols = L * p.group;
+  return L > 0 && cols > p.col_lo && cols <= p.col_hi;
+}
 
 // The bf16 output of a normalised fp32 value x of kv head kvh: bf16(x), or bf16(bf16(x) * s) with
 // an output scale (the reference rescales its bf16 attention output by s in fp32).
@@ -180,22 +203,29 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = p.group;
 
+  // ragged calls: this sequence's query tokens (workgroup-uniform; sequences of another column
+  // class run in another launch)
+  const MultiRows mr = kMulti ? multi_rows(p, b) : MultiRows{1, b};
+  if (kMulti && !in_column_class(p, mr.L)) return;
+  const int Lq = mr.L;
+
   const SeqView sv = make_seq_view(p.seg, b, kvh);
   const int nbt = sv.nb0 + (sv.n1 > 0 ? (sv.lead + sv.n1 + kBlockTokens - 1) / kBlockTokens : 0);
   const int bps = (nbt + p.splits - 1) / p.splits;
   const int blk_begin = split * bps;
   const int blk_end = min(blk_begin + bps, nbt);
 
-  const int cols = kMulti ? G * p.L : G;
+  const int cols = kMulti ? G * Lq : G;
   uint4 qf[CG][4];
   int lim[CG], lim_min = 0;  // causal limits (local token index) of this lane's columns and of column 0
-  if (kMulti) lim_min = p.causal ? sv.n1 - p.L : sv.n1 - 1;
+  if (kMulti) lim_min = p.causal ? sv.n1 - Lq : sv.n1 - 1;
   const int cg0 = kPairs ? (wave >> 1) * CG : 0;  // this wave's first column group
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
     const int c = 16 * (cg0 + cg) + n16;
     const int t = kMulti ? c / G : 0, h = c - t * G;
-    const uint16_t* qrow = p.q + b * p.q_sb + (kMulti ? t * p.q_st : 0) + static_cast<int64_t>(kvh * G + h) * kHeadDim;
+    const uint16_t* qrow = p.q + (kMulti && p.cu ? mr.row0 * p.q_st : b * p.q_sb) + (kMulti ? t * p.q_st : 0) +
+                           static_cast<int64_t>(kvh * G + h) * kHeadDim;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
       qf[cg][kb] = c < cols ? *reinterpret_cast<const uint4*>(qrow + 32 * kb + 8 * g4) : make_uint4(0, 0, 0, 0);
@@ -282,7 +312,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   for (int idx = threadIdx.x; idx < cols * kHeadDim; idx += 256) {
     const int h = idx >> 7, d = idx & (kHeadDim - 1);  // column h = (token tq, head hh)
     const int tq = kMulti ? h / G : 0, hh = h - tq * G;
-    const int64_t row_q = (static_cast<int64_t>(b) * (kMulti ? p.L : 1) + tq) * p.hq + kvh * G + hh;  // [B, L, Hq] row
+    const int64_t row_q = (mr.row0 + tq) * p.hq + kvh * G + hh;  // [rows, Hq] row
     // the waves that hold column h: all four, or the pair of its column group
     const int pair = kPairs ? h / kWaveCols : 0;
     const int w0 = 2 * pair, hl = h - pair * kWaveCols;  // its waves and its column inside their range
@@ -298,7 +328,8 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
       O += f * sm_o[w][hl][d];
     }
     if (p.splits == 1) {
-      p.out[b * p.out_sb + (kMulti ? tq * p.out_st : 0) + static_cast<int64_t>(kvh * G + hh) * kHeadDim + d] =
+      p.out[(kMulti && p.cu ? mr.row0 * p.out_st : b * p.out_sb) + (kMulti ? tq * p.out_st : 0) +
+            static_cast<int64_t>(kvh * G + hh) * kHeadDim + d] =
           out_bits(L > 0.f ? O / L : 0.f, p.out_scale, kvh);
       if (p.lse != nullptr && d == 0) p.lse[row_q] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
     } else {
@@ -322,9 +353,21 @@ constexpr int kMaxSplits = 1024;
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const DecodeParams p) {
   __shared__ float sm_w[kMaxSplits];
   __shared__ float sm_red[kCombineThreads / 64];
-  const int bh = blockIdx.x;  // [B, L, Hq] row
+  const int bh = blockIdx.x;  // [rows, Hq] row
   const int d = threadIdx.x;
-  const int b = bh / (p.L * p.hq), tq = (bh / p.hq) % p.L, h = bh % p.hq;
+  const int row = bh / p.hq, h = bh % p.hq;
+  int b = row / p.L, tq = row % p.L;
+  if (p.cu != nullptr) {  // ragged: the sequence of this row (largest b with cu[b] <= row)
+    int lo = 0, hi = p.batch;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (p.cu[mid] <= row) lo = mid; else hi = mid;
+    }
+    b = lo;
+    const MultiRows mr = multi_rows(p, b);
+    tq = row - static_cast<int>(mr.row0);
+    if (tq < 0 || tq >= mr.L || !in_column_class(p, mr.L)) return;  // (uniform over the block)
+  }
   const int S = p.splits;
   const float* ml = p.ws_ml + static_cast<int64_t>(bh) * S * 2;
   const float* o = p.ws_o + static_cast<int64_t>(bh) * S * kHeadDim;
@@ -360,7 +403,7 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const D
   }
   for (; s < S; ++s) O[0] += sm_w[s] * o[s * kHeadDim + d];
   const float Ot = (O[0] + O[1]) + (O[2] + O[3]);
-  p.out[b * p.out_sb + tq * p.out_st + static_cast<int64_t>(h) * kHeadDim + d] =
+  p.out[(p.cu ? static_cast<int64_t>(row) * p.out_st : b * p.out_sb + tq * p.out_st) + static_cast<int64_t>(h) * kHeadDim + d] =
       out_bits(L > 0.f ? Ot / L : 0.f, p.out_scale, h / p.group);
   if (p.lse != nullptr && d == 0) p.lse[bh] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
 }
@@ -424,7 +467,8 @@ int32_t launch_decode(const DecodeParams& p, dim3 grid, bool vscale, bool nt, in
 
 }  // namespace
 
-int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, hipStream_t s) {
+int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, int32_t col_lo,
+                                 int32_t col_hi, hipStream_t s) {
   DecodeParams p;
   p.seg = seg;
   p.q = static_cast<const uint16_t*>(a->q);
@@ -436,9 +480,14 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   p.lse = a->lse;
   p.vscale = a->vscale;
   p.out_scale = a->out_scale;
+  p.batch = a->batch;
   p.hq = a->num_q_heads;
   p.group = group;
-  p.L = a->tokens;
+  p.cu = a->cu_seqlens_q;
+  p.rows = a->tokens;
+  p.L = a->cu_seqlens_q ? std::min(a->max_seqlen_q, a->tokens) : a->tokens;
+  p.col_lo = col_lo;
+  p.col_hi = col_hi;
   p.causal = a->causal;
   p.scale_log2 = a->sm_scale * kLog2e;
   const int64_t tokens = call_key_tokens(a);
@@ -447,13 +496,22 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
   // about one workgroup per CU, at least 4 blocks per split, partial states within the workspace
   int64_t splits = std::min<int64_t>({(cus + pairs - 1) / pairs, std::max<int64_t>(blocks / 4, 1), 1024});
-  const int64_t rows = static_cast<int64_t>(a->batch) * a->tokens * a->num_q_heads;
+  // split-state rows: [rows, Hq] for ragged calls, [B, L, Hq] otherwise
+  const int64_t rows = (a->cu_seqlens_q ? static_cast<int64_t>(a->tokens) : static_cast<int64_t>(a->batch) * a->tokens) *
+                       a->num_q_heads;
+  if (a->num_splits > 0) {  // fixed by the caller (lkv_prefill_workspace_bytes counted its states)
+    splits = a->num_splits;
+    if (splits > 1 && rows * splits * (kHeadDim + 2) * 4 > a->workspace_bytes)
+      return fail(LKV_ERR_WORKSPACE, "prefill with %d decode splits needs %lld bytes of workspace, got %lld", a->num_splits,
+                  static_cast<long long>(rows * splits * (kHeadDim + 2) * 4), static_cast<long long>(a->workspace_bytes));
+  }
   while (splits > 1 && rows * splits * (kHeadDim + 2) * 4 > a->workspace_bytes) splits = (splits + 1) / 2;
   p.splits = static_cast<int32_t>(splits);
   p.ws_o = splits > 1 ? static_cast<float*>(a->workspace) : nullptr;
   p.ws_ml = splits > 1 ? p.ws_o + rows * splits * kHeadDim : nullptr;
   const bool nt = use_nontemporal(0, pairs * tokens * kHeadDim * 2 * 2);
-  const int64_t cols = static_cast<int64_t>(group) * a->tokens;
+  // the instance holds the class's widest sequence: 16, 32 or 64 columns
+  const int64_t cols = std::min<int64_t>(col_hi, static_cast<int64_t>(group) * p.L);
   const int cg = cols <= 16 ? 1 : cols <= 32 ? 2 : 4;
   return launch_decode(p, dim3(p.splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1, nt, cg,
                        static_cast<int>(rows), s, "lkv_prefill_attn (short call on the decode kernel)");
@@ -510,6 +568,11 @@ int32_t run_decode(const lkv_decode_args* a, void* ws, int64_t ws_bytes, hipStre
   p.out_st = 0;
   p.L = 1;
   p.causal = 0;
+  p.cu = nullptr;
+  p.rows = a->batch;
+  p.col_lo = 0;
+  p.col_hi = 1 << 30;
+  p.batch = a->batch;
   p.lse = a->lse;
   p.vscale = a->vscale;
   p.out_scale = a->out_scale;

@@ -6,6 +6,8 @@
 // through LDS).  Two rounding contracts: the torch op order of the HF model (every intermediate
 // rounded to bf16 where the reference's bf16 torch ops round) and the vLLM fused_qkv kernel's
 // (fused multiply-adds, one rounding per output, a fixed RMSNorm summation order).
+#include <algorithm>
+
 #include "common.h"
 #include "runtime.h"
 
@@ -50,7 +52,33 @@ struct QkvParams {
   int32_t d_npages;
   int32_t rounding;      // 0: torch op order (HF model), 1: vLLM fused_qkv order
   const float* rv_mul;   // ring V := bf16(v * rv_mul[g]) (the vLLM path's V / s rings), or nullptr
+  // ragged rows: sequence b's tokens are rows cu[b] .. cu[b + 1] - 1 (tokens = the call's total row
+  // count, max_seqlen bounds a sequence's count); nullptr: `tokens` tokens per sequence
+  const int32_t* cu;
+  int32_t max_seqlen;
 };
+
+// First row and token count of sequence b (ragged calls; offsets clamped into [0, tokens]).
+__device__ inline int2 ragged_rows(const QkvParams& p, int b) {
+  const int s0 = min(max(p.cu[b], 0), p.tokens);
+  return make_int2(s0, min(min(max(p.cu[b + 1], s0), p.tokens) - s0, p.max_seqlen));
+}
+
+// Sequence of ragged row t: the largest b with cu[b] <= t.
+__device__ inline int ragged_seq(const QkvParams& p, int t) {
+  int lo = 0, hi = p.batch;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (p.cu[mid] <= t) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// Element offset of token i of sequence b in a tensor with batch / token strides (sb, st); ragged
+// calls address row `row` (= first row of b + i) instead.
+__device__ inline int64_t tok_off(const QkvParams& p, int b, int i, int64_t row, int64_t sb, int64_t st) {
+  return p.cu ? row * st : b * sb + i * st;
+}
 
 // Element offset of block blk of sequence b: contiguous per slot, or a clamped page of a pool.
 __device__ inline int64_t write_block(const int32_t* tab, int64_t tab_stride, int64_t page, int32_t npages, int b,
@@ -93,19 +121,25 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
   const int lane = threadIdx.x & 63;
   const int heads = p.hq + p.hkv;
   const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (item >= static_cast<int64_t>(p.batch) * p.tokens * heads) return;
+  if (item >= (p.cu ? 1 : static_cast<int64_t>(p.batch)) * p.tokens * heads) return;
   const int h = static_cast<int>(item % heads);
-  const int64_t tok = item / heads;
-  const int i = static_cast<int>(tok % p.tokens);
-  const int b = static_cast<int>(tok / p.tokens);
+  const int64_t tok = item / heads;  // (ragged: the row)
+  int i = static_cast<int>(tok % p.tokens);
+  int b = static_cast<int>(tok / p.tokens);
+  if (p.cu) {
+    b = ragged_seq(p, static_cast<int>(tok));
+    const int2 r = ragged_rows(p, b);
+    i = static_cast<int>(tok) - r.x;
+    if (i < 0 || i >= r.y) return;  // a row past a clamped sequence
+  }
   const bool is_q = h < p.hq;
   const int g = h - p.hq;
-  const uint16_t* src = is_q ? p.q + b * p.q_sb + i * p.q_st + static_cast<int64_t>(h) * kHeadDim
-                             : p.k + b * p.k_sb + i * p.k_st + static_cast<int64_t>(g) * kHeadDim;
+  const uint16_t* src = is_q ? p.q + tok_off(p, b, i, tok, p.q_sb, p.q_st) + static_cast<int64_t>(h) * kHeadDim
+                             : p.k + tok_off(p, b, i, tok, p.k_sb, p.k_st) + static_cast<int64_t>(g) * kHeadDim;
   const float x0 = bf16_bits_to_f32(src[lane]);
   const float x1 = bf16_bits_to_f32(src[lane + 64]);
-  const uint16_t* cp = p.cos + b * p.cs_sb + i * p.cs_st;
-  const uint16_t* sp = p.sin + b * p.cs_sb + i * p.cs_st;
+  const uint16_t* cp = p.cos + tok_off(p, b, i, tok, p.cs_sb, p.cs_st);
+  const uint16_t* sp = p.sin + tok_off(p, b, i, tok, p.cs_sb, p.cs_st);
   const float c0 = bf16_bits_to_f32(cp[lane]), c1 = bf16_bits_to_f32(cp[lane + 64]);
   const float s0 = bf16_bits_to_f32(sp[lane]), s1 = bf16_bits_to_f32(sp[lane + 64]);
   const uint16_t* w = is_q ? p.qw : p.kw;
@@ -125,14 +159,14 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
   }
   const uint16_t o0 = f32_to_bf16_bits(r0), o1 = f32_to_bf16_bits(r1);
   if (is_q) {
-    uint16_t* dst = p.q_out + b * p.qo_sb + i * p.qo_st + static_cast<int64_t>(h) * kHeadDim;
+    uint16_t* dst = p.q_out + tok_off(p, b, i, tok, p.qo_sb, p.qo_st) + static_cast<int64_t>(h) * kHeadDim;
     dst[lane] = o0;
     dst[lane + 64] = o1;
     return;
   }
   const int position = (p.pos ? p.pos[b] : p.pos_c) + i;
   if (position < 0) return;
-  const uint16_t* vrow = p.v + b * p.v_sb + i * p.v_st + static_cast<int64_t>(g) * kHeadDim;
+  const uint16_t* vrow = p.v + tok_off(p, b, i, tok, p.v_sb, p.v_st) + static_cast<int64_t>(g) * kHeadDim;
   const uint16_t v0 = vrow[lane], v1 = vrow[lane + 64];
   {
     // the ring's V, scaled for the vLLM path (fp32 product, one rounding); the deep write is raw
@@ -346,8 +380,8 @@ struct QItem {
 __device__ inline void q_item_load(const QkvParams& p, int32_t grp, int32_t groups, int hgroups, int l, QItem& it) {
   grp = grp < groups ? grp : groups - 1;
   const int h0 = grp % hgroups * kQRows;
-  const int tok = grp / hgroups;
-  const int i = tok % p.tokens, b = tok / p.tokens;
+  const int tok = grp / hgroups;  // (ragged: the row; the query rows need no sequence)
+  const int i = p.cu ? tok : tok % p.tokens, b = p.cu ? 0 : tok / p.tokens;
   const uint16_t* qrow = p.q + b * p.q_sb + i * p.q_st;
 #pragma unroll
   for (int r = 0; r < kQRows; ++r)
@@ -361,7 +395,7 @@ __device__ inline void q_item_store(const QkvParams& p, int32_t grp, int32_t gro
   if (grp >= groups) return;
   const int h0 = grp % hgroups * kQRows;
   const int tok = grp / hgroups;
-  const int i = tok % p.tokens, b = tok / p.tokens;
+  const int i = p.cu ? tok : tok % p.tokens, b = p.cu ? 0 : tok / p.tokens;
   uint16_t* dst = p.q_out + b * p.qo_sb + i * p.qo_st + static_cast<int64_t>(h0) * kHeadDim;
   const RopeCS cs = rope_cs(it.ca, it.cb, it.sa, it.sb);
 #pragma unroll
@@ -380,7 +414,7 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
   const int t = threadIdx.x, l = t & (kRowLanes - 1);
   if (static_cast<int>(blockIdx.x) >= kv_wgs) {
     const int hgroups = (p.hq + kQRows - 1) / kQRows;
-    const int32_t groups = p.batch * p.tokens * hgroups;  // < 2^31 (checked by the host)
+    const int32_t groups = (p.cu ? 1 : p.batch) * p.tokens * hgroups;  // < 2^31 (checked by the host)
     const int32_t grp = (static_cast<int32_t>(blockIdx.x) - kv_wgs) * 32 + (t >> 3);
     if (grp >= groups) return;
     const NormW w = norm_weights(p.qw, l);
@@ -393,10 +427,15 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
   const int jr = kv % kv_blocks, g = (kv / kv_blocks) % p.hkv, b = kv / (kv_blocks * p.hkv);
   const int p0 = p.pos ? p.pos[b] : p.pos_c;
   if (p0 < 0) return;  // (uniform over the workgroup)
+  // this sequence's tokens: rows [r0, r0 + n) of a ragged call, else tokens [0, p.tokens)
+  const int2 rr = p.cu ? ragged_rows(p, b) : make_int2(0, p.tokens);
+  const int n = rr.y;
   const int blk = (p0 >> 5) + jr;             // positions [32 blk, 32 blk + 32)
+  if (blk * kBlockTokens >= p0 + n) return;   // past this sequence's tokens (uniform)
   const int w = t >> 3;                       // this thread's token of the block
-  const int i = blk * kBlockTokens + w - p0;  // its index in the call
-  const bool valid = i >= 0 && i < p.tokens;
+  const int i = blk * kBlockTokens + w - p0;  // its index in the sequence
+  const bool valid = i >= 0 && i < n;
+  const int64_t row = static_cast<int64_t>(rr.x) + i;  // (ragged calls)
   const int rslot = p.r_tab ? 0 : (p.ring_slot ? p.ring_slot[b] : b);
   const bool ring_ok = rslot >= 0 && rslot < p.ring_slots;
   const int dslot = p.d_tab ? 0 : (p.deep_slot ? p.deep_slot[b] : b);
@@ -407,10 +446,10 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
   const NormW kw = norm_weights(p.kw, l);
   if (valid) {
     uint4 ka, kb, ca, cb, sa, sb, va, vb;
-    load_row_nt(p.k + b * p.k_sb + i * p.k_st + static_cast<int64_t>(g) * kHeadDim, l, ka, kb);
-    load_row_nt(p.v + b * p.v_sb + i * p.v_st + static_cast<int64_t>(g) * kHeadDim, l, va, vb);
-    load_row(p.cos + b * p.cs_sb + i * p.cs_st, l, ca, cb);
-    load_row(p.sin + b * p.cs_sb + i * p.cs_st, l, sa, sb);
+    load_row_nt(p.k + tok_off(p, b, i, row, p.k_sb, p.k_st) + static_cast<int64_t>(g) * kHeadDim, l, ka, kb);
+    load_row_nt(p.v + tok_off(p, b, i, row, p.v_sb, p.v_st) + static_cast<int64_t>(g) * kHeadDim, l, va, vb);
+    load_row(p.cos + tok_off(p, b, i, row, p.cs_sb, p.cs_st), l, ca, cb);
+    load_row(p.sin + tok_off(p, b, i, row, p.cs_sb, p.cs_st), l, sa, sb);
     rope_norm_row_any(ka, kb, rope_cs(ca, cb, sa, sb), kw, p.eps, p.rounding);
     // dims [8l, 8l + 8) and [64 + 8l, 64 + 8l + 8) of token w are 16 contiguous bytes each in a K tile
     const int ko0 = k_tile_offset(w, 8 * l), ko1 = k_tile_offset(w, 64 + 8 * l);
@@ -433,7 +472,7 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
   __syncthreads();
   // V tile: element (token w, dim d) at d * 32 + w; 512 runs of 8 tokens of one dim.  The ring
   // takes bf16(v * rv_mul[g]) on the vLLM path, the deep store the raw V.
-  const int lo = max(0, p0 - blk * kBlockTokens), hi = min(kBlockTokens, p0 + p.tokens - blk * kBlockTokens);
+  const int lo = max(0, p0 - blk * kBlockTokens), hi = min(kBlockTokens, p0 + n - blk * kBlockTokens);
   const float vm = p.rv_mul != nullptr ? p.rv_mul[g] : 1.f;
 #pragma unroll
   for (int run = t; run < kHeadDim * 4; run += 256) {
@@ -557,7 +596,14 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
   LKV_REQUIRE(a->positions != nullptr || a->position_const >= 0, "negative position");
   LKV_REQUIRE(a->rounding == 0 || a->rounding == 1, "rounding must be 0 (torch op order) or 1 (vLLM fused_qkv), got %d",
               a->rounding);
-  const int64_t items = static_cast<int64_t>(a->batch) * a->tokens * (a->num_q_heads + a->num_kv_heads);
+  const bool ragged = a->cu_seqlens != nullptr;
+  LKV_REQUIRE(!ragged || a->batch == 0 || a->tokens == 0 || a->max_seqlen >= 1,
+              "ragged calls need max_seqlen >= 1, got %d", a->max_seqlen);
+  // token rows of the call: tokens per sequence x batch, or the ragged call's total
+  const int64_t rows = ragged ? (a->batch > 0 ? a->tokens : 0) : static_cast<int64_t>(a->batch) * a->tokens;
+  // tokens of the longest sequence
+  const int64_t seq_tokens = ragged ? std::min(a->max_seqlen, a->tokens) : a->tokens;
+  const int64_t items = rows * (a->num_q_heads + a->num_kv_heads);
   if (items == 0) return LKV_OK;
   LKV_REQUIRE(items / 4 + 1 < (1LL << 31), "too many tokens in one call");
   QkvParams p;
@@ -611,6 +657,8 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
   p.d_npages = a->deep_num_pages;
   p.rounding = a->rounding;
   p.rv_mul = a->ring_v_mul;
+  p.cu = a->cu_seqlens;
+  p.max_seqlen = static_cast<int32_t>(seq_tokens);
   // Calls of many tokens with 16-byte-aligned rows take the block form (16-byte accesses, V tiles
   // written through LDS), provided the call's 32-position blocks do not wrap onto each other in the
   // ring; decode-sized calls keep one wave per (token, head).
@@ -618,10 +666,10 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
     return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0 && s0 % 8 == 0 && s1 % 8 == 0;
   };
   // 32-position blocks one sequence's tokens span (exact for host-constant positions)
-  const int64_t kv_blocks = a->positions != nullptr
-                                ? (a->tokens + kBlockTokens - 1) / kBlockTokens + 1
+  const int64_t kv_blocks = a->positions != nullptr || ragged
+                                ? (seq_tokens + kBlockTokens - 1) / kBlockTokens + 1
                                 : (a->position_const + a->tokens - 1) / kBlockTokens - a->position_const / kBlockTokens + 1;
-  const bool block_form = a->tokens >= 16 && kv_blocks <= a->ring_tokens / kBlockTokens &&
+  const bool block_form = rows >= 16 && kv_blocks <= a->ring_tokens / kBlockTokens &&
                           aligned(a->q, a->q_stride_b, a->q_stride_t) && aligned(a->k, a->k_stride_b, a->k_stride_t) &&
                           aligned(a->v, a->v_stride_b, a->v_stride_t) && aligned(a->cos, a->cs_stride_b, a->cs_stride_t) &&
                           aligned(a->sin, a->cs_stride_b, a->cs_stride_t) &&
@@ -631,7 +679,7 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
                           aligned(a->deep_k, a->deep_seq_stride, a->deep_head_stride) &&
                           aligned(a->deep_v, a->deep_page_stride, 0);
   if (block_form) {
-    const int64_t q_groups = static_cast<int64_t>(a->batch) * a->tokens * ((a->num_q_heads + kQRows - 1) / kQRows);
+    const int64_t q_groups = rows * ((a->num_q_heads + kQRows - 1) / kQRows);
     const int64_t kv_wgs = static_cast<int64_t>(a->batch) * a->num_kv_heads * kv_blocks;
     const int64_t wgs = kv_wgs + (q_groups + 31) / 32;
     LKV_REQUIRE(wgs < (1LL << 31) && q_groups < (1LL << 31) - 32, "too many tokens in one call");

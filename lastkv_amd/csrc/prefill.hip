@@ -47,7 +47,41 @@ struct PrefillParams {
   int32_t vscale_mode;
   uint16_t* v16;       // fp16 V of every key block, [B, Hkv, v16_blocks, 4096]
   int32_t v16_blocks;  // blocks per (sequence, kv head) in v16
+  // ragged query rows: sequence b's tokens are rows cu[b] .. cu[b + 1] - 1 of q / out (nullptr:
+  // L tokens per sequence); rows = the call's total row count.  Sequences with at most
+  // decode_rows query rows per kv head run on the decode kernel and are skipped here.
+  const int32_t* cu;
+  int32_t rows, decode_rows;
 };
+
+// Query tokens of sequence b and the q / out / lse row of its token 0.
+struct SeqRows {
+  int L;
+  int64_t q0, o0, lse0;
+};
+
+__device__ inline SeqRows seq_rows(const PrefillParams& p, int b) {
+  SeqRows r;
+  if (p.cu == nullptr) {
+    r.L = p.L;
+    r.q0 = b * p.q_sb;
+    r.o0 = b * p.out_sb;
+    r.lse0 = static_cast<int64_t>(b) * p.L;
+    return r;
+  }
+  const int s0 = min(max(p.cu[b], 0), p.rows);
+  r.L = min(min(max(p.cu[b + 1], s0), p.rows) - s0, p.L);
+  r.q0 = s0 * p.q_st;
+  r.o0 = s0 * p.out_st;
+  r.lse0 = s0;
+  return r;
+}
+
+// Whether sequence b's queries run in this kernel (ragged calls hand short sequences to the decode
+// kernel).
+__device__ inline bool on_tile_path(const PrefillParams& p, const SeqRows& sr) {
+  return sr.L > 0 && static_cast<int64_t>(sr.L) * p.group > p.decode_rows;
+}
 
 __device__ inline uint32_t f16x2_bits(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
@@ -78,9 +112,10 @@ __device__ inline uint32_t pack_f16_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// Local-segment tokens visible to a query token (causal: bottom-right aligned).
-__device__ inline int visible_local(const PrefillParams& p, const SeqView& sv, int token) {
-  const int v = p.causal ? sv.n1 - p.L + token + 1 : sv.n1;
+// Local-segment tokens visible to query token `token` of a sequence of L query tokens (causal:
+// bottom-right aligned).
+__device__ inline int visible_local(const PrefillParams& p, const SeqView& sv, int L, int token) {
+  const int v = p.causal ? sv.n1 - L + token + 1 : sv.n1;
   return min(max(v, 0), sv.n1);
 }
 
@@ -230,6 +265,7 @@ __device__ __attribute__((always_inline)) inline void unroll_steps(std::integer_
 template <bool kPaged>
 __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
   const int blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  if (!on_tile_path(p, seq_rows(p, b))) return;
   const SeqView sv = make_seq_view(p.seg, b, kvh);
   if (blk >= sv.nb0 + local_blocks(sv, sv.n1)) return;
   const bool older = blk < sv.nb0;
@@ -275,9 +311,12 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   const int kvh = (logical / p.tiles) % p.hkv;
   const int b = logical / (p.tiles * p.hkv);
   const int G = p.group;
-  const int rows_total = p.L * G;
+  const SeqRows sr = seq_rows(p, b);
+  const int rows_total = sr.L * G;
   const int wg_row0 = tile * kRowsPerWg;
   const int row0 = wg_row0 + wave * kRowsPerWave;
+  // (workgroup-uniform: a ragged call's tiles past a sequence's rows, or its short sequences)
+  if (!on_tile_path(p, sr) || wg_row0 >= rows_total) return;
 
   SeqView sv = make_seq_view(p.seg, b, kvh);
   // these are wave-uniform; keeping them in scalar registers keeps every block offset scalar
@@ -287,7 +326,7 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   sv.lblk0 = __builtin_amdgcn_readfirstlane(sv.lblk0);
   sv.lead = __builtin_amdgcn_readfirstlane(sv.lead);
   const int wg_last_row = min(rows_total, wg_row0 + kRowsPerWg) - 1;
-  const int nbt = __builtin_amdgcn_readfirstlane(sv.nb0 + local_blocks(sv, visible_local(p, sv, wg_last_row / G)));
+  const int nbt = __builtin_amdgcn_readfirstlane(sv.nb0 + local_blocks(sv, visible_local(p, sv, sr.L, wg_last_row / G)));
 
   uint4 qf[CG][4];
   int lim[CG];  // last visible local-segment token of this lane's column
@@ -296,10 +335,10 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
     const int row = row0 + 16 * cg + n16;
     if (row < rows_total) {
       const int tok = row / G, h = row - tok * G;
-      const uint16_t* qrow = p.q + b * p.q_sb + tok * p.q_st + static_cast<int64_t>(kvh * G + h) * kHeadDim;
+      const uint16_t* qrow = p.q + sr.q0 + tok * p.q_st + static_cast<int64_t>(kvh * G + h) * kHeadDim;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) qf[cg][kb] = *reinterpret_cast<const uint4*>(qrow + 32 * kb + 8 * g4);
-      lim[cg] = visible_local(p, sv, tok) - 1;
+      lim[cg] = visible_local(p, sv, sr.L, tok) - 1;
     } else {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) qf[cg][kb] = make_uint4(0, 0, 0, 0);
@@ -309,7 +348,7 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   const float c = p.scale_log2;
   // smallest causal limit among the wave's rows (its first row); blocks past it need masking
   const int w_min_lim =
-      __builtin_amdgcn_readfirstlane(row0 < rows_total ? visible_local(p, sv, row0 / G) - 1 : -1);
+      __builtin_amdgcn_readfirstlane(row0 < rows_total ? visible_local(p, sv, sr.L, row0 / G) - 1 : -1);
 
   RowState rs[CG];
 #pragma unroll
@@ -508,7 +547,7 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
     const int row = row0 + 16 * cg + n16;
     if (row < rows_total) {
       const int tok = row / G, h = row - tok * G;
-      uint16_t* orow = p.out + b * p.out_sb + tok * p.out_st + static_cast<int64_t>(kvh * G + h) * kHeadDim;
+      uint16_t* orow = p.out + sr.o0 + tok * p.out_st + static_cast<int64_t>(kvh * G + h) * kHeadDim;
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb) {
         const f32x4 x = o[cg][nb] * linv;
@@ -520,7 +559,7 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
         *reinterpret_cast<uint2*>(orow + 16 * nb + 4 * g4) = make_uint2(w01, w23);
       }
       if (p.lse != nullptr && g4 == 0)
-        p.lse[(static_cast<int64_t>(b) * p.L + tok) * p.hq + kvh * G + h] =
+        p.lse[(sr.lse0 + tok) * p.hq + kvh * G + h] =
             lt > 0.f ? (rs[cg].mc + __log2f(lt)) * kLn2 : kNegInf;
     }
   }
@@ -566,7 +605,12 @@ int64_t v16_blocks(const lkv_prefill_args* a) {
 
 extern "C" int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args* a) {
   if (a == nullptr || a->batch <= 0 || a->num_kv_heads <= 0) return 0;
-  return static_cast<int64_t>(a->batch) * a->num_kv_heads * v16_blocks(a) * (lkv::kBlockElems * 2);
+  const int64_t v16 = static_cast<int64_t>(a->batch) * a->num_kv_heads * v16_blocks(a) * (lkv::kBlockElems * 2);
+  if (a->num_splits <= 1) return v16;
+  // split states of the decode kernel's sequences: [rows, Hq] (ragged) or [B, L, Hq] rows
+  const int64_t rows = (a->cu_seqlens_q ? int64_t{1} : static_cast<int64_t>(a->batch)) * std::max(a->tokens, 0) *
+                       a->num_q_heads;
+  return std::max(v16, rows * a->num_splits * (lkv::kHeadDim + 2) * 4);
 }
 
 extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stream) {
@@ -585,6 +629,10 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->older_vscale_mode == 1, "older_vscale_mode must be 0 or 1");
   LKV_REQUIRE(a->older_vscale_mode == 0 || a->vscale != nullptr, "older_vscale_mode 1 needs vscale");
   LKV_REQUIRE(a->q != nullptr && a->out != nullptr, "null q/out");
+  const bool ragged = a->cu_seqlens_q != nullptr;
+  LKV_REQUIRE(!ragged || a->tokens == 0 || a->max_seqlen_q >= 1, "ragged calls need max_seqlen_q >= 1, got %d",
+              a->max_seqlen_q);
+  LKV_REQUIRE(a->num_splits >= 0 && a->num_splits <= 1024, "num_splits must be in [0, 1024], got %d", a->num_splits);
   LKV_REQUIRE((a->q_stride_b % 8) == 0 && (a->q_stride_t % 8) == 0 && (reinterpret_cast<uintptr_t>(a->q) & 15) == 0,
               "q rows must be 16-byte aligned");
   LKV_REQUIRE((a->out_stride_b % 4) == 0 && (a->out_stride_t % 4) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 7) == 0,
@@ -592,7 +640,7 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   // causal = 1 masks the local segment bottom-right, the queries' own keys being its last `tokens`
   // tokens; a non-empty local segment shorter than that would need the mask to reach into the older
   // segment (without a local segment, or with an empty one, the older segment is fully visible)
-  LKV_REQUIRE(a->causal == 0 || a->local_k == nullptr || a->local_len != nullptr || a->local_len_const <= 0 ||
+  LKV_REQUIRE(ragged || a->causal == 0 || a->local_k == nullptr || a->local_len != nullptr || a->local_len_const <= 0 ||
                   a->local_len_const >= a->tokens,
               "causal calls need local_len >= tokens (the queries' own keys end the local segment), got %d < %d",
               a->local_len_const, a->tokens);
@@ -600,6 +648,8 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   if (const int32_t st = fill_segments(a, p.seg)) return st;
   LKV_REQUIRE(a->batch <= 65535 && a->num_kv_heads <= 65535, "batch and num_kv_heads must be <= 65535");
   if (a->batch == 0 || a->tokens == 0) return LKV_OK;
+  // query tokens per sequence (ragged: an upper bound)
+  const int64_t seq_tokens = ragged ? std::min(a->max_seqlen_q, a->tokens) : a->tokens;
   const int64_t vblocks = v16_blocks(a);
   const int64_t need = lkv_prefill_workspace_bytes(a);
   LKV_REQUIRE(vblocks * kBlockElems * 2 < (1LL << 31), "too many key blocks per sequence");
@@ -607,11 +657,24 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
               "prefill needs a workspace of %lld bytes (lkv_prefill_workspace_bytes), got %lld",
               static_cast<long long>(need), static_cast<long long>(a->workspace_bytes));
   LKV_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 15) == 0, "workspace must be 16-byte aligned");
-  // Calls of at most 64 query rows per kv head (e.g. up to 16 tokens of a GQA group of 4) read every
-  // key once on the decode kernel (one score column per (token, head)) instead of converting V to
-  // fp16 and running 2-wave tiles; tile_waves 4 or 8 keep them on the tile kernel.
-  if (a->tile_waves == 0 && static_cast<int64_t>(a->tokens) * group <= 64)
-    return prefill_on_decode_kernel(a, p.seg, group, as_stream(stream));
+  hipStream_t s = as_stream(stream);
+  // Sequences of at most 64 query rows per kv head (e.g. decode tokens, or up to 16 tokens of a GQA
+  // group of 4) read every key once on the decode kernel (one score column per (token, head))
+  // instead of converting V to fp16 and running 2-wave tiles; tile_waves 4 or 8 keep them on the
+  // tile kernel.  A ragged call runs its sequences of 1-16, 17-32 and 33-64 columns on the decode
+  // instance of that width (one launch per class present) and the longer ones on the tile kernel.
+  const int64_t max_cols = seq_tokens * group;
+  const bool short_on_decode = a->tile_waves == 0;
+  if (short_on_decode) {
+    const int32_t bounds[4] = {0, 16, 32, 64};
+    for (int c = 0; c < 3; ++c) {
+      if (max_cols <= bounds[c]) break;
+      // a uniform call is one class: the one its width falls in
+      if (!ragged && max_cols > bounds[c + 1]) continue;
+      if (const int32_t st = prefill_on_decode_kernel(a, p.seg, group, bounds[c], bounds[c + 1], s)) return st;
+    }
+    if (max_cols <= 64) return LKV_OK;
+  }
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_stride_b;
   p.q_st = a->q_stride_t;
@@ -621,7 +684,7 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.lse = a->lse;
   p.vscale = a->vscale;
   p.out_scale = a->out_scale;
-  p.L = a->tokens;
+  p.L = static_cast<int32_t>(seq_tokens);
   p.hq = a->num_q_heads;
   p.group = group;
   p.causal = a->causal;
@@ -629,12 +692,16 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.vscale_mode = a->older_vscale_mode;
   p.v16 = static_cast<uint16_t*>(a->workspace);
   p.v16_blocks = static_cast<int32_t>(vblocks);
-  const int64_t rows = static_cast<int64_t>(a->tokens) * group;
+  p.cu = a->cu_seqlens_q;
+  p.rows = a->tokens;
+  p.decode_rows = ragged && short_on_decode ? 64 : -1;
+  const int64_t rows = seq_tokens * group;
   const int64_t heads = static_cast<int64_t>(a->num_kv_heads) * a->batch;
   // Each wave takes 32 query rows.  Short calls (<= 64 rows per kv head): 2 waves.  Otherwise 8
   // waves (two per SIMD, one workgroup per CU), or 4 waves (two workgroups per CU) when the 4-wave
   // grid still leaves at most one workgroup per CU, which keeps twice the CUs busy (measured on 256
   // CUs: at B = 1 of a config-3 piece 23 vs 18 %; from B = 2 up the 8-wave tile is 0.5-1.5 points ahead).
+  // A ragged call sizes the grid by its longest sequence; the tiles past a sequence's own rows exit.
   const bool wide = rows > 64;
   int waves = wide ? 8 : 2;
   if (wide && a->tile_waves != 0) {
@@ -650,7 +717,6 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   LKV_REQUIRE(wgs < (1LL << 31), "too many query rows");
   p.tiles = static_cast<int32_t>(tiles);
   p.hkv = a->num_kv_heads;
-  hipStream_t s = as_stream(stream);
   const bool paged = a->older_block_table != nullptr || a->local_block_table != nullptr;
   if (vblocks > 0) {  // (no keys at all: every row's output is zero; the main kernel skips its loop)
     const dim3 vgrid(static_cast<unsigned>(vblocks), a->num_kv_heads, a->batch);

@@ -422,10 +422,21 @@ def prefill_attention(
     workspace: torch.Tensor | None = None,
     tile_waves: int = 0,
     out_scale: torch.Tensor | None = None,
+    cu_seqlens_q: torch.Tensor | None = None,
+    max_seqlen_q: int | None = None,
+    num_splits: int = 0,
 ) -> torch.Tensor:
     """Attention of ``q`` ``[B, L, Hq, 128]`` (L query tokens per sequence, the last L tokens of
     the local segment) over ``[older | local]``; the local segment is bottom-right causal
     (``causal``) or fully visible.  Returns ``out`` ``[B, L, Hq, 128]`` bf16.
+
+    Ragged rows (FlashAttention's varlen form): with ``cu_seqlens_q`` (int32 ``[B + 1]`` on the
+    device, ``cu[0] = 0``, non-decreasing) ``q`` is ``[T, Hq, 128]``, sequence b's queries being rows
+    ``cu[b] .. cu[b + 1] - 1`` (each sequence's L_b queries are the last L_b tokens of its local
+    segment); ``max_seqlen_q`` (a host int) bounds every L_b, and ``out`` / ``lse`` are ``[T, Hq, 128]``
+    / ``[T, Hq]``.  One call runs every sequence: those of at most 64 query rows per kv head on the
+    decode kernel, the others on the tile kernel.  ``num_splits`` fixes the decode kernel's key
+    splits for those sequences (0: chosen from the grid).
 
     ``workspace`` (uint8, 16-byte aligned, at least ``prefill_workspace_bytes`` of the same
     arguments) receives the fp16 V of every key block; without it one is allocated per call.
@@ -433,24 +444,43 @@ def prefill_attention(
     choose from the grid size and the device's CU count.  ``out_scale`` as in ``decode_attention``."""
 
     _require_bf16_cuda("q", q)
-    _require(q.dim() == 4 and q.shape[-1] == HEAD_DIM, "q must be [B, L, Hq, 128]")
+    ragged = cu_seqlens_q is not None
+    if ragged:
+        _require(q.dim() == 3 and q.shape[-1] == HEAD_DIM, "a ragged q must be [T, Hq, 128]")
+        _require(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_q.dim() == 1 and cu_seqlens_q.numel() >= 2
+                 and cu_seqlens_q.is_contiguous() and cu_seqlens_q.device == q.device,
+                 "cu_seqlens_q must be a contiguous int32 [B + 1] tensor on the query's device")
+        _require(max_seqlen_q is not None and int(max_seqlen_q) >= 1, "a ragged call needs max_seqlen_q >= 1")
+        q = q.unsqueeze(0)  # [1, T, Hq, 128]: the row stride is the token stride
+        B, L, Hq = cu_seqlens_q.numel() - 1, q.shape[1], q.shape[2]
+    else:
+        _require(max_seqlen_q is None, "max_seqlen_q applies to ragged calls (cu_seqlens_q)")
+        _require(q.dim() == 4 and q.shape[-1] == HEAD_DIM, "q must be [B, L, Hq, 128]")
+        B, L, Hq, _ = q.shape
     _require(q.stride(-1) == 1 and q.stride(2) == HEAD_DIM, "q heads must be contiguous rows of 128")
-    B, L, Hq, _ = q.shape
     device = q.device
     a = _lib.PrefillArgs()
     a.struct_size = ctypes.sizeof(_lib.PrefillArgs)
     Hkv = _fill_segments(a, B, device, older, older_len, older_slot, vscale, local, local_len, local_start, local_slot,
                          older_table, local_table, local_ring_blocks)
     _require(Hq % Hkv == 0, "Hq must be a multiple of Hkv")
+    QB = 1 if ragged else B  # leading dim of q / out
     if out is None:
-        out = torch.empty((B, L, Hq, HEAD_DIM), dtype=torch.bfloat16, device=device)
+        out = torch.empty((QB, L, Hq, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    elif ragged:
+        _require(out.dim() == 3, "a ragged out must be [T, Hq, 128]")
+        out = out.unsqueeze(0)
     _require_bf16_cuda("out", out)
-    _require(tuple(out.shape) == (B, L, Hq, HEAD_DIM), "out must be [B, L, Hq, 128]")
+    _require(tuple(out.shape) == (QB, L, Hq, HEAD_DIM), "out must be [B, L, Hq, 128] ([T, Hq, 128] ragged)")
     _require(out.stride(-1) == 1 and out.stride(2) == HEAD_DIM, "out heads must be contiguous rows of 128")
     if lse is not None:
-        _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() == B * L * Hq and lse.device == device,
-                 "lse must be a contiguous fp32 [B, L, Hq] tensor")
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() == QB * L * Hq and lse.device == device,
+                 "lse must be a contiguous fp32 [B, L, Hq] tensor ([T, Hq] ragged)")
     a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = B, L, Hq, Hkv, HEAD_DIM
+    if ragged:
+        a.cu_seqlens_q, a.max_seqlen_q = cu_seqlens_q.data_ptr(), int(max_seqlen_q)
+    _require(0 <= int(num_splits) <= 1024, "num_splits must be in [0, 1024]")
+    a.num_splits = int(num_splits)
     a.sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
     a.causal = 1 if causal else 0
     a.tile_waves = int(tile_waves)
@@ -467,7 +497,7 @@ def prefill_attention(
     a.workspace_bytes = workspace.numel() * workspace.element_size()
     _require(a.workspace_bytes >= need, f"prefill workspace too small: {a.workspace_bytes} < {need} bytes")
     _lib.check(lib.lkv_prefill_attn(ctypes.byref(a), _stream(device)), "lkv_prefill_attn")
-    return out
+    return out[0] if ragged else out
 
 
 def decode_workspace_bytes(batch: int, num_q_heads: int, num_splits: int) -> int:
@@ -482,6 +512,13 @@ def prefill_workspace_bytes(batch: int, kv_heads: int, older_tokens: int, local_
 
     blocks = -(-older_tokens // 32) + (-(-(local_lead + local_tokens) // 32) if local_tokens > 0 else 0)
     return batch * kv_heads * blocks * 8192
+
+
+def prefill_split_state_bytes(rows: int, num_q_heads: int, num_splits: int) -> int:
+    """Workspace a prefill call with a fixed ``num_splits`` > 1 needs for the decode kernel's split
+    states of ``rows`` query tokens (the call's total rows)."""
+
+    return 0 if num_splits <= 1 else rows * num_q_heads * num_splits * (HEAD_DIM + 2) * 4
 
 
 def merge_states(
@@ -588,17 +625,39 @@ def qkv_epilogue(
     deep_table: torch.Tensor | None = None,
     rounding: str = "torch",
     ring_v_mul: torch.Tensor | None = None,
+    cu_seqlens: torch.Tensor | None = None,
+    max_seqlen: int | None = None,
 ) -> torch.Tensor:
     """RoPE + q/k RMSNorm of the projections and the append of K/V to the layer ring (and, for
     the final layer, the shared cache) at positions ``positions + i``; returns the normalised
     queries ``[B, L, Hq, 128]``.  A PagedKV ring / deep store takes an int32 page table ``[B, W]``
     (``ring_tokens``: the ring length, default ``32 * W``).
 
+    Ragged rows: with ``cu_seqlens`` (int32 ``[B + 1]`` on the device) ``q`` / ``k`` / ``v`` are
+    ``[T, heads * 128]`` (or ``[T, heads, 128]``) and ``cos`` / ``sin`` ``[T, 128]`` (or ``[1, T,
+    128]``), sequence b's tokens being rows ``cu[b] .. cu[b + 1] - 1`` at positions ``positions[b] +
+    i``; ``max_seqlen`` bounds each sequence's count; returns ``[T, Hq, 128]``.
+
     ``rounding``: ``"torch"``, the HF model's bf16 op order, or ``"vllm"``, the reference's fused
     QKV kernel (single-FMA rotary, fixed RMSNorm summation order).  ``ring_v_mul`` ``[Hkv]`` fp32
     writes the ring's V as ``bf16(v * ring_v_mul[g])`` (the vLLM path's V / s rings); the shared
     cache keeps the raw V."""
 
+    ragged = cu_seqlens is not None
+    if ragged:
+        _require(cu_seqlens.dtype == torch.int32 and cu_seqlens.dim() == 1 and cu_seqlens.numel() >= 2
+                 and cu_seqlens.is_contiguous() and cu_seqlens.device == q.device,
+                 "cu_seqlens must be a contiguous int32 [B + 1] tensor on the query's device")
+        _require(max_seqlen is not None and int(max_seqlen) >= 1, "a ragged call needs max_seqlen >= 1")
+        q, k, v = q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0)  # [1, T, ...]
+        if cos.dim() == 2:
+            cos, sin = cos.unsqueeze(0), sin.unsqueeze(0)
+        _require(cos.dim() == 3 and cos.shape[0] == 1, "ragged cos / sin must be [T, 128] or [1, T, 128]")
+        if q_out is not None:
+            _require(q_out.dim() == 3, "a ragged q_out must be [T, Hq, 128]")
+            q_out = q_out.unsqueeze(0)
+    else:
+        _require(max_seqlen is None, "max_seqlen applies to ragged calls (cu_seqlens)")
     B, L = int(q.shape[0]), int(q.shape[1])
     qp, qsb, qst = _rows("q", q, num_q_heads)
     kp, ksb, kst = _rows("k", k, num_kv_heads)
@@ -624,11 +683,14 @@ def qkv_epilogue(
                  and ring_v_mul.device == device, "ring_v_mul must be a contiguous fp32 [Hkv] tensor on the query's device")
     a = _lib.QkvArgs()
     a.struct_size = ctypes.sizeof(_lib.QkvArgs)
-    a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = B, L, num_q_heads, num_kv_heads, HEAD_DIM
+    NB = cu_seqlens.numel() - 1 if ragged else B  # sequences
+    a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = NB, L, num_q_heads, num_kv_heads, HEAD_DIM
+    if ragged:
+        a.cu_seqlens, a.max_seqlen = cu_seqlens.data_ptr(), int(max_seqlen)
     a.rounding = ROUNDINGS[rounding]
     a.ring_v_mul = _ptr(ring_v_mul)
     a.eps = float(eps)
-    a.positions, a.position_const = _len_arg(positions, B, "positions", device)
+    a.positions, a.position_const = _len_arg(positions, NB, "positions", device)
     a.q, a.q_stride_b, a.q_stride_t = qp, qsb, qst
     a.k, a.k_stride_b, a.k_stride_t = kp, ksb, kst
     a.v, a.v_stride_b, a.v_stride_t = vp, vsb, vst
@@ -640,7 +702,7 @@ def qkv_epilogue(
     a.ring_k, a.ring_v = ring.k.data_ptr(), ring.v.data_ptr()
     a.ring_head_stride = ring.head_stride
     if isinstance(ring, PagedKV):
-        _table_arg(ring_table, B, "ring", device)
+        _table_arg(ring_table, NB, "ring", device)
         a.ring_block_table, a.ring_table_stride = ring_table.data_ptr(), ring_table.stride(0)
         a.ring_page_stride, a.ring_num_pages = ring.page_stride, ring.pages
         a.ring_tokens = int(ring_tokens if ring_tokens is not None else ring_table.shape[1] * BLOCK_TOKENS)
@@ -654,7 +716,7 @@ def qkv_epilogue(
         a.deep_k, a.deep_v = deep.k.data_ptr(), deep.v.data_ptr()
         a.deep_head_stride = deep.head_stride
         if isinstance(deep, PagedKV):
-            _table_arg(deep_table, B, "deep", device)
+            _table_arg(deep_table, NB, "deep", device)
             a.deep_block_table, a.deep_table_stride = deep_table.data_ptr(), deep_table.stride(0)
             a.deep_page_stride, a.deep_num_pages = deep.page_stride, deep.pages
             a.deep_capacity_tokens = deep_table.shape[1] * BLOCK_TOKENS
@@ -662,10 +724,11 @@ def qkv_epilogue(
             a.deep_seq_stride = deep.seq_stride
             a.deep_capacity_tokens, a.deep_num_slots, a.deep_slot = deep.capacity_tokens, deep.slots, _ptr(deep_slot)
         if not isinstance(positions, torch.Tensor):
-            _require(positions + L <= a.deep_capacity_tokens, "positions exceed the shared cache capacity")
+            _require(positions + (int(max_seqlen) if ragged else L) <= a.deep_capacity_tokens,
+                     "positions exceed the shared cache capacity")
     lib = _lib.load()
     _lib.check(lib.lkv_qkv_epilogue(ctypes.byref(a), _stream(device)), "lkv_qkv_epilogue")
-    return q_out
+    return q_out[0] if ragged else q_out
 
 
 def blend_chunk(

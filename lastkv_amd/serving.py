@@ -250,6 +250,7 @@ class LastKVFastPath:
         self._open = np.zeros(pool.max_slots, dtype=bool)
         i32 = dict(dtype=torch.int32, device=dev)
         self._meta = torch.zeros((4, max_batch), **i32)  # positions, older_len, local_len, local_start
+        self._cu = torch.zeros(max_batch + 1, **i32)  # row offsets of a ragged step (cu_seqlens)
         self._slots = torch.zeros(max_batch, dtype=torch.long, device=dev)
         self._older_table = torch.full((max_batch, pool.src_width), pool.scratch_page, **i32)
         self._ring_table = torch.full((pool.num_layers, max_batch, pool.ring_blocks), pool.scratch_page, **i32)
@@ -263,8 +264,8 @@ class LastKVFastPath:
         self.tokens = 0  # query tokens of this step, padding included
         self.splits = 1
         self.uniform = True  # every row of this step has the same token count
+        self.max_rows = 1  # query tokens of this step's longest row
         self._row_rope: list[tuple[torch.Tensor, torch.Tensor]] = []
-        self._row_splits: list[int] = []
 
     @classmethod
     def from_model(cls, model, pool: LastKVPagePool, *, max_batch: int, num_splits: int | None = None,
@@ -368,26 +369,22 @@ class LastKVFastPath:
             if self._decode_ws.numel() < need:
                 self._decode_ws = torch.empty(need, dtype=torch.uint8, device=P.device)
         else:
-            self._row_rope = []
             if uniform:
                 n = parsed[0].tokens
                 pos = self._meta[0, :B].long()[:, None] + torch.arange(n, device=P.device)[None, :]
-                self._row_rope = [self.rotary(pos)]
-                # device-resident lengths: the kernel sizes its fp16 V copy by the older table's
-                # width and the whole ring
-                width = max(1, -(-max(r.older for r in parsed) // BLOCK))
-                need = ops.prefill_workspace_bytes(B, P.kv_heads, width * BLOCK, P.ring_tokens)
             else:
-                cu = ops._cu_count(P.device)
-                self._row_splits = [self.num_splits or ops.default_decode_splits(1, P.kv_heads, r.older + r.local, cu)
-                                    for r in parsed]
-                for r in parsed:
-                    self._row_rope.append(self.rotary(torch.arange(r.position, r.position + r.tokens,
-                                                                   device=P.device)[None, :]))
-                need = max(ops.prefill_workspace_bytes(1, P.kv_heads, r.older, r.local) for r in parsed)
-                dneed = max(ops.decode_workspace_bytes(1, Hq, sp) for sp in self._row_splits)
-                if self._decode_ws.numel() < dneed:
-                    self._decode_ws = torch.empty(dneed, dtype=torch.uint8, device=P.device)
+                # ragged step: the rows' tokens back to back (cu_seqlens), RoPE rows for each
+                cu = np.zeros(B + 1, dtype=np.int32)
+                cu[1:] = np.cumsum([r.tokens for r in parsed])
+                P.stager.copy(self._cu[:B + 1], cu)
+                pos = torch.from_numpy(np.concatenate([np.arange(r.position, r.position + r.tokens)
+                                                       for r in parsed])).to(P.device, non_blocking=True)[None, :]
+            self._row_rope = [self.rotary(pos)]
+            # device-resident lengths: the kernel sizes its fp16 V copy by the older table's width
+            # and the whole ring (a ragged call's short rows share it for their split state)
+            width = max(1, -(-max(r.older for r in parsed) // BLOCK))
+            need = ops.prefill_workspace_bytes(B, P.kv_heads, width * BLOCK, P.ring_tokens)
+            need = max(need, ops.prefill_split_state_bytes(self.tokens, Hq, self.num_splits or 0))
             if self._prefill_ws.numel() < need:
                 self._prefill_ws = torch.empty(need, dtype=torch.uint8, device=P.device)
         if self._q_out.shape[0] < self.tokens:
@@ -395,6 +392,7 @@ class LastKVFastPath:
         for r in parsed:
             self._seen[r.slot] = r.position + r.tokens
         self.rows, self.batch, self.uniform = parsed, Bp, uniform
+        self.max_rows = max(r.tokens for r in parsed)
 
     def _commit(self, slot: int, boundary: int) -> None:
         """Blend chunk [boundary - C, boundary) of every layer's ring of ``slot`` with its shared pages."""
@@ -450,30 +448,25 @@ class LastKVFastPath:
                 width = max(1, -(-max(r.older for r in self.rows) // BLOCK))
                 seg["older_table"] = self._older_table[:B, :width]
                 ops.prefill_attention(q_out, causal=True, out=output[:T].view(B, n, Hq, 128),
-                                      workspace=self._prefill_ws, **seg)
+                                      workspace=self._prefill_ws, num_splits=self.num_splits or 0, **seg)
             return output
-        start = 0
-        for b, r in enumerate(self.rows):
-            n = r.tokens
-            sl = slice(start, start + n)
-            cos, sin = self._row_rope[b]
-            q_out = ops.qkv_epilogue(
-                query[sl].reshape(1, n, Hq * 128), key[sl].reshape(1, n, Hkv * 128), value[sl].reshape(1, n, Hkv * 128),
-                cos, sin, num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=qn_w, k_norm_weight=kn_w, eps=eps,
-                positions=r.position, ring=P.pool, ring_table=ring_tab[b:b + 1], ring_tokens=P.ring_tokens,
-                deep=P.pool if top else None, deep_table=self._older_table[b:b + 1] if top else None,
-                q_out=self._q_out[sl].view(1, n, Hq, 128), **epi)
-            width = max(1, -(-r.older // BLOCK))
-            seg = dict(older=P.pool, older_table=self._older_table[b:b + 1, :width], older_len=r.older, vscale=vs,
-                       local=P.pool, local_table=ring_tab[b:b + 1], local_ring_blocks=P.ring_blocks, local_len=r.local,
-                       local_start=r.older % P.ring_tokens, out_scale=out_scale)
-            if n == 1:
-                ops.decode_attention(q_out.view(1, Hq, 128), out=output[sl].view(1, Hq, 128), num_splits=self._row_splits[b],
-                                     workspace=self._decode_ws, **seg)
-            else:
-                ops.prefill_attention(q_out, causal=True, out=output[sl].view(1, n, Hq, 128), workspace=self._prefill_ws,
-                                      **seg)
-            start += n
+        # ragged step (prefill pieces and decode tokens of different lengths): one epilogue and one
+        # attention call over the rows back to back (cu_seqlens), as the reference's single varlen
+        # FA3 call per layer (fastpath.py:643-648)
+        cu = self._cu[:B + 1]
+        cos, sin = self._row_rope[0]
+        q_out = ops.qkv_epilogue(
+            query[:T].reshape(T, Hq * 128), key[:T].reshape(T, Hkv * 128), value[:T].reshape(T, Hkv * 128),
+            cos, sin, num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=qn_w, k_norm_weight=kn_w, eps=eps,
+            positions=pos[:B], ring=P.pool, ring_table=ring_tab[:B], ring_tokens=P.ring_tokens,
+            deep=P.pool if top else None, deep_table=self._older_table[:B] if top else None,
+            q_out=self._q_out[:T], cu_seqlens=cu, max_seqlen=self.max_rows, **epi)
+        width = max(1, -(-max(r.older for r in self.rows) // BLOCK))
+        ops.prefill_attention(q_out, causal=True, out=output[:T].view(T, Hq, 128), workspace=self._prefill_ws,
+                              older=P.pool, older_table=self._older_table[:B, :width], older_len=older_len[:B],
+                              vscale=vs, local=P.pool, local_table=ring_tab[:B], local_ring_blocks=P.ring_blocks,
+                              local_len=local_len[:B], local_start=local_start[:B], out_scale=out_scale,
+                              cu_seqlens_q=cu, max_seqlen_q=self.max_rows, num_splits=self.num_splits or 0)
         return output
 
 

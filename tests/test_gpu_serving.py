@@ -57,7 +57,7 @@ class _Twin:
                    local_start=rec % c.ring_tokens)
         if n == 1:
             return ops.decode_attention(qn.view(1, Hq, 128), num_splits=1, **seg).view(1, Hq, 128)
-        return ops.prefill_attention(qn, causal=True, **seg).view(n, Hq, 128)
+        return ops.prefill_attention(qn, causal=True, num_splits=1, **seg).view(n, Hq, 128)
 
     def advance(self, n):
         c = self.cache

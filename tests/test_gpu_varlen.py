@@ -1,0 +1,229 @@
+"""Ragged (varlen) calls: one attention and one epilogue launch for a step whose sequences carry
+different numbers of query tokens (cu_seqlens), the reference's single FA3 varlen call per layer
+(vllm/src/lastkv/vllm/backends/rmarin_flashinfer/fastpath.py:643-648).
+
+1. ``prefill_attention(cu_seqlens_q=...)`` over sequences of 0-300 query tokens (every column class
+   of the decode kernel and the tile kernel in one call) equals the per-sequence uniform calls bit
+   for bit when both fix the decode kernel's split count, and is within the north-star bar of the
+   fp64 oracle with the automatic split count (contiguous and paged caches, causal and
+   bidirectional, V scale and output scale).
+2. ``qkv_epilogue(cu_seqlens=...)`` equals per-sequence calls bit for bit (normalised queries,
+   ring and shared-store contents) in both rounding contracts, per-token and block forms.
+3. The serving path's mixed step (31 decode rows + one 1024-token prefill row + one 7-token row)
+   through ``LastKVServingModel`` against the oracle model run per sequence.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from lastkv_amd import ops
+from lastkv_amd.serving import LastKVServingModel
+from oracle import attention as A
+from oracle import bf16
+
+from test_gpu_decode import MAX_ABS, REL_L2, _bf, _t
+from test_gpu_llm import _no_worse_than_reference_bf16, _o16, _o32, _tiny
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _ragged_case(rng, lengths, Hkv, G, paged, causal):
+    """Per sequence b: an older segment of T0_b tokens (slot b of a tiled store, or pages of a pool)
+    and a ring holding n1_b >= L_b tokens from a random start; returns the kernel segments, the
+    composed K / V per sequence (older V as bf16(V * s)) and the lengths."""
+
+    B = len(lengths)
+    ring_blocks = max(-(-max(lengths) // 32) + 2, 6)
+    R = ring_blocks * 32
+    T0 = [int(rng.integers(0, 700)) for _ in range(B)]
+    n1 = [int(rng.integers(max(L, 1), R + 1)) for L in lengths]
+    start = [int(rng.integers(0, R)) for _ in range(B)]
+    cap = max(32, -(-max(T0) // 32) * 32)
+    s = bf16.round_bf16(rng.uniform(0.4, 1.4, Hkv).astype(np.float32))
+    older = ops.TiledKV.zeros(B, Hkv, cap, DEV)
+    ring = ops.TiledKV.zeros(B, Hkv, R, DEV)
+    ks, vs = [], []
+    for b in range(B):
+        ok, ov = _bf(rng, (1, Hkv, T0[b], 128)), _bf(rng, (1, Hkv, T0[b], 128))
+        lk, lv = _bf(rng, (1, Hkv, n1[b], 128)), _bf(rng, (1, Hkv, n1[b], 128))
+        if T0[b]:
+            ops.pack_kv(_t(ok), _t(ov), ops.TiledKV(older.k[b:b + 1], older.v[b:b + 1]))
+        one = ops.TiledKV(ring.k[b:b + 1], ring.v[b:b + 1])
+        first = min(n1[b], R - start[b])
+        ops.pack_kv(_t(lk[:, :, :first]), _t(lv[:, :, :first]), one, token0=start[b])
+        if first < n1[b]:
+            ops.pack_kv(_t(lk[:, :, first:]), _t(lv[:, :, first:]), one, token0=0)
+        ks.append(np.concatenate([ok, lk], 2))
+        vs.append(np.concatenate([bf16.mul(ov, s.reshape(1, -1, 1, 1)), lv], 2))
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=DEV)
+    seg = dict(older_len=i32(T0), vscale=torch.from_numpy(s).to(DEV), local_len=i32(n1), local_start=i32(start))
+    if paged:
+        # the same blocks as pages of one head-major pool: older pages first, then the rings
+        ob, rb = cap // 32, ring_blocks
+        pool = ops.PagedKV.zeros(B * (ob + rb) + 1, Hkv, DEV)
+        perm = torch.randperm(B * (ob + rb), generator=torch.Generator().manual_seed(3)).to(DEV, torch.int32)
+        otab = perm[:B * ob].view(B, ob).contiguous()
+        rtab = perm[B * ob:].view(B, rb).contiguous()
+        for b in range(B):
+            for j in range(ob):
+                pool.k[:, otab[b, j]] = older.k[b, :, j]
+                pool.v[:, otab[b, j]] = older.v[b, :, j]
+            for j in range(rb):
+                pool.k[:, rtab[b, j]] = ring.k[b, :, j]
+                pool.v[:, rtab[b, j]] = ring.v[b, :, j]
+        seg.update(older=pool, older_table=otab, local=pool, local_table=rtab, local_ring_blocks=rb)
+    else:
+        seg.update(older=older, local=ring)
+    return seg, ks, vs, (T0, n1, start)
+
+
+def _one(seg, b, meta):
+    """Segment arguments of sequence b alone (host-constant lengths)."""
+
+    T0, n1, start = meta
+    one = dict(vscale=seg["vscale"], older_len=T0[b], local_len=n1[b], local_start=start[b])
+    if "older_table" in seg:
+        one.update(older=seg["older"], older_table=seg["older_table"][b:b + 1], local=seg["local"],
+                   local_table=seg["local_table"][b:b + 1], local_ring_blocks=seg["local_ring_blocks"])
+    else:
+        sl = lambda c: ops.TiledKV(c.k[b:b + 1], c.v[b:b + 1])
+        one.update(older=sl(seg["older"]), local=sl(seg["local"]))
+    return one
+
+
+LENGTHS = [1, 0, 5, 16, 17, 1, 33, 70, 200, 3, 300, 1]
+
+
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("causal", [True, False])
+def test_ragged_prefill_equals_per_sequence_calls_and_oracle(paged, causal):
+    rng = np.random.default_rng(41 + 2 * paged + causal)
+    Hkv, G = 2, 4
+    Hq = Hkv * G
+    seg, ks, vs, meta = _ragged_case(rng, LENGTHS, Hkv, G, paged, causal)
+    cu = np.concatenate([[0], np.cumsum(LENGTHS)]).astype(np.int32)
+    T = int(cu[-1])
+    q = _bf(rng, (T, Hq, 128))
+    cu_t = torch.from_numpy(cu).to(DEV)
+    out_scale = torch.from_numpy(bf16.round_bf16(rng.uniform(0.5, 1.5, Hkv).astype(np.float32))).to(DEV)
+    label = f"paged={paged} causal={causal}"
+    for splits in (1, 0):
+        lse = torch.empty((T, Hq), dtype=torch.float32, device=DEV)
+        out = ops.prefill_attention(_t(q), causal=causal, cu_seqlens_q=cu_t, max_seqlen_q=max(LENGTHS), lse=lse,
+                                    num_splits=splits, **seg)
+        scaled = ops.prefill_attention(_t(q), causal=causal, cu_seqlens_q=cu_t, max_seqlen_q=max(LENGTHS),
+                                       num_splits=splits, out_scale=out_scale, **seg)
+        worst = 0.0
+        for b, L in enumerate(LENGTHS):
+            if L == 0:
+                continue
+            rows = slice(int(cu[b]), int(cu[b + 1]))
+            want, want_lse = A.attention(q[rows].transpose(1, 0, 2)[None], ks[b], vs[b], causal_bottom_right=causal)
+            want = bf16.round_bf16(want[0].transpose(1, 0, 2).astype(np.float32))
+            got = out[rows].float().cpu().numpy()
+            ma, rl = A.max_abs(got, want), A.rel_l2(got, want)
+            worst = max(worst, rl)
+            assert ma <= MAX_ABS and rl <= REL_L2, f"{label} splits={splits} sequence {b} (L={L}): {ma} {rl}"
+            np.testing.assert_allclose(lse[rows].cpu().numpy(), want_lse[0].T, rtol=1e-4, atol=1e-4)
+            # the output scale is bf16(bf16(o) * s) of the unscaled rows
+            s_q = out_scale.repeat_interleave(G)[None, :, None]
+            assert torch.equal(scaled[rows], (out[rows].float() * s_q).bfloat16()), f"{label} out_scale sequence {b}"
+            if splits == 1:  # the per-sequence uniform call, same arithmetic
+                alone = ops.prefill_attention(_t(q[rows][None]), causal=causal, num_splits=1, **_one(seg, b, meta))
+                assert torch.equal(out[rows], alone[0]), f"{label}: sequence {b} (L={L}) differs from its own call"
+        print(f"{label} splits={splits}: worst rel_l2 {worst:.2e} over {len(LENGTHS)} sequences", flush=True)
+
+
+def test_ragged_prefill_forced_tiles_and_short_only_calls():
+    """tile_waves 4 / 8 run every sequence on the tiles; a ragged call whose sequences all have at
+    most 64 rows per kv head runs on the decode kernel alone."""
+
+    rng = np.random.default_rng(77)
+    Hkv, G = 2, 4
+    for lengths in ([1, 16, 9, 2, 1], [3, 80, 1, 40]):
+        seg, ks, vs, _ = _ragged_case(rng, lengths, Hkv, G, False, True)
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        q = _bf(rng, (int(cu[-1]), Hkv * G, 128))
+        for tw in (0, 4, 8):
+            out = ops.prefill_attention(_t(q), causal=True, cu_seqlens_q=torch.from_numpy(cu).to(DEV),
+                                        max_seqlen_q=max(lengths), tile_waves=tw, **seg)
+            for b in range(len(lengths)):
+                rows = slice(int(cu[b]), int(cu[b + 1]))
+                want, _ = A.attention(q[rows].transpose(1, 0, 2)[None], ks[b], vs[b], causal_bottom_right=True)
+                want = bf16.round_bf16(want[0].transpose(1, 0, 2).astype(np.float32))
+                got = out[rows].float().cpu().numpy()
+                assert A.max_abs(got, want) <= MAX_ABS and A.rel_l2(got, want) <= REL_L2, (lengths, tw, b)
+
+
+def _rotary(positions):
+    inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, device=positions.device).float() / 128))
+    f = positions[..., None].float() * inv
+    emb = torch.cat((f, f), -1)
+    return emb.cos().bfloat16(), emb.sin().bfloat16()
+
+
+@pytest.mark.parametrize("rounding", ["torch", "vllm"])
+@pytest.mark.parametrize("lengths", [[1, 3, 0, 2], [1, 40, 7, 100, 1, 33]])
+def test_ragged_epilogue_equals_per_sequence_calls(rounding, lengths):
+    g = torch.Generator(device=DEV).manual_seed(len(lengths) + (rounding == "vllm"))
+    Hq, Hkv, R, cap = 8, 2, 256, 512
+    B = len(lengths)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int32, device=DEV)
+    T = int(cu[-1])
+    pos = torch.tensor([int(x) for x in np.random.default_rng(B).integers(0, 300, B)], dtype=torch.int32, device=DEV)
+    fused = torch.randn((T, (Hq + 2 * Hkv) * 128), generator=g, device=DEV).bfloat16()
+    q, k, v = fused.split([Hq * 128, Hkv * 128, Hkv * 128], dim=-1)
+    flat = torch.cat([torch.arange(int(pos[b]), int(pos[b]) + L, device=DEV) for b, L in enumerate(lengths)])
+    cos, sin = _rotary(flat[None])
+    qw = (torch.rand(128, generator=g, device=DEV) + 0.5).bfloat16()
+    kw = (torch.rand(128, generator=g, device=DEV) + 0.5).bfloat16()
+    vmul = (torch.rand(Hkv, generator=g, device=DEV) + 0.5) if rounding == "vllm" else None
+    kwargs = dict(num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=qw, k_norm_weight=kw, eps=1e-5, rounding=rounding,
+                  ring_v_mul=vmul)
+    ring_a, deep_a = ops.TiledKV.zeros(B, Hkv, R, DEV), ops.TiledKV.zeros(B, Hkv, cap, DEV)
+    ring_b, deep_b = ops.TiledKV.zeros(B, Hkv, R, DEV), ops.TiledKV.zeros(B, Hkv, cap, DEV)
+    qa = ops.qkv_epilogue(q, k, v, cos, sin, positions=pos, ring=ring_a, deep=deep_a, cu_seqlens=cu,
+                          max_seqlen=max(lengths), **kwargs)
+    for b, L in enumerate(lengths):
+        if L == 0:
+            continue
+        rows = slice(int(cu[b]), int(cu[b + 1]))
+        sl = lambda c: ops.TiledKV(c.k[b:b + 1], c.v[b:b + 1])
+        qb = ops.qkv_epilogue(q[rows][None], k[rows][None], v[rows][None], cos[:, rows], sin[:, rows],
+                              positions=int(pos[b]), ring=sl(ring_b), deep=sl(deep_b), **kwargs)
+        assert torch.equal(qa[rows], qb[0]), f"sequence {b}: normalised queries differ"
+    assert torch.equal(ring_a.k, ring_b.k) and torch.equal(ring_a.v, ring_b.v), "ring contents differ"
+    assert torch.equal(deep_a.k, deep_b.k) and torch.equal(deep_a.v, deep_b.v), "shared-store contents differ"
+
+
+def test_serving_mixed_step_31_decode_1024_and_7_rows_match_oracle():
+    """A step of 31 decode rows, one 1024-token prefill row (positions 2048-3071: 1024 older keys
+    and a causal local segment of 2048) and one 7-token row, one epilogue and one attention launch
+    per layer, against the oracle model run per sequence."""
+
+    oracle, ours = _tiny(chunk=1024, layers=2)
+    runner = LastKVServingModel(ours, max_batch=33, max_tokens_per_slot=3104)
+    gen = torch.Generator().manual_seed(12)
+    prompts = [torch.randint(3, 97, (int(n),), generator=gen).to(DEV) for n in torch.randint(20, 90, (31,), generator=gen)]
+    long_seq = torch.randint(3, 97, (3072,), generator=gen).to(DEV)
+    short_seq = torch.randint(3, 97, (40,), generator=gen).to(DEV)
+    slots = [runner.add_sequence() for _ in range(33)]
+    with torch.inference_mode():
+        first = runner.step([(s, p) for s, p in zip(slots[:31], prompts)])  # a ragged prefill step
+        runner.step([(slots[31], long_seq[:1024]), (slots[32], short_seq[:33])])
+        runner.step([(slots[31], long_seq[1024:2048])])
+        nxt = first.argmax(-1)
+        seqs = [torch.cat([p, nxt[i:i + 1]]) for i, p in enumerate(prompts)]
+        rows = [(s, seqs[i][-1:]) for i, s in enumerate(slots[:31])]
+        rows += [(slots[31], long_seq[2048:]), (slots[32], short_seq[33:])]
+        assert sorted({int(ids.numel()) for _, ids in rows}) == [1, 7, 1024]
+        logits = runner.step(rows)
+        fulls = seqs + [long_seq, short_seq]
+        got = logits.float()
+        want = torch.stack([_o32(oracle)(s[None])[0][0, -1] for s in fulls]).float()
+        ref16 = torch.stack([_o16(oracle)(s[None])[0][0, -1] for s in fulls]).float()
+    _no_worse_than_reference_bf16(got[None], want[None], ref16[None], "mixed step (31 decode + 1024 + 7 rows)")
