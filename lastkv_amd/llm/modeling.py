@@ -132,6 +132,12 @@ class LastKVAttention(nn.Module):
         if c.use_nope:
             cos, sin = torch.ones_like(cos), torch.zeros_like(sin)
         p0 = cache.seen_tokens
+        # a cache driven by the reference's own decoder loop: allocate on first use, run this
+        # layer's boundary blend scheduled by its `cache.previous = ...` (modeling.py:203-207)
+        cache.reserve(B, Hkv, hidden_states.device, p0 + L)
+        if cache._pending[self.layer_idx] is not None:
+            cache.commit_layer(self.layer_idx, self.blend_params())
+        cache.check_layer(self.layer_idx, p0, L)
         ring = cache.ring(self.layer_idx)
         last = self.layer_idx == cache.num_layers - 1
         qn = ops.qkv_epilogue(
@@ -205,12 +211,10 @@ class CustomRecurrentMarinAKV254ReuseKVModel(nn.Module):
 
     def _commit_chunk(self, cache: LastKVCache, batch: int):
         """Boundary commit (modeling.py:203-207): the chunk just completed becomes every layer's
-        recent region, materialised once as alpha * shared + (1 - alpha) * own."""
+        recent region, materialised once as alpha * shared + (1 - alpha) * own, for all layers in
+        one launch."""
 
-        C = self.config.chunk_size
-        alpha, om, s = self._blend_params()
-        ops.blend_chunk(cache.ring_k, cache.ring_v, cache.store, batch=batch, chunk_start=cache.seen_tokens - C,
-                        chunk_len=C, alpha=alpha, one_minus_alpha=om, vscale=s)
+        cache.commit_all(self._blend_params())
 
     def forward(self, input_ids=None, inputs_embeds=None, attention_mask=None, position_ids=None,
                 past_key_values=None, use_cache=True):
