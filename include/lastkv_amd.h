@@ -184,15 +184,19 @@ int32_t lkv_decode_attn_noalloc(const lkv_decode_args *args, lkv_stream_t stream
  * local tokens (causal = 0); the last L local tokens are the queries' own K/V.  Segments,
  * slots, clamping and vscale are as in lkv_decode_args.  out is bf16 [B, L, Hq, 128] with
  * 8-byte-aligned rows (q: 16-byte-aligned rows); optional lse is fp32 [B, L, Hq] (natural log).
- * P*V runs in fp16, which represents bf16 V exactly for 2^-17 <= |V| <= 65280 and 0 (smaller
- * magnitudes are truncated toward zero, an absolute error below 2^-24; larger ones saturate at
- * 65504).  causal = 1 masks only the local segment, whose last `tokens` tokens are the queries' own
+ * The tile kernel runs P*V in fp16, which represents bf16 V exactly for 2^-17 <= |V| <= 65280 and 0
+ * (smaller magnitudes are truncated toward zero, an absolute error below 2^-24); a query tile whose
+ * keys include a finite V (older: bf16(V * vscale)) of magnitude 65536 or more runs instead on a
+ * second instance with bf16 V and the probabilities split into bf16 hi + lo, so no value
+ * saturates.  causal = 1 masks only the local segment, whose last `tokens` tokens are the queries' own
  * keys: a host-constant local_len in [1, tokens) is rejected (the mask would have to reach into
  * the older segment); without a local segment, or with local_len 0, the older segment is fully
  * visible (the two-pass path's source pass).  Device lengths are not checked: a row then sees the
  * local tokens up to its bottom-right limit, if any.  The call first writes the fp16 V (older segment as bf16(V * vscale)) of every key
- * block into the caller's workspace (lkv_prefill_workspace_bytes), then runs the attention over
- * it; both launches go on `stream`, and the workspace may be reused once the call has run.
+ * block and a flag per block (does some value exceed fp16's range) into the caller's workspace
+ * (lkv_prefill_workspace_bytes), then runs the attention over it (the fp16 instance, then the
+ * wide instance for the flagged tiles); all launches go on `stream`, and the workspace may be
+ * reused once the call has run.
  * ------------------------------------------------------------------------------------- */
 typedef struct lkv_prefill_args {
   int32_t struct_size; /* sizeof(lkv_prefill_args) */
@@ -273,8 +277,9 @@ typedef struct lkv_prefill_args {
 
 /* Workspace bytes lkv_prefill_attn needs for these args: the fp16 V of every key block of every
  * (sequence, kv head), 8 KiB per 32-token block (exact when the lengths and the ring start are
- * host constants, else bounded by the capacities), or with num_splits > 0 the decode kernel's
- * split states if those are larger.  Takes the same filled-in struct. */
+ * host constants, else bounded by the capacities), one flag byte per block (rows padded to 16
+ * bytes) and one 16-byte word; or the decode kernel's split states (ragged calls, or num_splits > 1)
+ * if those are larger.  Takes the same filled-in struct. */
 int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args *args);
 
 int32_t lkv_prefill_attn(const lkv_prefill_args *args, lkv_stream_t stream);

@@ -242,4 +242,10 @@ __device__ inline uint4 scale_frag(uint4 v, float s) {
 int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, int32_t col_lo,
                                  int32_t col_hi, hipStream_t s);
 
+// Split-state rows x splits a ragged call's decode-kernel class needs in the worst case over the
+// number n <= batch of its sequences (lmax query tokens each): the split count is `fixed` when
+// positive, else min(cap, ceil(cus / (n * num_kv_heads))); rows of one split count nothing.
+int64_t ragged_split_state_rows(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t lmax, int32_t cap,
+                                int32_t fixed, int32_t cus);
+
 }  // namespace lkv

@@ -42,9 +42,13 @@ struct DecodeParams {
   float scale_log2;
   // ragged query rows (short-prefill calls): sequence b's tokens are rows cu[b] .. cu[b + 1] - 1 of
   // q / out (nullptr: L tokens per sequence); rows = the call's total row count.  Only sequences
-  // with col_lo < tokens * group <= col_hi run in this launch.
+  // with col_lo < tokens * group <= col_hi run in this launch.  Their split count is `splits` when
+  // dyn_splits is 0, else chosen per launch on the device from the number n of sequences in the
+  // class, min(splits, ceil(cus / (n * Hkv))); their split states are laid out by the sequence's
+  // rank in the class, lmax token rows each.
   const int32_t* cu;
   int32_t rows, col_lo, col_hi;
+  int32_t dyn_splits, cus, lmax;
 };
 
 // Query tokens of sequence b (kMulti calls) and the flattened row of its token 0 (the q / out / lse
@@ -63,6 +67,27 @@ __device__ inline MultiRows multi_rows(const DecodeParams& p, int b) {
 __device__ inline bool in_column_class(const DecodeParams& p, int L) {
   const int cols = L * p.group;
   return L > 0 && cols > p.col_lo && cols <= p.col_hi;
+}
+
+// Ragged calls: the number of sequences in this launch's column class and b's rank among them (every
+// wave counts them itself, 64 sequences per ballot), and the class's split count.
+struct ClassRank {
+  int n, rank, splits;
+};
+
+__device__ inline ClassRank class_rank(const DecodeParams& p, int b, int hkv) {
+  const int lane = threadIdx.x & 63;
+  int n = 0, rank = 0;
+  for (int i0 = 0; i0 < p.batch; i0 += 64) {
+    const int i = i0 + lane;
+    const bool in = i < p.batch && in_column_class(p, multi_rows(p, i).L);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(in);
+    n += __builtin_popcountll(m);
+    if (b >= i0) rank += __builtin_popcountll(b - i0 >= 64 ? m : (m & ((uint64_t{1} << (b - i0)) - 1)));
+  }
+  int splits = p.splits;
+  if (p.dyn_splits && n > 0) splits = min(p.splits, max(1, (p.cus + n * hkv - 1) / (n * hkv)));
+  return ClassRank{n, rank, splits};
 }
 
 // The bf16 output of a normalised fp32 value x of kv head kvh: bf16(x), or bf16(bf16(x) * s) with
@@ -204,14 +229,22 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   const int G = p.group;
 
   // ragged calls: this sequence's query tokens (workgroup-uniform; sequences of another column
-  // class run in another launch)
+  // class run in another launch), the class's split count and this sequence's rows of split state
   const MultiRows mr = kMulti ? multi_rows(p, b) : MultiRows{1, b};
   if (kMulti && !in_column_class(p, mr.L)) return;
   const int Lq = mr.L;
+  int S = p.splits;
+  int64_t ws_row0 = mr.row0;  // split-state row of this sequence's token 0
+  if (kMulti && p.cu != nullptr) {
+    const ClassRank cr = class_rank(p, b, gridDim.y);
+    S = cr.splits;
+    ws_row0 = static_cast<int64_t>(cr.rank) * p.lmax;
+    if (split >= S) return;
+  }
 
   const SeqView sv = make_seq_view(p.seg, b, kvh);
   const int nbt = sv.nb0 + (sv.n1 > 0 ? (sv.lead + sv.n1 + kBlockTokens - 1) / kBlockTokens : 0);
-  const int bps = (nbt + p.splits - 1) / p.splits;
+  const int bps = (nbt + S - 1) / S;
   const int blk_begin = split * bps;
   const int blk_end = min(blk_begin + bps, nbt);
 
@@ -327,13 +360,13 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
       L += f * sm_l[w][hl];
       O += f * sm_o[w][hl][d];
     }
-    if (p.splits == 1) {
+    if (S == 1) {
       p.out[(kMulti && p.cu ? mr.row0 * p.out_st : b * p.out_sb) + (kMulti ? tq * p.out_st : 0) +
             static_cast<int64_t>(kvh * G + hh) * kHeadDim + d] =
           out_bits(L > 0.f ? O / L : 0.f, p.out_scale, kvh);
       if (p.lse != nullptr && d == 0) p.lse[row_q] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
     } else {
-      const int64_t row = row_q * p.splits + split;
+      const int64_t row = ((ws_row0 + tq) * p.hq + kvh * G + hh) * S + split;
       p.ws_o[row * kHeadDim + d] = O;
       if (d == 0) {
         p.ws_ml[row * 2] = M;
@@ -350,27 +383,11 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
 constexpr int kCombineThreads = kHeadDim;
 constexpr int kMaxSplits = 1024;
 
-__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const DecodeParams p) {
-  __shared__ float sm_w[kMaxSplits];
-  __shared__ float sm_red[kCombineThreads / 64];
-  const int bh = blockIdx.x;  // [rows, Hq] row
+// Merges the S split states (ml: (m, l) pairs, o: partial O rows) of one (query token, head) into
+// its output row and optional LSE; every thread of the block calls it (one per head dim).
+__device__ inline void combine_row(const DecodeParams& p, const float* ml, const float* o, int S, uint16_t* out_row,
+                                   float* lse, int kvh, float* sm_w, float* sm_red) {
   const int d = threadIdx.x;
-  const int row = bh / p.hq, h = bh % p.hq;
-  int b = row / p.L, tq = row % p.L;
-  if (p.cu != nullptr) {  // ragged: the sequence of this row (largest b with cu[b] <= row)
-    int lo = 0, hi = p.batch;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (p.cu[mid] <= row) lo = mid; else hi = mid;
-    }
-    b = lo;
-    const MultiRows mr = multi_rows(p, b);
-    tq = row - static_cast<int>(mr.row0);
-    if (tq < 0 || tq >= mr.L || !in_column_class(p, mr.L)) return;  // (uniform over the block)
-  }
-  const int S = p.splits;
-  const float* ml = p.ws_ml + static_cast<int64_t>(bh) * S * 2;
-  const float* o = p.ws_o + static_cast<int64_t>(bh) * S * kHeadDim;
   float mx = kNegInf;
   for (int s = d; s < S; s += kCombineThreads) {
     const float m = ml[2 * s];
@@ -403,9 +420,40 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const D
   }
   for (; s < S; ++s) O[0] += sm_w[s] * o[s * kHeadDim + d];
   const float Ot = (O[0] + O[1]) + (O[2] + O[3]);
-  p.out[(p.cu ? static_cast<int64_t>(row) * p.out_st : b * p.out_sb + tq * p.out_st) + static_cast<int64_t>(h) * kHeadDim + d] =
-      out_bits(L > 0.f ? Ot / L : 0.f, p.out_scale, h / p.group);
-  if (p.lse != nullptr && d == 0) p.lse[bh] = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
+  out_row[d] = out_bits(L > 0.f ? Ot / L : 0.f, p.out_scale, kvh);
+  if (lse != nullptr && d == 0) *lse = L > 0.f ? (M + __log2f(L)) * kLn2 : kNegInf;
+  __syncthreads();  // (sm_w and sm_red are reused by the caller's next row)
+}
+
+// Uniform calls: one block per [B, L, Hq] row.  Ragged calls: one block per (head, sequence) of the
+// launch's column class, over the sequence's query tokens (its split count and split-state rows come
+// from its rank in the class, as in the split kernel; with one split that kernel wrote the output).
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const DecodeParams p) {
+  __shared__ float sm_w[kMaxSplits];
+  __shared__ float sm_red[kCombineThreads / 64];
+  if (p.cu != nullptr) {
+    const int h = blockIdx.x, b = blockIdx.y;
+    const MultiRows mr = multi_rows(p, b);
+    if (!in_column_class(p, mr.L)) return;  // (uniform over the block)
+    const ClassRank cr = class_rank(p, b, p.hq / p.group);
+    const int S = cr.splits;
+    if (S == 1) return;
+    for (int tq = 0; tq < mr.L; ++tq) {
+      const int64_t ws_row = (static_cast<int64_t>(cr.rank) * p.lmax + tq) * p.hq + h;
+      const int64_t out_row = mr.row0 + tq;
+      combine_row(p, p.ws_ml + ws_row * S * 2, p.ws_o + ws_row * S * kHeadDim,
+                  S, p.out + out_row * p.out_st + static_cast<int64_t>(h) * kHeadDim,
+                  p.lse != nullptr ? p.lse + out_row * p.hq + h : nullptr, h / p.group, sm_w, sm_red);
+    }
+    return;
+  }
+  const int bh = blockIdx.x;  // [B, L, Hq] row
+  const int row = bh / p.hq, h = bh % p.hq;
+  const int b = row / p.L, tq = row % p.L;
+  const int S = p.splits;
+  combine_row(p, p.ws_ml + static_cast<int64_t>(bh) * S * 2, p.ws_o + static_cast<int64_t>(bh) * S * kHeadDim, S,
+              p.out + b * p.out_sb + tq * p.out_st + static_cast<int64_t>(h) * kHeadDim,
+              p.lse != nullptr ? p.lse + bh : nullptr, h / p.group, sm_w, sm_red);
 }
 
 // Key tokens a call can read per sequence (lengths read from device memory bounded by the
@@ -459,13 +507,24 @@ int32_t launch_decode(const DecodeParams& p, dim3 grid, bool vscale, bool nt, in
   }
   if (const int32_t st = check_launch(what)) return st;
   if (p.splits > 1) {
-    decode_combine_kernel<<<rows, kCombineThreads, 0, s>>>(p);
+    const dim3 grid = p.cu != nullptr ? dim3(p.hq, p.batch) : dim3(rows);
+    decode_combine_kernel<<<grid, kCombineThreads, 0, s>>>(p);
     return check_launch(what);
   }
   return LKV_OK;
 }
 
 }  // namespace
+
+int64_t ragged_split_state_rows(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t lmax, int32_t cap,
+                                int32_t fixed, int32_t cus) {
+  int64_t worst = 0;
+  for (int64_t n = 1; n <= batch; ++n) {
+    const int64_t S = fixed > 0 ? fixed : std::min<int64_t>(cap, (cus + n * num_kv_heads - 1) / (n * num_kv_heads));
+    if (S > 1) worst = std::max(worst, n * lmax * num_q_heads * S);
+  }
+  return worst;
+}
 
 int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, int32_t col_lo,
                                  int32_t col_hi, hipStream_t s) {
@@ -490,31 +549,53 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   p.col_hi = col_hi;
   p.causal = a->causal;
   p.scale_log2 = a->sm_scale * kLog2e;
+  const bool ragged = p.cu != nullptr;
+  // a ragged call's sequences of this class have at most lmax query tokens
+  p.lmax = ragged ? std::min(col_hi / group, p.L) : p.L;
+  if (p.lmax < 1) return LKV_OK;  // (no sequence fits the class)
   const int64_t tokens = call_key_tokens(a);
   const int64_t blocks = (tokens + 2 * kBlockTokens - 1) / kBlockTokens;  // (+1 for a ring start inside a block)
   const int64_t pairs = static_cast<int64_t>(a->batch) * a->num_kv_heads;
   const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  // about one workgroup per CU, at least 4 blocks per split, partial states within the workspace
-  int64_t splits = std::min<int64_t>({(cus + pairs - 1) / pairs, std::max<int64_t>(blocks / 4, 1), 1024});
-  // split-state rows: [rows, Hq] for ragged calls, [B, L, Hq] otherwise
-  const int64_t rows = (a->cu_seqlens_q ? static_cast<int64_t>(a->tokens) : static_cast<int64_t>(a->batch) * a->tokens) *
-                       a->num_q_heads;
+  p.cus = static_cast<int32_t>(cus);
+  // about one workgroup per CU, at least 4 blocks per split, partial states within the workspace; a
+  // ragged call's launch caps the count at what one sequence alone would take and each launch
+  // divides the CUs among the sequences it finds in its class
+  // (ragged: at most 8, because every class launch's grid carries that many splits for every sequence)
+  int64_t splits = std::min<int64_t>({ragged ? std::min<int64_t>((cus + a->num_kv_heads - 1) / a->num_kv_heads, 8)
+                                             : (cus + pairs - 1) / pairs,
+                                      std::max<int64_t>(blocks / 4, 1), 1024});
+  // split-state rows x splits: [B, L, Hq] rows for uniform calls, the class's sequences by rank
+  // (lmax rows each) for ragged ones
+  auto state = [&](int64_t cap, int32_t fixed) -> int64_t {
+    if (ragged) return ragged_split_state_rows(a->batch, a->num_q_heads, a->num_kv_heads, p.lmax, cap, fixed, p.cus);
+    const int64_t S = fixed > 0 ? fixed : cap;
+    return S > 1 ? static_cast<int64_t>(a->batch) * a->tokens * a->num_q_heads * S : 0;
+  };
   if (a->num_splits > 0) {  // fixed by the caller (lkv_prefill_workspace_bytes counted its states)
     splits = a->num_splits;
-    if (splits > 1 && rows * splits * (kHeadDim + 2) * 4 > a->workspace_bytes)
+    const int64_t need = state(splits, a->num_splits) * (kHeadDim + 2) * 4;
+    if (need > a->workspace_bytes)
       return fail(LKV_ERR_WORKSPACE, "prefill with %d decode splits needs %lld bytes of workspace, got %lld", a->num_splits,
-                  static_cast<long long>(rows * splits * (kHeadDim + 2) * 4), static_cast<long long>(a->workspace_bytes));
+                  static_cast<long long>(need), static_cast<long long>(a->workspace_bytes));
   }
-  while (splits > 1 && rows * splits * (kHeadDim + 2) * 4 > a->workspace_bytes) splits = (splits + 1) / 2;
+  while (splits > 1 && state(splits, a->num_splits > 0 ? static_cast<int32_t>(splits) : 0) * (kHeadDim + 2) * 4 >
+                           a->workspace_bytes)
+    splits = (splits + 1) / 2;
   p.splits = static_cast<int32_t>(splits);
-  p.ws_o = splits > 1 ? static_cast<float*>(a->workspace) : nullptr;
-  p.ws_ml = splits > 1 ? p.ws_o + rows * splits * kHeadDim : nullptr;
+  p.dyn_splits = ragged && a->num_splits == 0;
+  const int64_t state_rows = state(splits, a->num_splits > 0 ? static_cast<int32_t>(splits) : 0);
+  p.ws_o = state_rows > 0 ? static_cast<float*>(a->workspace) : nullptr;
+  p.ws_ml = state_rows > 0 ? p.ws_o + state_rows * kHeadDim : nullptr;
   const bool nt = use_nontemporal(0, pairs * tokens * kHeadDim * 2 * 2);
   // the instance holds the class's widest sequence: 16, 32 or 64 columns
   const int64_t cols = std::min<int64_t>(col_hi, static_cast<int64_t>(group) * p.L);
   const int cg = cols <= 16 ? 1 : cols <= 32 ? 2 : 4;
+  // combine grid: one block per output row ([rows, Hq] ragged, [B, L, Hq] uniform)
+  const int64_t out_rows = (ragged ? static_cast<int64_t>(a->tokens) : static_cast<int64_t>(a->batch) * a->tokens) *
+                           a->num_q_heads;
   return launch_decode(p, dim3(p.splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1, nt, cg,
-                       static_cast<int>(rows), s, "lkv_prefill_attn (short call on the decode kernel)");
+                       static_cast<int>(out_rows), s, "lkv_prefill_attn (short call on the decode kernel)");
 }
 
 }  // namespace lkv
@@ -572,6 +653,9 @@ int32_t run_decode(const lkv_decode_args* a, void* ws, int64_t ws_bytes, hipStre
   p.rows = a->batch;
   p.col_lo = 0;
   p.col_hi = 1 << 30;
+  p.dyn_splits = 0;
+  p.cus = 0;
+  p.lmax = 1;
   p.batch = a->batch;
   p.lse = a->lse;
   p.vscale = a->vscale;

@@ -43,10 +43,18 @@ struct PrefillParams {
   const float* vscale;
   const float* out_scale;  // [Hkv] or nullptr: out = bf16(bf16(o) * out_scale[kvh])
   int32_t L, hq, hkv, group, causal, tiles;
+  int32_t batch;
   float scale_log2;
   int32_t vscale_mode;
   uint16_t* v16;       // fp16 V of every key block, [B, Hkv, v16_blocks, 4096]
   int32_t v16_blocks;  // blocks per (sequence, kv head) in v16
+  // per key block of v16: 1 when some V value (older: bf16(V * s)) is finite with magnitude >= 65536,
+  // which fp16 cannot hold ([B, Hkv, vflag_stride] bytes after v16); the tiles that read such a block
+  // run on the wide instance instead (bf16 V, P as bf16 hi + lo)
+  uint8_t* vflags;
+  int32_t vflag_stride;
+  // set to 1 by the fp16 instance when it skips a tile for the wide one (cleared by the pre-pass)
+  int32_t* any_wide;
   // ragged query rows: sequence b's tokens are rows cu[b] .. cu[b + 1] - 1 of q / out (nullptr:
   // L tokens per sequence); rows = the call's total row count.  Sequences with at most
   // decode_rows query rows per kv head run on the decode kernel and are skipped here.
@@ -104,6 +112,13 @@ __device__ inline uint4 v_to_f16(uint4 v, float s) {
   return make_uint4(cv(v.x), cv(v.y), cv(v.z), cv(v.w));
 }
 
+// Whether either bf16 of a packed pair is finite with magnitude >= 65536 (exponent field 143-254):
+// fp16 cannot represent it (its largest finite value is 65504; bf16 has none between 65280 and 65536).
+__device__ inline bool f16_overflow(uint32_t w) {
+  const uint32_t e_lo = (w >> 7) & 0xffu, e_hi = (w >> 23) & 0xffu;
+  return (e_lo >= 143u && e_lo < 255u) || (e_hi >= 143u && e_hi < 255u);
+}
+
 __device__ inline uint32_t pack_f16_rne(float lo, float hi) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   h2 r;
@@ -155,25 +170,36 @@ __device__ inline const uint16_t* k_block(const SeqView& sv, int blk) {
   return uniform_ptr((blk < sv.nb0 ? sv.ok : sv.lk) + block_offset<kPaged>(sv, blk));
 }
 
+// Wave-uniform address of block blk's V in the cache (the wide instance reads bf16 V from there).
+template <bool kPaged>
+__device__ inline const uint16_t* v_block(const SeqView& sv, int blk) {
+  return uniform_ptr((blk < sv.nb0 ? sv.ov : sv.lv) + block_offset<kPaged>(sv, blk));
+}
+
 // kblk = k_block<kPaged>(sv, blk), computed by the caller outside the scheduled region (the page-table
-// lookup branches).
-template <int NW>
-__device__ inline void stage_load(Stage<NW>& st, const SegBase sb, const uint16_t* kblk, int blk, int wave,
-                                  int lane_off) {
+// lookup branches).  kWide: V (bf16) from the cache block vblk instead of the fp16 workspace.
+template <int NW, bool kWide = false>
+__device__ inline void stage_load(Stage<NW>& st, const SegBase sb, const uint16_t* kblk, const uint16_t* vblk, int blk,
+                                  int wave, int lane_off) {
   const int voff = blk * (kBlockElems * 2);
 #pragma unroll
   for (int j = 0; j < 16 / NW; ++j) {
     const int f = wave + j * NW;  // wave < NW, so f < 8 exactly when j < 8 / NW
-    const __amdgpu_buffer_rsrc_t r = j < 8 / NW ? make_rsrc(kblk, kBlockElems * 2) : make_rsrc(sb.v16, sb.v16_bytes);
-    const int off = (j < 8 / NW ? 0 : voff) + (f & 7) * 1024;
+    const bool is_k = j < 8 / NW;
+    const __amdgpu_buffer_rsrc_t r = is_k ? make_rsrc(kblk, kBlockElems * 2)
+                                          : (kWide ? make_rsrc(vblk, kBlockElems * 2) : make_rsrc(sb.v16, sb.v16_bytes));
+    const int off = (is_k || kWide ? 0 : voff) + (f & 7) * 1024;
     st.r[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, off, 0));
   }
 }
 
-template <int NW>
-__device__ inline void stage_store(const Stage<NW>& st, uint4* buf, int wave, int lane) {
+// kWide: the V fragments are bf16 from the cache; an older block's become bf16(V * vs) here (vs = 1:
+// unchanged), the value the V pre-pass gives the fp16 instance.
+template <int NW, bool kWide = false>
+__device__ inline void stage_store(const Stage<NW>& st, uint4* buf, int wave, int lane, float vs = 1.f) {
 #pragma unroll
-  for (int j = 0; j < 16 / NW; ++j) buf[(wave + j * NW) * 64 + lane] = st.r[j];
+  for (int j = 0; j < 16 / NW; ++j)
+    buf[(wave + j * NW) * 64 + lane] = (kWide && j >= 8 / NW) ? scale_frag(st.r[j], vs) : st.r[j];
 }
 
 // -inf for tokens outside the block's valid range or past the column's causal limit.
@@ -236,6 +262,21 @@ __device__ inline void probs_lo(const float (&pr)[8], const uint32_t (&w)[4], ui
   }
 }
 
+// The wide instance's probabilities: bf16 hi + lo of each (~16 bits, the decode kernel's split) and
+// the lane's largest (NaN-propagating).
+__device__ inline void probs_bf16(const float (&s)[8], float c, float mc, uint32_t (&hi)[4], uint32_t (&lo)[4],
+                                  float& pm) {
+  float pr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(s[j], c, -mc));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    hi[j] = pack_bf16x2(pr[2 * j], pr[2 * j + 1]);
+    lo[j] = pack_bf16x2(pr[2 * j] - bf16_lo(hi[j]), pr[2 * j + 1] - bf16_hi(hi[j]));
+  }
+  pm = max8(pr);
+}
+
 // The lane's largest packed fp16 probabilities of a block (one per half, NaN-propagating).
 __device__ inline uint32_t probs_max(uint32_t a, uint32_t b, uint32_t c) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -261,10 +302,12 @@ __device__ __attribute__((always_inline)) inline void unroll_steps(std::integer_
 // V pre-pass: every key block of every (sequence, kv head) as fp16 in block order [older |
 // local], with the older segment as bf16(V * s) (the reference's rounded _scale()).  The
 // attention kernel's query tiles then stage V as plain copies instead of each converting it.
+// Each block also gets its flag: whether some value does not fit fp16 (magnitude 65536 or more).
 // One workgroup per (block, kv head, sequence); 256 threads x 16 values.
 template <bool kPaged>
 __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
   const int blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  if ((blk | kvh | b) == 0 && threadIdx.x == 0) *p.any_wide = 0;  // (the tile kernels run after this one)
   if (!on_tile_path(p, seq_rows(p, b))) return;
   const SeqView sv = make_seq_view(p.seg, b, kvh);
   if (blk >= sv.nb0 + local_blocks(sv, sv.n1)) return;
@@ -272,13 +315,46 @@ __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
   const uint16_t* src = (older ? sv.ov : sv.lv) + block_offset<kPaged>(sv, blk);
   uint16_t* dst = p.v16 + ((static_cast<int64_t>(b) * p.hkv + kvh) * p.v16_blocks + blk) * kBlockElems;
   const float s = (p.vscale_mode && older) ? p.vscale[kvh] : 1.f;
+  bool over = false;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int e = (threadIdx.x + j * 256) * 8;
-    const uint4 x = *reinterpret_cast<const uint4*>(src + e);
-    // bf16(v * 1) == v, so the unscaled blocks take the same instructions
-    *reinterpret_cast<uint4*>(dst + e) = v_to_f16<true>(x, s);
+    // bf16(v * s); bf16(v * 1) == v, so the unscaled blocks take the same instructions
+    const uint4 y = scale_frag(*reinterpret_cast<const uint4*>(src + e), s);
+    over = over || f16_overflow(y.x) || f16_overflow(y.y) || f16_overflow(y.z) || f16_overflow(y.w);
+    *reinterpret_cast<uint4*>(dst + e) = make_uint4(f16x2_bits(bf16_lo(y.x), bf16_hi(y.x)),
+                                                    f16x2_bits(bf16_lo(y.y), bf16_hi(y.y)),
+                                                    f16x2_bits(bf16_lo(y.z), bf16_hi(y.z)),
+                                                    f16x2_bits(bf16_lo(y.w), bf16_hi(y.w)));
   }
+  const int any = __syncthreads_or(over);
+  if (threadIdx.x == 0) p.vflags[(static_cast<int64_t>(b) * p.hkv + kvh) * p.vflag_stride + blk] = any ? 1 : 0;
+}
+
+// Whether some block in [0, nbt) of (b, kvh) holds a V value fp16 cannot (the pre-pass's flags),
+// read 16 flags per load over the wave.
+__device__ inline bool tile_needs_wide(const PrefillParams& p, int b, int kvh, int nbt) {
+  const uint8_t* f = p.vflags + (static_cast<int64_t>(b) * p.hkv + kvh) * p.vflag_stride;
+  const int lane = threadIdx.x & 63;
+  bool any = false;
+  for (int i = lane * 16; i < nbt; i += 64 * 16) {
+    uint4 w = *reinterpret_cast<const uint4*>(f + i);
+    // flags past nbt (other blocks of the row, or padding) do not count
+    const int valid = min(16, nbt - i);
+    if (valid < 16) {
+      uint32_t* ww = reinterpret_cast<uint32_t*>(&w);
+      for (int k = valid; k < 16; ++k) ww[k >> 2] &= ~(0xffu << (8 * (k & 3)));
+    }
+    any |= (w.x | w.y | w.z | w.w) != 0;
+  }
+  return __builtin_amdgcn_ballot_w64(any) != 0;
+}
+
+// Whether some key block of (b, kvh) holds a V value fp16 cannot, over all nb of its blocks.
+__device__ inline bool pair_needs_wide(const PrefillParams& p, int b, int kvh) {
+  if (!on_tile_path(p, seq_rows(p, b))) return false;  // (the pre-pass wrote no flags for it)
+  const SeqView sv = make_seq_view(p.seg, b, kvh);
+  return tile_needs_wide(p, b, kvh, sv.nb0 + local_blocks(sv, sv.n1));
 }
 
 constexpr int kTileRing = 4;       // LDS block buffers of the tile kernel
@@ -293,10 +369,13 @@ constexpr int kTileBuf = 1024;     // uint4 per block buffer (16 KiB)
 // The 2-wave instance (calls of at most 64 query rows per kv head, bound by HBM, not by the matrix
 // pipe) splits P into fp16 hi + lo and runs P V twice, so its probabilities carry ~22 bits
 // instead of 11.  prefill_tile runs one query tile (logical index = (sequence, kv head, tile)).
-template <int NW, int CG, bool kPaged>
+// kWide: the instance for tiles whose V does not fit fp16 (the pre-pass flagged one of their blocks):
+// V staged as bf16 from the caches (older blocks as bf16(V * s)), P split into bf16 hi + lo, P V and
+// the row sums on bf16 MFMAs; the fp16 instance skips those tiles and this one runs only them.
+template <int NW, int CG, bool kPaged, bool kWide = false>
 __device__ __attribute__((always_inline)) inline void prefill_tile(const PrefillParams& p, const int logical,
                                                                    uint4* lds) {
-  constexpr bool kSplitP = NW == 2;
+  constexpr bool kSplitP = NW == 2 || kWide;
   constexpr int kStages = 2;  // register stage sets (global loads run kStages steps ahead of their LDS store)
   constexpr int kDist = 2;    // step i stores block i + kDist into the LDS ring
   constexpr int kRing = kTileRing;
@@ -327,6 +406,12 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   sv.lead = __builtin_amdgcn_readfirstlane(sv.lead);
   const int wg_last_row = min(rows_total, wg_row0 + kRowsPerWg) - 1;
   const int nbt = __builtin_amdgcn_readfirstlane(sv.nb0 + local_blocks(sv, visible_local(p, sv, sr.L, wg_last_row / G)));
+  // The tiles that read a V block fp16 cannot hold belong to the wide instance: it leaves the other
+  // tiles at once, and the fp16 instance leaves these at its prologue's barrier, so that the flag
+  // load overlaps its first loads.  (Both workgroup-uniform.)
+  const bool needs_wide = tile_needs_wide(p, b, kvh, nbt);
+  if (kWide && !needs_wide) return;
+  const float vs_older = p.vscale_mode ? p.vscale[kvh] : 1.f;  // (the wide instance's V scale)
 
   uint4 qf[CG][4];
   int lim[CG];  // last visible local-segment token of this lane's column
@@ -357,6 +442,7 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   // accumulated on the matrix pipe as P times a tile of ones (each lane holds its row's sum).
   f32x4 o[CG][8], ol[CG];
   const uint4 kOnes = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
+  const uint4 kOnesBf16 = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) {
     ol[cg] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -374,14 +460,22 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
     const int last = nbt - 1;
 
     Stage<NW> sets[kStages];
+    // (the V blocks of the wide instance; the fp16 instance reads V from the workspace)
+    auto vb = [&](int blk) __attribute__((always_inline)) { return kWide ? v_block<kPaged>(sv, blk) : nullptr; };
+    auto vs_of = [&](int blk) __attribute__((always_inline)) { return kWide && blk < sv.nb0 ? vs_older : 1.f; };
 #pragma unroll
     for (int j = 0; j < kStages; ++j)
-      stage_load<NW>(sets[j], rsrc, k_block<kPaged>(sv, min(j, last)), min(j, last), wave, lane_off);
+      stage_load<NW, kWide>(sets[j], rsrc, k_block<kPaged>(sv, min(j, last)), vb(min(j, last)), min(j, last), wave,
+                            lane_off);
 #pragma unroll
     for (int j = 0; j < kDist; ++j) {
-      stage_store<NW>(sets[j % kStages], lds + j * kBuf, wave, lane);
+      stage_store<NW, kWide>(sets[j % kStages], lds + j * kBuf, wave, lane, vs_of(min(j, last)));
       const int lb = min(j + kStages, last);
-      stage_load<NW>(sets[j % kStages], rsrc, k_block<kPaged>(sv, lb), lb, wave, lane_off);
+      stage_load<NW, kWide>(sets[j % kStages], rsrc, k_block<kPaged>(sv, lb), vb(lb), lb, wave, lane_off);
+    }
+    if (!kWide && needs_wide) {
+      if (threadIdx.x == 0) *p.any_wide = 1;
+      return;
     }
     __syncthreads();
 
@@ -439,6 +533,8 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
       Stage<NW>& st = sets[(R + kDist) % kStages];
       const int ld_blk = min(blk + kDist + kStages, last);
       const uint16_t* ld_k = k_block<kPaged>(sv, ld_blk);
+      const uint16_t* ld_v = vb(ld_blk);
+      const float st_vs = vs_of(min(blk + kDist, last));  // (the block st holds)
       uint4 kf[8];
 #pragma unroll
       for (int t = 0; t < 8; ++t) kf[t] = nxt[t * 64 + lane];
@@ -470,13 +566,20 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
         }
       uint32_t pw[CG][4], pl[CG][4];
       uint32_t pmax;  // the lane's largest probabilities of this block (packed fp16)
+      float pmf = 0.f;  // (the wide instance: the largest as fp32)
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) {
-        float pr[8];
-        probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
-        if (kSplitP) probs_lo(pr, pw[cg], pl[cg]);
-        pmax = cg == 0 ? probs_max(pw[cg][0], pw[cg][1], probs_max(pw[cg][2], pw[cg][3], pw[cg][3]))
-                       : probs_max(pmax, probs_max(pw[cg][0], pw[cg][1], pw[cg][2]), pw[cg][3]);
+        if constexpr (kWide) {
+          float pm;
+          probs_bf16(s[cg], c, rs[cg].mc, pw[cg], pl[cg], pm);
+          pmf = fmax_nan(pmf, pm);
+        } else {
+          float pr[8];
+          probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
+          if (kSplitP) probs_lo(pr, pw[cg], pl[cg]);
+          pmax = cg == 0 ? probs_max(pw[cg][0], pw[cg][1], probs_max(pw[cg][2], pw[cg][3], pw[cg][3]))
+                         : probs_max(pmax, probs_max(pw[cg][0], pw[cg][1], pw[cg][2]), pw[cg][3]);
+        }
       }
       uint4 vf[8];
 #pragma unroll
@@ -493,29 +596,47 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
         __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);  // exp
       }
       // a new row maximum: exact maxima, rescale, recompute this block's P
-      if (__builtin_amdgcn_ballot_w64(probs_overflow(pmax))) {
+      if (__builtin_amdgcn_ballot_w64(kWide ? !(pmf < 512.f) : probs_overflow(pmax))) {
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
           raise_rows(rs[cg], max8(s[cg]), c, o[cg], ol[cg]);
-          float pr[8];
-          probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
-          if (kSplitP) probs_lo(pr, pw[cg], pl[cg]);
+          if constexpr (kWide) {
+            float pm;
+            probs_bf16(s[cg], c, rs[cg].mc, pw[cg], pl[cg], pm);
+          } else {
+            float pr[8];
+            probs(s[cg], c, rs[cg].mc, pr, pw[cg]);
+            if (kSplitP) probs_lo(pr, pw[cg], pl[cg]);
+          }
         }
       }
 #pragma unroll
       for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
         for (int cg = 0; cg < CG; ++cg) {
-          o[cg][nb] = mfma_f16(vf[nb], make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]), o[cg][nb]);
-          if (kSplitP) o[cg][nb] = mfma_f16(vf[nb], make_uint4(pl[cg][0], pl[cg][1], pl[cg][2], pl[cg][3]), o[cg][nb]);
+          const uint4 ph = make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]);
+          if constexpr (kWide) {
+            o[cg][nb] = mfma_bf16(vf[nb], ph, o[cg][nb]);
+            o[cg][nb] = mfma_bf16(vf[nb], make_uint4(pl[cg][0], pl[cg][1], pl[cg][2], pl[cg][3]), o[cg][nb]);
+          } else {
+            o[cg][nb] = mfma_f16(vf[nb], ph, o[cg][nb]);
+            if constexpr (kSplitP)
+              o[cg][nb] = mfma_f16(vf[nb], make_uint4(pl[cg][0], pl[cg][1], pl[cg][2], pl[cg][3]), o[cg][nb]);
+          }
         }
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg) {
-        ol[cg] = mfma_f16(kOnes, make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]), ol[cg]);
-        if (kSplitP) ol[cg] = mfma_f16(kOnes, make_uint4(pl[cg][0], pl[cg][1], pl[cg][2], pl[cg][3]), ol[cg]);
+        const uint4 ph = make_uint4(pw[cg][0], pw[cg][1], pw[cg][2], pw[cg][3]);
+        if constexpr (kWide) {
+          ol[cg] = mfma_bf16(kOnesBf16, ph, ol[cg]);
+          ol[cg] = mfma_bf16(kOnesBf16, make_uint4(pl[cg][0], pl[cg][1], pl[cg][2], pl[cg][3]), ol[cg]);
+        } else {
+          ol[cg] = mfma_f16(kOnes, ph, ol[cg]);
+          if constexpr (kSplitP) ol[cg] = mfma_f16(kOnes, make_uint4(pl[cg][0], pl[cg][1], pl[cg][2], pl[cg][3]), ol[cg]);
+        }
       }
-      stage_store<NW>(st, wr, wave, lane);
-      stage_load<NW>(st, rsrc, ld_k, ld_blk, wave, lane_off);
+      stage_store<NW, kWide>(st, wr, wave, lane, st_vs);
+      stage_load<NW, kWide>(st, rsrc, ld_k, ld_v, ld_blk, wave, lane_off);
 #pragma unroll
       for (int i = 0; i < (kSplitP ? 18 : 9) * CG; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA (P V and P 1 of block i)
@@ -574,9 +695,32 @@ template <int NW, int CG, int WPE, bool kPaged>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_kernel(
     const PrefillParams p) {
   __shared__ uint4 lds[kTileRing * kTileBuf];
-  const int logical = xcd_logical_index(blockIdx.x, gridDim.x);
+  // (a ragged call's grid covers every sequence at the longest one's tile count, and most of it
+  // exits: round-robin over the XCDs spreads the tiles that work over all of them)
+  const int logical = p.cu != nullptr ? static_cast<int>(blockIdx.x) : xcd_logical_index(blockIdx.x, gridDim.x);
   const int tile = logical % p.tiles;
   prefill_tile<NW, CG, kPaged>(p, logical - tile + (p.causal ? p.tiles - 1 - tile : tile), lds);
+}
+
+// The wide instance: one workgroup per (sequence, kv head) pair at a time, min(pairs, CUs) of them.
+// Unless the fp16 instance skipped a tile, every workgroup exits after one load (the launch costs a
+// few microseconds instead of a full grid of tile workgroups that each check their flags and exit).
+// Otherwise a pair none of whose V blocks the pre-pass flagged is skipped after one flag scan, and a
+// flagged pair's tiles run here one after another, each tile again checking whether its own blocks
+// reach a flagged one (the fp16 instance ran the others).
+template <int NW, int CG, int WPE, bool kPaged>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_wide_kernel(
+    const PrefillParams p) {
+  __shared__ uint4 lds[kTileRing * kTileBuf];
+  if (*p.any_wide == 0) return;  // the fp16 instance ran every tile (workgroup-uniform)
+  const int pairs = p.batch * p.hkv;
+  for (int pair = blockIdx.x; pair < pairs; pair += gridDim.x) {
+    if (!pair_needs_wide(p, pair / p.hkv, pair % p.hkv)) continue;  // (workgroup-uniform)
+    for (int tile = 0; tile < p.tiles; ++tile) {
+      prefill_tile<NW, CG, kPaged, true>(p, pair * p.tiles + tile, lds);
+      __syncthreads();  // the next tile's staging reuses the LDS ring
+    }
+  }
 }
 
 }  // namespace
@@ -601,16 +745,75 @@ int64_t v16_blocks(const lkv_prefill_args* a) {
   return (n0 + kBlockTokens - 1) / kBlockTokens + lblocks;
 }
 
+// Bytes of the V pre-pass's output: the fp16 V blocks, then one overflow flag per block (rows of a
+// multiple of 16 bytes per (sequence, kv head)), then a 16-byte word that says whether the fp16
+// tile instance skipped a tile.
+int64_t v16_region_bytes(const lkv_prefill_args* a, int64_t vblocks) {
+  const int64_t heads = static_cast<int64_t>(a->batch) * a->num_kv_heads;
+  return heads * vblocks * (lkv::kBlockElems * 2) + heads * ((vblocks + 15) / 16 * 16) + 16;
+}
+
 }  // namespace
 
 extern "C" int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args* a) {
-  if (a == nullptr || a->batch <= 0 || a->num_kv_heads <= 0) return 0;
-  const int64_t v16 = static_cast<int64_t>(a->batch) * a->num_kv_heads * v16_blocks(a) * (lkv::kBlockElems * 2);
+  using namespace lkv;
+  if (a == nullptr || a->batch <= 0 || a->num_kv_heads <= 0 || a->num_q_heads <= 0) return 0;
+  const int64_t v16 = v16_region_bytes(a, v16_blocks(a));
+  const int64_t per_row = (kHeadDim + 2) * 4;  // one split state
+  if (a->cu_seqlens_q != nullptr && a->tile_waves == 0 && a->max_seqlen_q >= 1 && a->tokens > 0) {
+    // a ragged call's decode-kernel classes: split states of their sequences, by rank in the class
+    const int group = a->num_q_heads / a->num_kv_heads;
+    const int L = std::min(a->max_seqlen_q, a->tokens);
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const int cap = std::min(8, (cus + a->num_kv_heads - 1) / a->num_kv_heads);
+    int64_t states = 0;
+    for (const int col_hi : {16, 32, 64}) {
+      const int lmax = std::min(col_hi / std::max(group, 1), L);
+      if (lmax >= 1)
+        states = std::max(states, ragged_split_state_rows(a->batch, a->num_q_heads, a->num_kv_heads, lmax, cap,
+                                                          a->num_splits, cus));
+    }
+    return std::max(v16, states * per_row);
+  }
   if (a->num_splits <= 1) return v16;
-  // split states of the decode kernel's sequences: [rows, Hq] (ragged) or [B, L, Hq] rows
-  const int64_t rows = (a->cu_seqlens_q ? int64_t{1} : static_cast<int64_t>(a->batch)) * std::max(a->tokens, 0) *
-                       a->num_q_heads;
-  return std::max(v16, rows * a->num_splits * (lkv::kHeadDim + 2) * 4);
+  // split states of the decode kernel's sequences: [B, L, Hq] rows
+  return std::max(v16, static_cast<int64_t>(a->batch) * std::max(a->tokens, 0) * a->num_q_heads * a->num_splits * per_row);
+}
+
+// The tile kernel instance for this call's wave count and addressing.
+void launch_tiles(int waves, bool paged, dim3 grid, const lkv::PrefillParams& p, hipStream_t s) {
+  using namespace lkv;
+  if (waves == 8 && paged)
+    prefill_kernel<8, 2, 2, true><<<grid, 8 * 64, 0, s>>>(p);
+  else if (waves == 8)
+    prefill_kernel<8, 2, 2, false><<<grid, 8 * 64, 0, s>>>(p);
+  else if (waves == 4 && paged)
+    prefill_kernel<4, 2, 2, true><<<grid, 4 * 64, 0, s>>>(p);
+  else if (waves == 4)
+    prefill_kernel<4, 2, 2, false><<<grid, 4 * 64, 0, s>>>(p);
+  else if (paged)
+    prefill_kernel<2, 2, 1, true><<<grid, 2 * 64, 0, s>>>(p);
+  else
+    prefill_kernel<2, 2, 1, false><<<grid, 2 * 64, 0, s>>>(p);
+}
+
+// The wide-range V instance for the same wave count and addressing, over `pair_wgs` workgroups
+// (4-wave tiles at one wave per SIMD: the bf16 instance needs more than 256 registers).
+void launch_wide(int waves, bool paged, int pair_wgs, const lkv::PrefillParams& p, hipStream_t s) {
+  using namespace lkv;
+  const dim3 grid(static_cast<unsigned>(pair_wgs));
+  if (waves == 8 && paged)
+    prefill_wide_kernel<8, 2, 2, true><<<grid, 8 * 64, 0, s>>>(p);
+  else if (waves == 8)
+    prefill_wide_kernel<8, 2, 2, false><<<grid, 8 * 64, 0, s>>>(p);
+  else if (waves == 4 && paged)
+    prefill_wide_kernel<4, 2, 1, true><<<grid, 4 * 64, 0, s>>>(p);
+  else if (waves == 4)
+    prefill_wide_kernel<4, 2, 1, false><<<grid, 4 * 64, 0, s>>>(p);
+  else if (paged)
+    prefill_wide_kernel<2, 2, 1, true><<<grid, 2 * 64, 0, s>>>(p);
+  else
+    prefill_wide_kernel<2, 2, 1, false><<<grid, 2 * 64, 0, s>>>(p);
 }
 
 extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stream) {
@@ -692,6 +895,9 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.vscale_mode = a->older_vscale_mode;
   p.v16 = static_cast<uint16_t*>(a->workspace);
   p.v16_blocks = static_cast<int32_t>(vblocks);
+  p.vflag_stride = static_cast<int32_t>((vblocks + 15) / 16 * 16);
+  p.vflags = static_cast<uint8_t*>(a->workspace) + static_cast<int64_t>(a->batch) * a->num_kv_heads * vblocks * (kBlockElems * 2);
+  p.any_wide = reinterpret_cast<int32_t*>(p.vflags + static_cast<int64_t>(a->batch) * a->num_kv_heads * p.vflag_stride);
   p.cu = a->cu_seqlens_q;
   p.rows = a->tokens;
   p.decode_rows = ragged && short_on_decode ? 64 : -1;
@@ -702,10 +908,14 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   // grid still leaves at most one workgroup per CU, which keeps twice the CUs busy (measured on 256
   // CUs: at B = 1 of a config-3 piece 23 vs 18 %; from B = 2 up the 8-wave tile is 0.5-1.5 points ahead).
   // A ragged call sizes the grid by its longest sequence; the tiles past a sequence's own rows exit.
+  // It takes 4-wave tiles: the host does not know how many of its sequences are long, and a step of
+  // decode rows and one or two prefill pieces would leave half the CUs idle with 8-wave tiles.
   const bool wide = rows > 64;
   int waves = wide ? 8 : 2;
   if (wide && a->tile_waves != 0) {
     waves = a->tile_waves;
+  } else if (wide && ragged) {
+    waves = 4;
   } else if (wide) {
     const int64_t cus = device_cu_count();
     const int64_t wgs4 = (rows + 127) / 128 * heads;
@@ -717,6 +927,7 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   LKV_REQUIRE(wgs < (1LL << 31), "too many query rows");
   p.tiles = static_cast<int32_t>(tiles);
   p.hkv = a->num_kv_heads;
+  p.batch = a->batch;
   const bool paged = a->older_block_table != nullptr || a->local_block_table != nullptr;
   if (vblocks > 0) {  // (no keys at all: every row's output is zero; the main kernel skips its loop)
     const dim3 vgrid(static_cast<unsigned>(vblocks), a->num_kv_heads, a->batch);
@@ -727,17 +938,13 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
     if (const int32_t e = check_launch("lkv_prefill_attn (V pre-pass)")) return e;
   }
   const dim3 grid(static_cast<unsigned>(wgs));
-  if (waves == 8 && paged)
-    prefill_kernel<8, 2, 2, true><<<grid, 8 * 64, 0, s>>>(p);
-  else if (waves == 8)
-    prefill_kernel<8, 2, 2, false><<<grid, 8 * 64, 0, s>>>(p);
-  else if (waves == 4 && paged)
-    prefill_kernel<4, 2, 2, true><<<grid, 4 * 64, 0, s>>>(p);
-  else if (waves == 4)
-    prefill_kernel<4, 2, 2, false><<<grid, 4 * 64, 0, s>>>(p);
-  else if (paged)
-    prefill_kernel<2, 2, 1, true><<<grid, 2 * 64, 0, s>>>(p);
-  else
-    prefill_kernel<2, 2, 1, false><<<grid, 2 * 64, 0, s>>>(p);
-  return check_launch("lkv_prefill_attn");
+  launch_tiles(waves, paged, grid, p, s);
+  if (const int32_t e = check_launch("lkv_prefill_attn")) return e;
+  if (vblocks == 0) return LKV_OK;
+  // the tiles that read a V value of magnitude 65536 or more (flagged by the pre-pass; the instance
+  // above skipped them), exactly in bf16, by workgroups that each scan one (sequence, kv head)'s
+  // flags at a time
+  const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  launch_wide(waves, paged, static_cast<int>(std::min(heads, cus)), p, s);
+  return check_launch("lkv_prefill_attn (wide-range V)");
 }

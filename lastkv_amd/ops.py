@@ -511,14 +511,36 @@ def prefill_workspace_bytes(batch: int, kv_heads: int, older_tokens: int, local_
     ``local_tokens`` keys (``local_lead``: the ring start's offset inside its 32-token block)."""
 
     blocks = -(-older_tokens // 32) + (-(-(local_lead + local_tokens) // 32) if local_tokens > 0 else 0)
-    return batch * kv_heads * blocks * 8192
+    # fp16 V of every block, then one flag byte per block (rows padded to 16 bytes), then one 16-byte word
+    return batch * kv_heads * (blocks * 8192 + -(-blocks // 16) * 16) + 16
 
 
 def prefill_split_state_bytes(rows: int, num_q_heads: int, num_splits: int) -> int:
-    """Workspace a prefill call with a fixed ``num_splits`` > 1 needs for the decode kernel's split
-    states of ``rows`` query tokens (the call's total rows)."""
+    """Workspace a uniform prefill call with a fixed ``num_splits`` > 1 needs for the decode kernel's
+    split states of ``rows`` query tokens (batch x tokens)."""
 
     return 0 if num_splits <= 1 else rows * num_q_heads * num_splits * (HEAD_DIM + 2) * 4
+
+
+def ragged_split_state_bytes(batch: int, num_q_heads: int, num_kv_heads: int, max_seqlen: int, num_splits: int,
+                             cu_count: int) -> int:
+    """Upper bound of the split states a ragged prefill call keeps for its sequences of at most 64
+    query rows per kv head (what ``lkv_prefill_workspace_bytes`` adds for them): per column class
+    (16, 32, 64 columns) the worst case over the number n of its sequences of n * lmax * Hq * S(n)
+    states, S(n) = ``num_splits`` or min(8, ceil(CUs / Hkv), ceil(CUs / (n Hkv)))."""
+
+    group = num_q_heads // num_kv_heads
+    cap = min(8, -(-cu_count // num_kv_heads))
+    worst = 0
+    for col_hi in (16, 32, 64):
+        lmax = min(col_hi // group, max_seqlen)
+        if lmax < 1:
+            continue
+        for n in range(1, batch + 1):
+            S = num_splits if num_splits > 0 else min(cap, -(-cu_count // (n * num_kv_heads)))
+            if S > 1:
+                worst = max(worst, n * lmax * num_q_heads * S)
+    return worst * (HEAD_DIM + 2) * 4
 
 
 def merge_states(

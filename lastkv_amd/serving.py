@@ -384,7 +384,11 @@ class LastKVFastPath:
             # and the whole ring (a ragged call's short rows share it for their split state)
             width = max(1, -(-max(r.older for r in parsed) // BLOCK))
             need = ops.prefill_workspace_bytes(B, P.kv_heads, width * BLOCK, P.ring_tokens)
-            need = max(need, ops.prefill_split_state_bytes(self.tokens, Hq, self.num_splits or 0))
+            if uniform:
+                need = max(need, ops.prefill_split_state_bytes(self.tokens, Hq, self.num_splits or 0))
+            else:
+                need = max(need, ops.ragged_split_state_bytes(B, Hq, P.kv_heads, max(r.tokens for r in parsed),
+                                                              self.num_splits or 0, ops._cu_count(P.device)))
             if self._prefill_ws.numel() < need:
                 self._prefill_ws = torch.empty(need, dtype=torch.uint8, device=P.device)
         if self._q_out.shape[0] < self.tokens:

@@ -220,7 +220,8 @@ def test_prefill_workspace_contract():
     q = torch.zeros((B, 40, Hq, 128), dtype=torch.bfloat16, device=DEV)
     kw = dict(older=older, older_len=100, local=ring, local_len=40, local_start=70)
     need = ops.prefill_workspace_bytes(B, Hkv, 100, 40, 70 % 32)
-    assert need == B * Hkv * (4 + 2) * 8192
+    # fp16 V of 6 blocks, a 16-byte row of block flags per (sequence, kv head), one 16-byte word
+    assert need == B * Hkv * ((4 + 2) * 8192 + 16) + 16
     ops.prefill_attention(q, workspace=torch.empty(need, dtype=torch.uint8, device=DEV), **kw)
     with pytest.raises(ValueError, match="workspace"):
         ops.prefill_attention(q, workspace=torch.empty(need - 8192, dtype=torch.uint8, device=DEV), **kw)
