@@ -34,6 +34,13 @@ Printed JSON line (one, from this single process):
                                       then greedy decode steps, tok/s of each, through the
                                       drop-in model (eager) and through the serving path (paged
                                       pool, decode steps replayed from one HIP graph)
+                 config4_e2e_8b       the same model at B=4: a 131072-token prompt in 4096-token
+                                      calls, then 128 greedy decode steps, against the 10.6 ms
+                                      per-step HBM bound
+                 mixed_step           one ragged serving step at the 8B attention shape (31 decode
+                                      rows at 8K context + a 1024-token and a 7-token prefill row):
+                                      the single varlen epilogue + attention launch per layer
+                                      against the same rows called one by one
 """
 
 from __future__ import annotations
@@ -77,7 +84,7 @@ def parse_args():
                     help="skip the config 4 (128K decode), config 5 (Wan) and config 3 (8B end to end) measurements")
     ap.add_argument("--decode-steps", type=int, default=256, help="greedy decode steps of the config 3 model run")
     ap.add_argument("--only", choices=["prefill", "short", "config4", "config4p", "config5", "config3", "epilogue",
-                                       "peaks"],
+                                       "peaks", "config4e2e", "mixed"],
                     default=None,
                     help="run one secondary measurement alone and print its JSON (for profiling); "
                          "this is not the bench line")
@@ -389,20 +396,15 @@ def wan_measurement(ops, torch, dev) -> dict:
     }
 
 
-def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
-    """BASELINE config 3 end to end through the drop-in model (lastkv_amd.llm): 8B geometry
-    (32 layers, 4096, 32 / 8 heads, FFN 14336, vocab 128256, llama3 RoPE theta 500000), random
-    N(0, 0.02) bf16 weights, B = 32, an 8192-token uniform-random prompt prefilled in 2048-token
-    calls (C = 1024), then greedy decode steps feeding one new token per sequence.  Eager PyTorch
-    host loop; projections / MLP / norms / lm_head are torch (hipBLASLt) ops, attention and cache
-    writes are this library's kernels."""
+def build_8b_model(torch, dev):
+    """The 8B-shape LastKV model (32 layers, 4096, 32 / 8 heads, FFN 14336, vocab 128256, llama3 RoPE
+    theta 500000, C = 1024) with random N(0, 0.02) bf16 weights (seed 0), on the GPU."""
 
-    from lastkv_amd.llm import CustomRecurrentMarinAKV254ReuseKVForCausalLM, LastKVCache, LastKVConfig
+    from lastkv_amd.llm import CustomRecurrentMarinAKV254ReuseKVForCausalLM, LastKVConfig
 
-    Bm, prompt, call = 32, 8192, 2048
     cfg = LastKVConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
                        num_attention_heads=32, num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-5,
-                       rope_theta=500000.0, max_position_embeddings=131072, chunk_size=CHUNK,
+                       rope_theta=500000.0, max_position_embeddings=131072 + 1024, chunk_size=CHUNK,
                        rope_scaling={"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
                                      "high_freq_factor": 4.0, "original_max_position_embeddings": 8192})
     default = torch.get_default_dtype()
@@ -412,7 +414,201 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
             model = CustomRecurrentMarinAKV254ReuseKVForCausalLM(cfg)
     finally:
         torch.set_default_dtype(default)
-    model = model.to(dev, torch.bfloat16).init_weights(torch.Generator(device=dev).manual_seed(0)).eval()
+    return model.to(dev, torch.bfloat16).init_weights(torch.Generator(device=dev).manual_seed(0)).eval()
+
+
+def e2e_config4_measurement(torch, dev, model, decode_steps: int = 128) -> dict:
+    """BASELINE config 4 end to end: the 8B-shape model at B = 4, a 131072-token uniform-random
+    prompt prefilled in 4096-token calls (each cut into 4 chunk pieces of C = 1024 against the
+    last-layer cache) through the drop-in model, then greedy decode steps (eager host loop); and the
+    serving path (1024-token rows on the paged pool, decode steps replayed from one HIP graph).
+    The HBM bound of a decode step: 16.06 GB of weights + 32 layer-calls reading 2.147 GB of K / V
+    each = 84.8 GB, 10.6 ms at 8 TB/s."""
+
+    from lastkv_amd.llm import LastKVCache
+    from lastkv_amd.serving import LastKVServingModel
+
+    cfg = model.config
+    Bm, prompt, call = 4, 131072, 4096
+    ids = torch.randint(0, cfg.vocab_size, (Bm, prompt), generator=torch.Generator().manual_seed(3)).to(dev)
+    params = sum(p.numel() for p in model.parameters())
+    kv_bytes = 2 * Bm * cfg.num_key_value_heads * (prompt + decode_steps // 2) * 128 * 2
+    bound_ms = (params * 2 + cfg.num_hidden_layers * kv_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3
+    cache = LastKVCache(cfg.num_hidden_layers, CHUNK, capacity_tokens=prompt + decode_steps)
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(0, prompt, call):
+            out = model(ids[:, s:s + call], past_key_values=cache, logits_to_keep=1)
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        hf_logits = out.logits[:, -1].float()
+        tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(decode_steps):
+            out = model(tok, past_key_values=cache, logits_to_keep=1)
+            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        torch.cuda.synchronize()
+        t_decode = time.perf_counter() - t0
+    del cache, out
+    torch.cuda.empty_cache()
+    runner = LastKVServingModel(model, max_batch=Bm, max_tokens_per_slot=prompt + decode_steps + 1)
+    slots = [runner.add_sequence() for _ in range(Bm)]
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(0, prompt, CHUNK):
+            logits = runner.step([(slot, ids[b, s:s + CHUNK]) for b, slot in enumerate(slots)])
+        torch.cuda.synchronize()
+        t_sprefill = time.perf_counter() - t0
+        sv_logits = logits.float()
+        tok = logits.argmax(-1)
+        graph = runner.decode_graph(slots)
+        _, tok = graph.step(tok)  # capture + first replay, untimed
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(decode_steps - 1):
+            _, tok = graph.step(tok)
+        torch.cuda.synchronize()
+        t_sdecode = time.perf_counter() - t0
+    del runner, graph
+    torch.cuda.empty_cache()
+    dec_ms, sdec_ms = t_decode * 1e3 / decode_steps, t_sdecode * 1e3 / (decode_steps - 1)
+    return {
+        "workload": f"config 4: 8B-shape LastKV model, B={Bm}, {prompt}-token prompt in {call}-token calls (C=1024), "
+                    f"then {decode_steps} greedy decode steps",
+        "decode_bound_ms_per_step": round(bound_ms, 3),
+        "hf_path": {
+            "how": "drop-in lastkv_amd.llm model, 4096-token prefill calls, eager host loop",
+            "prefill_s": round(t_prefill, 3), "prefill_tok_s": round(Bm * prompt / t_prefill, 1),
+            "decode_ms_per_step": round(dec_ms, 3), "decode_tok_s": round(Bm / dec_ms * 1e3, 1),
+            "decode_frac_of_bound": round(bound_ms / dec_ms, 4),
+        },
+        "serving_path": {
+            "how": "lastkv_amd.serving paged pool, 1024-token prefill rows, decode steps replayed from one HIP graph",
+            "prefill_s": round(t_sprefill, 3), "prefill_tok_s": round(Bm * prompt / t_sprefill, 1),
+            "decode_ms_per_step": round(sdec_ms, 3), "decode_tok_s": round(Bm / sdec_ms * 1e3, 1),
+            "decode_frac_of_bound": round(bound_ms / sdec_ms, 4),
+        },
+        "prefill_logits_rel_l2_serving_vs_hf": round(float((sv_logits - hf_logits).norm() / hf_logits.norm()), 5),
+    }
+
+
+def mixed_step_measurement(ops, torch, dev, reps: int = 10) -> dict:
+    """One ragged serving step at the 8B attention shape (Hq 32, Hkv 8, C = 1024, one layer of the
+    paged pool): 31 decode rows at position 8192, a 1024-token prefill row at 7168-8191 and a 7-token
+    row at 8192-8198, through LastKVFastPath.run_layer (one varlen epilogue launch and one varlen
+    attention launch), against the same rows called one at a time (an epilogue and an attention call
+    per row, the form run_layer had before it took cu_seqlens).  Synthetic N(0, 1) projections;
+    HIP events around the device work only (the host prologue is excluded from both)."""
+
+    from lastkv_amd.serving import BLOCK, LastKVFastPath, LastKVPagePool
+
+    Hq, Hkv = HQ, HKV
+    pool = LastKVPagePool(num_layers=1, kv_heads=Hkv, chunk_size=CHUNK, max_slots=33, source_pages=33 * 260,
+                          max_tokens_per_slot=8320, device=dev)
+    g = torch.Generator(device=dev).manual_seed(9)
+    vs = (torch.rand(Hkv, generator=g, device=dev) + 0.5).bfloat16().float()
+    w = (torch.rand(128, generator=g, device=dev) + 0.5).bfloat16()
+    alpha = torch.rand(Hkv, generator=g, device=dev).bfloat16().float()
+
+    def rotary(positions):
+        inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, device=positions.device).float() / 128))
+        f = positions[..., None].float() * inv
+        e = torch.cat((f, f), -1)
+        return e.cos().bfloat16(), e.sin().bfloat16()
+
+    fast = LastKVFastPath(pool, num_q_heads=Hq, layer_params=[(w, w, 1e-5, vs)],
+                          blend=(alpha, (1 - alpha).bfloat16().float(), vs), rotary=rotary, max_batch=33)
+    slots = [fast.add_sequence() for _ in range(33)]
+
+    def run(rows):
+        fast.prepare(rows)
+        T = fast.tokens
+        qkv = torch.randn((T, (Hq + 2 * Hkv) * 128), generator=g, device=dev).bfloat16()
+        q, k, v = qkv.split([Hq * 128, Hkv * 128, Hkv * 128], dim=-1)
+        out = torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=dev)
+        fast.run_layer(0, q, k, v, out)
+        return q, k, v, out
+
+    for s in range(0, 8192, CHUNK):  # 32 sequences to 8192 tokens, one to 7168
+        run([(slot, CHUNK) for slot in (slots if s < 7168 else slots[:32])])
+    rows = [(slot, 1) for slot in slots[:31]] + [(slots[32], CHUNK), (slots[31], 7)]
+    q, k, v, out = run(rows)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(reps)]
+    for e0, e1 in events:  # the same step again: rewrites the same K / V
+        e0.record()
+        fast.run_layer(0, q, k, v, out)
+        e1.record()
+    torch.cuda.synchronize()
+    one_launch = statistics.median(a.elapsed_time(b) for a, b in events) * 1e3
+    # the same rows one at a time
+    T = fast.tokens
+    pos, older_len, local_len, local_start = fast._meta
+    ring_tab = fast._ring_table[0]
+    rope = []
+    for r in fast.rows:
+        rope.append(rotary(torch.arange(r.position, r.position + r.tokens, device=dev)[None, :]))
+    splits = [ops.default_decode_splits(1, Hkv, r.older + r.local, ops._cu_count(pool.device)) for r in fast.rows]
+    ws = torch.empty(ops.prefill_workspace_bytes(1, Hkv, 8192, pool.ring_tokens) + (1 << 24), dtype=torch.uint8, device=dev)
+
+    def per_row():
+        start = 0
+        for b, r in enumerate(fast.rows):
+            n = r.tokens
+            sl = slice(start, start + n)
+            cos, sin = rope[b]
+            qo = ops.qkv_epilogue(q[sl].reshape(1, n, -1), k[sl].reshape(1, n, -1), v[sl].reshape(1, n, -1), cos, sin,
+                                  num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=w, k_norm_weight=w, eps=1e-5,
+                                  positions=r.position, ring=pool.pool, ring_table=ring_tab[b:b + 1],
+                                  ring_tokens=pool.ring_tokens, deep=pool.pool,
+                                  deep_table=fast._older_table[b:b + 1])
+            width = max(1, -(-r.older // BLOCK))
+            seg = dict(older=pool.pool, older_table=fast._older_table[b:b + 1, :width], older_len=r.older, vscale=vs,
+                       local=pool.pool, local_table=ring_tab[b:b + 1], local_ring_blocks=pool.ring_blocks,
+                       local_len=r.local, local_start=r.older % pool.ring_tokens)
+            if n == 1:
+                ops.decode_attention(qo.view(1, Hq, 128), out=out[sl].view(1, Hq, 128), num_splits=splits[b],
+                                     workspace=ws, **seg)
+            else:
+                ops.prefill_attention(qo, causal=True, out=out[sl].view(1, n, Hq, 128), workspace=ws, **seg)
+            start += n
+
+    per_row()
+    for e0, e1 in events:
+        e0.record()
+        per_row()
+        e1.record()
+    torch.cuda.synchronize()
+    per_row_us = statistics.median(a.elapsed_time(b) for a, b in events) * 1e3
+    decode_bytes = 31 * Hkv * (8192 + 1) * 128 * 2 * 2
+    return {
+        "workload": "one layer of a ragged serving step: 31 decode rows at position 8192 + a 1024-token row "
+                    "(positions 7168-8191) + a 7-token row (8192-8198); Hq 32, Hkv 8, C 1024, paged pool",
+        "tokens": int(T),
+        "one_launch_us_per_layer": round(one_launch, 1),
+        "per_row_calls_us_per_layer": round(per_row_us, 1),
+        "speedup": round(per_row_us / one_launch, 2),
+        "decode_rows_kv_bytes": decode_bytes,
+        "decode_rows_hbm_bound_us": round(decode_bytes / (HBM_PEAK_GBS * 1e3), 1),
+    }
+
+
+def e2e_8b_measurement(torch, dev, decode_steps: int = 256, model=None) -> dict:
+    """BASELINE config 3 end to end through the drop-in model (lastkv_amd.llm): 8B geometry
+    (32 layers, 4096, 32 / 8 heads, FFN 14336, vocab 128256, llama3 RoPE theta 500000), random
+    N(0, 0.02) bf16 weights, B = 32, an 8192-token uniform-random prompt prefilled in 2048-token
+    calls (C = 1024), then greedy decode steps feeding one new token per sequence.  Eager PyTorch
+    host loop; projections / MLP / norms / lm_head are torch (hipBLASLt) ops, attention and cache
+    writes are this library's kernels."""
+
+    from lastkv_amd.llm import LastKVCache
+
+    Bm, prompt, call = 32, 8192, 2048
+    if model is None:
+        model = build_8b_model(torch, dev)
+    cfg = model.config
     params = sum(p.numel() for p in model.parameters())
     ids = torch.randint(0, cfg.vocab_size, (Bm, prompt), generator=torch.Generator().manual_seed(1)).to(dev)
     cache = LastKVCache(cfg.num_hidden_layers, CHUNK, capacity_tokens=prompt + decode_steps)
@@ -514,7 +710,7 @@ def e2e_8b_measurement(torch, dev, decode_steps: int = 256) -> dict:
         torch.cuda.synchronize()
         t_vdecode = time.perf_counter() - t0
     v_rel = float((v_logits - hf_logits).norm() / hf_logits.norm())
-    del runner, graph, model
+    del runner, graph
     torch.cuda.empty_cache()
     return {
         "workload": "config 3: 8B-shape LastKV model, B=32, 8192-token prompt (C=1024), then "
@@ -609,9 +805,10 @@ def _cpu_time(fn, seconds: float, max_runs: int = 20) -> tuple[float, int]:
 
 
 def cpu_baseline_configs(seconds: float, model_step: bool = False) -> dict:
-    """The rest of the CPU baseline plan (BASELINE configs 2-5), each a bounded sample of the torch
-    restatement of the reference path (torch.cat composition + SDPA, oracle/reference_path.py) on
-    this host's cores: config 2 in fp32; the attention layer-call of configs 3 and 4 at their decode
+    """The rest of the CPU baseline plan (BASELINE configs 1-5), each a bounded sample of the torch
+    restatement of the reference path (torch.cat composition + SDPA, oracle/reference_path.py;
+    the whole model, oracle/model.py, for config 1) on this host's cores: config 1's 124M model in
+    fp32 (prompt + 64 greedy steps, C = 1024 and 32); config 2 in fp32; the attention layer-call of configs 3 and 4 at their decode
     positions (older shared region with the V scale, blended recent chunk, current token); one Wan
     layer's block attention (config 5); and, with ``model_step`` (tens of seconds per step), full
     8B-shape decode steps of the reference model at B = 32, 8K context in fp32, the reference CPU
@@ -627,6 +824,25 @@ def cpu_baseline_configs(seconds: float, model_step: bool = False) -> dict:
     bf = torch.bfloat16
     rnd = lambda *shape, dtype=bf: torch.randn(shape, generator=g).to(dtype)
     res = {}
+
+    # config 1: the whole 124M-shape model in fp32 (12 layers, 768, 12 heads = kv heads, head_dim 64,
+    # FFN 2048, vocab 50304; weights N(0, 0.02) seed 0), batch 1: a 128-token prompt then 64 greedy
+    # steps feeding one new token each (modeling.py:263-274), at C = 1024 (no chunk boundary) and
+    # C = 32 (shared and blended regions); the shape and seeds of the oracle's config-1 test
+    for chunk in (1024, 32):
+        cfg1 = M.Config(hidden_size=768, intermediate_size=2048, num_attention_heads=12, num_key_value_heads=12,
+                        num_hidden_layers=12, head_dim=64, vocab_size=50304, chunk_size=chunk,
+                        max_position_embeddings=1024)
+        model1 = M.ForCausalLM(cfg1).init_weights(torch.Generator().manual_seed(0)).eval()
+        prompt = torch.randint(0, 50304, (1, 128), generator=torch.Generator().manual_seed(1))
+        with torch.inference_mode():
+            t_pre, _ = _cpu_time(lambda: model1(prompt, None, logits_to_keep=1), seconds / 4, max_runs=10)
+            sec, n = _cpu_time(lambda: model1.generate_greedy(prompt, 64), seconds, max_runs=5)
+        res[f"config1_124m_fp32_c{chunk}"] = {
+            "ms_prompt_and_64_steps": round(sec * 1e3, 1), "ms_prompt_prefill": round(t_pre * 1e3, 2),
+            "decode_tok_s": round(64 / max(sec - t_pre, 1e-9), 1), "runs": n, "batch": 1, "prompt": 128,
+            "steps": 64, "chunk": chunk}
+        del model1
 
     k, v, q = rnd(B, HKV, T, D, dtype=torch.float32), rnd(B, HKV, T, D, dtype=torch.float32), rnd(B, HQ, 1, D, dtype=torch.float32)
     sec, n = _cpu_time(lambda: sdpa_bottom_right(q, k, v, native_gqa=True), seconds)
@@ -722,6 +938,10 @@ def main() -> int:
             res = epilogue_measurement(ops, torch, dev)
         elif args.only == "peaks":
             res = peaks_measurement(ops, torch, dev)
+        elif args.only == "mixed":
+            res = mixed_step_measurement(ops, torch, dev)
+        elif args.only == "config4e2e":
+            res = e2e_config4_measurement(torch, dev, build_8b_model(torch, dev))
         else:
             res = e2e_8b_measurement(torch, dev, args.decode_steps)
         print(json.dumps({"only": args.only, **res}), flush=True)
@@ -780,10 +1000,15 @@ def main() -> int:
         configs = {"short_prefill_calls": short_prefill_measurement(ops, torch, cache, dev),
                    "config4_decode_128k": decode_long_measurement(ops, torch, dev),
                    "config4_prefill_128k": prefill_long_measurement(ops, torch, dev),
-                   "config5_wan": wan_measurement(ops, torch, dev)}
+                   "config5_wan": wan_measurement(ops, torch, dev),
+                   "mixed_step": mixed_step_measurement(ops, torch, dev)}
         del cache
         torch.cuda.empty_cache()
-        configs["config3_e2e_8b"] = e2e_8b_measurement(torch, dev, args.decode_steps)
+        model = build_8b_model(torch, dev)
+        configs["config3_e2e_8b"] = e2e_8b_measurement(torch, dev, args.decode_steps, model=model)
+        configs["config4_e2e_8b"] = e2e_config4_measurement(torch, dev, model)
+        del model
+        torch.cuda.empty_cache()
     if args.calibrate_copy:
         src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev)
         dst = torch.empty_like(src)

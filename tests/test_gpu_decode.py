@@ -357,3 +357,62 @@ def test_short_prefill_on_decode_kernel(L, Hq, Hkv, causal, B):
     np.testing.assert_allclose(lse.cpu().numpy(), want_lse.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
     tile = ops.prefill_attention(_t(q), causal=causal, tile_waves=4, **seg)
     _close(tile, out.float().cpu().numpy(), f"short prefill tile vs decode kernel L={L}")
+
+
+# block-maximum jumps (exp2 units) along each wave's blocks: the decode kernel raises its softmax
+# reference only when a block maximum exceeds it by more than 8; jumps just below, at and above that,
+# a far one and a second raise after a first
+LAZY_PATTERNS = {
+    "below 7.5": [0.0, 7.5, 7.0, 7.5],
+    "at 8.0": [0.0, 8.0, 3.0, 8.0],
+    "above 8.0625": [0.0, 8.0625, 1.0, 8.0625],
+    "8.5": [0.0, 8.5, 4.0, -2.0],
+    "far 20": [0.0, 20.0, 5.0, 19.5],
+    "second raise": [0.0, 8.5, 17.25, 17.0],
+}
+
+
+def _lazy_case(pattern, blocks, Hq, Hkv, seed):
+    """K whose dim 0 carries the scores (q = e_0, sm_scale = ln 2: scores in exp2 units equal the K
+    values): the block with index j peaks at pattern[(j // 4) % 4] (each of the 4 waves of a
+    decode workgroup walks blocks w, w + 4, ..., so every wave meets the jumps in order), its other
+    tokens below it; bf16 values, so every product is exact."""
+
+    rng = np.random.default_rng(seed)
+    T = blocks * 32
+    k = np.zeros((1, Hkv, T, 128), np.float32)
+    for h in range(Hkv):
+        for j in range(blocks):
+            top = pattern[(j // 4) % len(pattern)] + 0.25 * h
+            vals = top - rng.uniform(0.5, 12.0, 32)
+            vals[rng.integers(0, 32)] = top
+            k[0, h, j * 32:(j + 1) * 32, 0] = vals
+    k = bf16.round_bf16(k)
+    v = _bf(rng, (1, Hkv, T, 128))
+    q = np.zeros((1, Hq, 1, 128), np.float32)
+    q[..., 0] = 1.0
+    return q, k, v
+
+
+@pytest.mark.parametrize("name", list(LAZY_PATTERNS))
+def test_decode_lazy_rescale_threshold_regimes(name):
+    """The decode kernel's lazy softmax reference with constructed block-maximum jumps of 7.5, 8,
+    8.0625, 8.5 and 20 exp2 units and a second raise after a first, through one and five key
+    splits and a short prefill call on the decode kernel, against the fp64 oracle."""
+
+    Hq, Hkv, blocks = 8, 2, 80
+    q, k, v = _lazy_case(LAZY_PATTERNS[name], blocks, Hq, Hkv, seed=len(name))
+    sm = float(np.log(2.0))  # scale * log2(e) = 1: exp2 units = raw scores
+    cache = ops.TiledKV.zeros(1, Hkv, blocks * 32, DEV)
+    ops.pack_kv(_t(k), _t(v), cache)
+    want, want_lse = A.attention(q, k, v, scale=sm)
+    for splits in (1, 5):
+        lse = torch.empty((1, Hq), dtype=torch.float32, device=DEV)
+        out = ops.decode_attention(_t(q), older=cache, older_len=blocks * 32, num_splits=splits, sm_scale=sm, lse=lse)
+        _close(out, bf16.round_bf16(want[:, :, 0].astype(np.float32)), f"lazy {name} splits={splits}")
+        np.testing.assert_allclose(lse.cpu().numpy(), want_lse[:, :, 0], rtol=1e-5, atol=1e-4)
+    # two query tokens (8 score columns) on the decode kernel: the older segment is fully visible
+    q2 = np.concatenate([q, q * 0.5], 2).transpose(0, 2, 1, 3)  # [1, 2, Hq, 128]
+    out = ops.prefill_attention(_t(q2), older=cache, older_len=blocks * 32, causal=True, sm_scale=sm)
+    want2, _ = A.attention(q2.transpose(0, 2, 1, 3), k, v, scale=sm)
+    _close(out, bf16.round_bf16(want2.transpose(0, 2, 1, 3).astype(np.float32)), f"lazy {name} short prefill")
