@@ -659,9 +659,11 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
   p.rv_mul = a->ring_v_mul;
   p.cu = a->cu_seqlens;
   p.max_seqlen = static_cast<int32_t>(seq_tokens);
-  // Calls of many tokens with 16-byte-aligned rows take the block form (16-byte accesses, V tiles
-  // written through LDS), provided the call's 32-position blocks do not wrap onto each other in the
-  // ring; decode-sized calls keep one wave per (token, head).
+  // Calls of many tokens per sequence (16 or more; ragged calls: the longest sequence) with
+  // 16-byte-aligned rows take the block form (16-byte accesses, V tiles written through LDS),
+  // provided the call's 32-position blocks do not wrap onto each other in the ring; decode-sized
+  // calls keep one wave per (token, head) however many sequences they hold (B = 32 one-token rows:
+  // 7 us against 22 us in block form, whose workgroups would each hold one token of a block).
   auto aligned = [](const void* ptr, int64_t s0, int64_t s1) {
     return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0 && s0 % 8 == 0 && s1 % 8 == 0;
   };
@@ -669,7 +671,7 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
   const int64_t kv_blocks = a->positions != nullptr || ragged
                                 ? (seq_tokens + kBlockTokens - 1) / kBlockTokens + 1
                                 : (a->position_const + a->tokens - 1) / kBlockTokens - a->position_const / kBlockTokens + 1;
-  const bool block_form = rows >= 16 && kv_blocks <= a->ring_tokens / kBlockTokens &&
+  const bool block_form = seq_tokens >= 16 && kv_blocks <= a->ring_tokens / kBlockTokens &&
                           aligned(a->q, a->q_stride_b, a->q_stride_t) && aligned(a->k, a->k_stride_b, a->k_stride_t) &&
                           aligned(a->v, a->v_stride_b, a->v_stride_t) && aligned(a->cos, a->cs_stride_b, a->cs_stride_t) &&
                           aligned(a->sin, a->cs_stride_b, a->cs_stride_t) &&

@@ -53,8 +53,10 @@ struct PrefillParams {
   // run on the wide instance instead (bf16 V, P as bf16 hi + lo)
   uint8_t* vflags;
   int32_t vflag_stride;
-  // set to 1 by the fp16 instance when it skips a tile for the wide one (cleared by the pre-pass)
-  int32_t* any_wide;
+  // set to 1 by the fp16 instance when it skips a tile for the wide one (cleared by the pre-pass).
+  // A float: a store of int32 type in the tile kernel may alias the int32 page tables for the
+  // compiler, which then reads every page id with a vector load instead of a scalar one.
+  float* any_wide;
   // ragged query rows: sequence b's tokens are rows cu[b] .. cu[b + 1] - 1 of q / out (nullptr:
   // L tokens per sequence); rows = the call's total row count.  Sequences with at most
   // decode_rows query rows per kv head run on the decode kernel and are skipped here.
@@ -307,7 +309,7 @@ __device__ __attribute__((always_inline)) inline void unroll_steps(std::integer_
 template <bool kPaged>
 __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
   const int blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  if ((blk | kvh | b) == 0 && threadIdx.x == 0) *p.any_wide = 0;  // (the tile kernels run after this one)
+  if ((blk | kvh | b) == 0 && threadIdx.x == 0) *p.any_wide = 0.f;  // (the tile kernels run after this one)
   if (!on_tile_path(p, seq_rows(p, b))) return;
   const SeqView sv = make_seq_view(p.seg, b, kvh);
   if (blk >= sv.nb0 + local_blocks(sv, sv.n1)) return;
@@ -474,7 +476,7 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
       stage_load<NW, kWide>(sets[j % kStages], rsrc, k_block<kPaged>(sv, lb), vb(lb), lb, wave, lane_off);
     }
     if (!kWide && needs_wide) {
-      if (threadIdx.x == 0) *p.any_wide = 1;
+      if (threadIdx.x == 0) *p.any_wide = 1.f;
       return;
     }
     __syncthreads();
@@ -712,7 +714,7 @@ template <int NW, int CG, int WPE, bool kPaged>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_wide_kernel(
     const PrefillParams p) {
   __shared__ uint4 lds[kTileRing * kTileBuf];
-  if (*p.any_wide == 0) return;  // the fp16 instance ran every tile (workgroup-uniform)
+  if (*p.any_wide == 0.f) return;  // the fp16 instance ran every tile (workgroup-uniform)
   const int pairs = p.batch * p.hkv;
   for (int pair = blockIdx.x; pair < pairs; pair += gridDim.x) {
     if (!pair_needs_wide(p, pair / p.hkv, pair % p.hkv)) continue;  // (workgroup-uniform)
@@ -897,7 +899,7 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.v16_blocks = static_cast<int32_t>(vblocks);
   p.vflag_stride = static_cast<int32_t>((vblocks + 15) / 16 * 16);
   p.vflags = static_cast<uint8_t*>(a->workspace) + static_cast<int64_t>(a->batch) * a->num_kv_heads * vblocks * (kBlockElems * 2);
-  p.any_wide = reinterpret_cast<int32_t*>(p.vflags + static_cast<int64_t>(a->batch) * a->num_kv_heads * p.vflag_stride);
+  p.any_wide = reinterpret_cast<float*>(p.vflags + static_cast<int64_t>(a->batch) * a->num_kv_heads * p.vflag_stride);
   p.cu = a->cu_seqlens_q;
   p.rows = a->tokens;
   p.decode_rows = ragged && short_on_decode ? 64 : -1;
