@@ -225,7 +225,19 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // Workgroup ids go round-robin over the XCDs, and the grid's fastest dimension is the split: with
+  // splits chosen on the device (ragged calls), the workgroups past a sequence's split count exit,
+  // and with 8 splits in the grid those would be whole XCDs (2 splits: 6 of 8 idle).  Those calls
+  // take the split as the slowest dimension of the linear id instead, so the working workgroups
+  // (splits below the count) are consecutive ids spread over every XCD.
+  int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  if (kMulti && p.dyn_splits) {
+    const int pairs = gridDim.y * gridDim.z;
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    split = lin / pairs;
+    kvh = lin % pairs % gridDim.y;
+    b = lin % pairs / gridDim.y;
+  }
   const int G = p.group;
 
   // ragged calls: this sequence's query tokens (workgroup-uniform; sequences of another column
@@ -425,26 +437,24 @@ __device__ inline void combine_row(const DecodeParams& p, const float* ml, const
   __syncthreads();  // (sm_w and sm_red are reused by the caller's next row)
 }
 
-// Uniform calls: one block per [B, L, Hq] row.  Ragged calls: one block per (head, sequence) of the
-// launch's column class, over the sequence's query tokens (its split count and split-state rows come
-// from its rank in the class, as in the split kernel; with one split that kernel wrote the output).
+// Uniform calls: one block per [B, L, Hq] row.  Ragged calls: one block per (head, sequence, query
+// token) of the launch's column class (its split count and split-state rows come from the
+// sequence's rank in the class, as in the split kernel; with one split that kernel wrote the output).
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(const DecodeParams p) {
   __shared__ float sm_w[kMaxSplits];
   __shared__ float sm_red[kCombineThreads / 64];
   if (p.cu != nullptr) {
-    const int h = blockIdx.x, b = blockIdx.y;
+    const int h = blockIdx.x, b = blockIdx.y, tq = blockIdx.z;
     const MultiRows mr = multi_rows(p, b);
-    if (!in_column_class(p, mr.L)) return;  // (uniform over the block)
+    if (!in_column_class(p, mr.L) || tq >= mr.L) return;  // (uniform over the block)
     const ClassRank cr = class_rank(p, b, p.hq / p.group);
     const int S = cr.splits;
     if (S == 1) return;
-    for (int tq = 0; tq < mr.L; ++tq) {
-      const int64_t ws_row = (static_cast<int64_t>(cr.rank) * p.lmax + tq) * p.hq + h;
-      const int64_t out_row = mr.row0 + tq;
-      combine_row(p, p.ws_ml + ws_row * S * 2, p.ws_o + ws_row * S * kHeadDim,
-                  S, p.out + out_row * p.out_st + static_cast<int64_t>(h) * kHeadDim,
-                  p.lse != nullptr ? p.lse + out_row * p.hq + h : nullptr, h / p.group, sm_w, sm_red);
-    }
+    const int64_t ws_row = (static_cast<int64_t>(cr.rank) * p.lmax + tq) * p.hq + h;
+    const int64_t out_row = mr.row0 + tq;
+    combine_row(p, p.ws_ml + ws_row * S * 2, p.ws_o + ws_row * S * kHeadDim, S,
+                p.out + out_row * p.out_st + static_cast<int64_t>(h) * kHeadDim,
+                p.lse != nullptr ? p.lse + out_row * p.hq + h : nullptr, h / p.group, sm_w, sm_red);
     return;
   }
   const int bh = blockIdx.x;  // [B, L, Hq] row
@@ -507,7 +517,7 @@ int32_t launch_decode(const DecodeParams& p, dim3 grid, bool vscale, bool nt, in
   }
   if (const int32_t st = check_launch(what)) return st;
   if (p.splits > 1) {
-    const dim3 grid = p.cu != nullptr ? dim3(p.hq, p.batch) : dim3(rows);
+    const dim3 grid = p.cu != nullptr ? dim3(p.hq, p.batch, p.lmax) : dim3(rows);
     decode_combine_kernel<<<grid, kCombineThreads, 0, s>>>(p);
     return check_launch(what);
   }

@@ -305,32 +305,40 @@ __device__ __attribute__((always_inline)) inline void unroll_steps(std::integer_
 // local], with the older segment as bf16(V * s) (the reference's rounded _scale()).  The
 // attention kernel's query tiles then stage V as plain copies instead of each converting it.
 // Each block also gets its flag: whether some value does not fit fp16 (magnitude 65536 or more).
-// One workgroup per (block, kv head, sequence); 256 threads x 16 values.
-template <bool kPaged>
+// One workgroup per kBlocks consecutive blocks of one (kv head, sequence); 256 threads x 16 values
+// per block.  Ragged calls take 8 blocks per workgroup: their grid covers every sequence, and the
+// workgroups of the sequences that are not on the tile path exit (a serving step of 31 decode rows
+// and one 1024-token row: 33 us for the pass with one block per workgroup).
+template <bool kPaged, int kBlocks>
 __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
-  const int blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  if ((blk | kvh | b) == 0 && threadIdx.x == 0) *p.any_wide = 0.f;  // (the tile kernels run after this one)
+  const int kvh = blockIdx.y, b = blockIdx.z;
+  if ((blockIdx.x | kvh | b) == 0 && threadIdx.x == 0) *p.any_wide = 0.f;  // (the tile kernels run after this one)
   if (!on_tile_path(p, seq_rows(p, b))) return;
   const SeqView sv = make_seq_view(p.seg, b, kvh);
-  if (blk >= sv.nb0 + local_blocks(sv, sv.n1)) return;
-  const bool older = blk < sv.nb0;
-  const uint16_t* src = (older ? sv.ov : sv.lv) + block_offset<kPaged>(sv, blk);
-  uint16_t* dst = p.v16 + ((static_cast<int64_t>(b) * p.hkv + kvh) * p.v16_blocks + blk) * kBlockElems;
-  const float s = (p.vscale_mode && older) ? p.vscale[kvh] : 1.f;
-  bool over = false;
+  const int nb = sv.nb0 + local_blocks(sv, sv.n1);
+  const float vs = p.vscale_mode ? p.vscale[kvh] : 1.f;
+  for (int k = 0; k < kBlocks; ++k) {
+    const int blk = static_cast<int>(blockIdx.x) * kBlocks + k;
+    if (blk >= nb) return;  // (workgroup-uniform)
+    const bool older = blk < sv.nb0;
+    const uint16_t* src = (older ? sv.ov : sv.lv) + block_offset<kPaged>(sv, blk);
+    uint16_t* dst = p.v16 + ((static_cast<int64_t>(b) * p.hkv + kvh) * p.v16_blocks + blk) * kBlockElems;
+    const float s = older ? vs : 1.f;
+    bool over = false;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int e = (threadIdx.x + j * 256) * 8;
-    // bf16(v * s); bf16(v * 1) == v, so the unscaled blocks take the same instructions
-    const uint4 y = scale_frag(*reinterpret_cast<const uint4*>(src + e), s);
-    over = over || f16_overflow(y.x) || f16_overflow(y.y) || f16_overflow(y.z) || f16_overflow(y.w);
-    *reinterpret_cast<uint4*>(dst + e) = make_uint4(f16x2_bits(bf16_lo(y.x), bf16_hi(y.x)),
-                                                    f16x2_bits(bf16_lo(y.y), bf16_hi(y.y)),
-                                                    f16x2_bits(bf16_lo(y.z), bf16_hi(y.z)),
-                                                    f16x2_bits(bf16_lo(y.w), bf16_hi(y.w)));
+    for (int j = 0; j < 2; ++j) {
+      const int e = (threadIdx.x + j * 256) * 8;
+      // bf16(v * s); bf16(v * 1) == v, so the unscaled blocks take the same instructions
+      const uint4 y = scale_frag(*reinterpret_cast<const uint4*>(src + e), s);
+      over = over || f16_overflow(y.x) || f16_overflow(y.y) || f16_overflow(y.z) || f16_overflow(y.w);
+      *reinterpret_cast<uint4*>(dst + e) = make_uint4(f16x2_bits(bf16_lo(y.x), bf16_hi(y.x)),
+                                                      f16x2_bits(bf16_lo(y.y), bf16_hi(y.y)),
+                                                      f16x2_bits(bf16_lo(y.z), bf16_hi(y.z)),
+                                                      f16x2_bits(bf16_lo(y.w), bf16_hi(y.w)));
+    }
+    const int any = __syncthreads_or(over);
+    if (threadIdx.x == 0) p.vflags[(static_cast<int64_t>(b) * p.hkv + kvh) * p.vflag_stride + blk] = any ? 1 : 0;
   }
-  const int any = __syncthreads_or(over);
-  if (threadIdx.x == 0) p.vflags[(static_cast<int64_t>(b) * p.hkv + kvh) * p.vflag_stride + blk] = any ? 1 : 0;
 }
 
 // Whether some block in [0, nbt) of (b, kvh) holds a V value fp16 cannot (the pre-pass's flags),
@@ -370,13 +378,13 @@ constexpr int kTileBuf = 1024;     // uint4 per block buffer (16 KiB)
 // (i + 2) % 4, load block i + 4, one barrier.
 // The 2-wave instance (calls of at most 64 query rows per kv head, bound by HBM, not by the matrix
 // pipe) splits P into fp16 hi + lo and runs P V twice, so its probabilities carry ~22 bits
-// instead of 11.  prefill_tile runs one query tile (logical index = (sequence, kv head, tile)).
+// instead of 11.  prefill_tile runs query tile `tile` of (sequence b, kv head kvh).
 // kWide: the instance for tiles whose V does not fit fp16 (the pre-pass flagged one of their blocks):
 // V staged as bf16 from the caches (older blocks as bf16(V * s)), P split into bf16 hi + lo, P V and
 // the row sums on bf16 MFMAs; the fp16 instance skips those tiles and this one runs only them.
 template <int NW, int CG, bool kPaged, bool kWide = false>
-__device__ __attribute__((always_inline)) inline void prefill_tile(const PrefillParams& p, const int logical,
-                                                                   uint4* lds) {
+__device__ __attribute__((always_inline)) inline void prefill_tile(const PrefillParams& p, const int b, const int kvh,
+                                                                   const int tile, uint4* lds) {
   constexpr bool kSplitP = NW == 2 || kWide;
   constexpr int kStages = 2;  // register stage sets (global loads run kStages steps ahead of their LDS store)
   constexpr int kDist = 2;    // step i stores block i + kDist into the LDS ring
@@ -388,9 +396,6 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
-  const int tile = logical % p.tiles;
-  const int kvh = (logical / p.tiles) % p.hkv;
-  const int b = logical / (p.tiles * p.hkv);
   const int G = p.group;
   const SeqRows sr = seq_rows(p, b);
   const int rows_total = sr.L * G;
@@ -688,20 +693,66 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   }
 }
 
+// Ragged calls: the sequence and tile of the call's tile number gt, counting the tiles of the
+// sequences on the tile path in order (ceil(rows / rows_per_wg) each); false past the last one.
+// Every wave scans the sequences itself, 64 per step (an inclusive scan of the tile counts over the
+// lanes, then a ballot for the first lane whose running total exceeds gt).
+__device__ inline bool ragged_tile(const PrefillParams& p, int gt, int rows_per_wg, int& b, int& tile) {
+  const int lane = threadIdx.x & 63;
+  int base = 0;  // tiles of the sequences before this step's 64
+  for (int i0 = 0; i0 < p.batch; i0 += 64) {
+    const int i = i0 + lane;
+    int nt = 0;
+    if (i < p.batch) {
+      const SeqRows sr = seq_rows(p, i);
+      if (on_tile_path(p, sr)) nt = (sr.L * p.group + rows_per_wg - 1) / rows_per_wg;
+    }
+    int incl = nt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off);
+      if (lane >= off) incl += y;
+    }
+    const int total = __shfl(incl, 63);
+    if (gt < base + total) {
+      const int l = __builtin_ctzll(__builtin_amdgcn_ballot_w64(base + incl > gt));
+      b = i0 + l;
+      tile = gt - base - __shfl(incl - nt, l);
+      return true;
+    }
+    base += total;
+  }
+  return false;
+}
+
 // One workgroup per query tile.  Workgroup ids map to tiles so that the tiles of one (sequence, kv
 // head) run on one XCD; in causal calls a tile's key count grows with its index, and the tiles are
 // dispatched longest first (largest index first), which shortens the tail of the last workgroups
 // (config-3 chunk pieces: 41.9 -> 43.1 % of the MFMA peak in a same-box A/B; the bidirectional Wan
-// block's tiles are all alike and keep their order).
+// block's tiles are all alike and keep their order).  A ragged call's grid holds (an upper bound of)
+// the tiles its sequences need, kv head fastest, each workgroup finding its sequence and tile by a
+// scan of cu_seqlens: a grid sized by the longest sequence for every sequence mostly exits, and the
+// exits delayed the working tiles (a serving step of 31 decode rows, a 1024-token row and a 7-token
+// row: 258 us for the one long row against 206 us for the same tiles alone).
 template <int NW, int CG, int WPE, bool kPaged>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_kernel(
     const PrefillParams p) {
   __shared__ uint4 lds[kTileRing * kTileBuf];
-  // (a ragged call's grid covers every sequence at the longest one's tile count, and most of it
-  // exits: round-robin over the XCDs spreads the tiles that work over all of them)
-  const int logical = p.cu != nullptr ? static_cast<int>(blockIdx.x) : xcd_logical_index(blockIdx.x, gridDim.x);
-  const int tile = logical % p.tiles;
-  prefill_tile<NW, CG, kPaged>(p, logical - tile + (p.causal ? p.tiles - 1 - tile : tile), lds);
+  int b, kvh, tile, tiles;
+  if (p.cu != nullptr) {
+    kvh = static_cast<int>(blockIdx.x) % p.hkv;
+    if (!ragged_tile(p, static_cast<int>(blockIdx.x) / p.hkv, NW * 32, b, tile)) return;  // (workgroup-uniform)
+    tiles = (seq_rows(p, b).L * p.group + NW * 32 - 1) / (NW * 32);
+  } else {
+    const int logical = xcd_logical_index(blockIdx.x, gridDim.x);
+    tiles = p.tiles;
+    tile = logical % tiles;
+    kvh = (logical / tiles) % p.hkv;
+    b = logical / (tiles * p.hkv);
+  }
+  // (one call site: the tile body is inlined once)
+  prefill_tile<NW, CG, kPaged>(p, __builtin_amdgcn_readfirstlane(b), __builtin_amdgcn_readfirstlane(kvh),
+                               __builtin_amdgcn_readfirstlane(p.causal ? tiles - 1 - tile : tile), lds);
 }
 
 // The wide instance: one workgroup per (sequence, kv head) pair at a time, min(pairs, CUs) of them.
@@ -719,7 +770,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   for (int pair = blockIdx.x; pair < pairs; pair += gridDim.x) {
     if (!pair_needs_wide(p, pair / p.hkv, pair % p.hkv)) continue;  // (workgroup-uniform)
     for (int tile = 0; tile < p.tiles; ++tile) {
-      prefill_tile<NW, CG, kPaged, true>(p, pair * p.tiles + tile, lds);
+      prefill_tile<NW, CG, kPaged, true>(p, pair / p.hkv, pair % p.hkv, tile, lds);
       __syncthreads();  // the next tile's staging reuses the LDS ring
     }
   }
@@ -925,18 +976,26 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   }
   const int64_t rows_per_wg = waves * 32;
   const int64_t tiles = (rows + rows_per_wg - 1) / rows_per_wg;
-  const int64_t wgs = tiles * heads;
+  // ragged: at most ceil(T * G / rows_per_wg) + B tiles over the sequences, each of Hkv workgroups
+  const int64_t wgs = ragged ? ((static_cast<int64_t>(a->tokens) * group + rows_per_wg - 1) / rows_per_wg + a->batch) *
+                                   a->num_kv_heads
+                             : tiles * heads;
   LKV_REQUIRE(wgs < (1LL << 31), "too many query rows");
   p.tiles = static_cast<int32_t>(tiles);
   p.hkv = a->num_kv_heads;
   p.batch = a->batch;
   const bool paged = a->older_block_table != nullptr || a->local_block_table != nullptr;
   if (vblocks > 0) {  // (no keys at all: every row's output is zero; the main kernel skips its loop)
-    const dim3 vgrid(static_cast<unsigned>(vblocks), a->num_kv_heads, a->batch);
-    if (paged)
-      v16_stage_kernel<true><<<vgrid, 256, 0, s>>>(p);
+    const int per_wg = ragged ? 8 : 1;
+    const dim3 vgrid(static_cast<unsigned>((vblocks + per_wg - 1) / per_wg), a->num_kv_heads, a->batch);
+    if (paged && ragged)
+      v16_stage_kernel<true, 8><<<vgrid, 256, 0, s>>>(p);
+    else if (paged)
+      v16_stage_kernel<true, 1><<<vgrid, 256, 0, s>>>(p);
+    else if (ragged)
+      v16_stage_kernel<false, 8><<<vgrid, 256, 0, s>>>(p);
     else
-      v16_stage_kernel<false><<<vgrid, 256, 0, s>>>(p);
+      v16_stage_kernel<false, 1><<<vgrid, 256, 0, s>>>(p);
     if (const int32_t e = check_launch("lkv_prefill_attn (V pre-pass)")) return e;
   }
   const dim3 grid(static_cast<unsigned>(wgs));
