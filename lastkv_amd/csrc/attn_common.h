@@ -242,6 +242,10 @@ __device__ inline uint4 scale_frag(uint4 v, float s) {
 int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, int32_t col_lo,
                                  int32_t col_hi, hipStream_t s);
 
+// The largest split count a ragged call's decode-kernel classes take (a lone sequence of the class
+// then spreads over 32 workgroups per kv head: 256 at Hkv 8).
+constexpr int kRaggedSplitCap = 32;
+
 // Split-state rows x splits a ragged call's decode-kernel class needs in the worst case over the
 // number n <= batch of its sequences (lmax query tokens each): the split count is `fixed` when
 // positive, else min(cap, ceil(cus / (n * num_kv_heads))); rows of one split count nothing.

@@ -90,6 +90,41 @@ __device__ inline ClassRank class_rank(const DecodeParams& p, int b, int hkv) {
   return ClassRank{n, rank, splits};
 }
 
+// Ragged calls with the split count chosen on the device run on a compact grid: workgroup
+// (kv head fastest) u-th (sequence, split) pair of the class, sequences in order, each with the
+// class's split count S.  Returns false past the class's n * S pairs.
+struct ClassPick {
+  int b, rank, split, splits;
+};
+
+__device__ inline bool class_pick(const DecodeParams& p, int u, int hkv, ClassPick& r) {
+  const int lane = threadIdx.x & 63;
+  int n = 0;
+  for (int i0 = 0; i0 < p.batch; i0 += 64) {
+    const int i = i0 + lane;
+    n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(i < p.batch && in_column_class(p, multi_rows(p, i).L)));
+  }
+  if (n == 0) return false;
+  r.splits = min(p.splits, max(1, (p.cus + n * hkv - 1) / (n * hkv)));
+  r.rank = u / r.splits;
+  r.split = u - r.rank * r.splits;
+  if (r.rank >= n) return false;
+  int base = 0;  // class sequences before this step's 64
+  for (int i0 = 0; i0 < p.batch; i0 += 64) {
+    const int i = i0 + lane;
+    const bool in = i < p.batch && in_column_class(p, multi_rows(p, i).L);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(in);
+    const int c = __builtin_popcountll(m);
+    if (r.rank < base + c) {  // the (rank - base)-th class sequence of these 64
+      const int below = __builtin_popcountll(m & ((uint64_t{1} << lane) - 1));
+      r.b = i0 + __builtin_ctzll(__builtin_amdgcn_ballot_w64(in && below == r.rank - base));
+      return true;
+    }
+    base += c;
+  }
+  return false;
+}
+
 // The bf16 output of a normalised fp32 value x of kv head kvh: bf16(x), or bf16(bf16(x) * s) with
 // an output scale (the reference rescales its bf16 attention output by s in fp32).
 __device__ inline uint16_t out_bits(float x, const float* out_scale, int kvh) {
@@ -225,33 +260,34 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
-  // Workgroup ids go round-robin over the XCDs, and the grid's fastest dimension is the split: with
-  // splits chosen on the device (ragged calls), the workgroups past a sequence's split count exit,
-  // and with 8 splits in the grid those would be whole XCDs (2 splits: 6 of 8 idle).  Those calls
-  // take the split as the slowest dimension of the linear id instead, so the working workgroups
-  // (splits below the count) are consecutive ids spread over every XCD.
-  int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  if (kMulti && p.dyn_splits) {
-    const int pairs = gridDim.y * gridDim.z;
-    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    split = lin / pairs;
-    kvh = lin % pairs % gridDim.y;
-    b = lin % pairs / gridDim.y;
-  }
   const int G = p.group;
+  int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  int S = p.splits;
+  int64_t ws_row0 = 0;  // ragged calls: split-state row of the sequence's token 0 (its rank in the class)
+  if (kMulti && p.dyn_splits) {
+    // the class's (sequence, split) pairs on a compact 1-D grid (the split count, chosen from the
+    // number of sequences in the class, is not known to the host; a grid of every sequence at the
+    // largest count would mostly exit, and with the split as its fastest dimension the exiting
+    // workgroups were whole XCDs: 2 splits left 6 of 8 idle)
+    const int hkv = p.hq / G;
+    kvh = static_cast<int>(blockIdx.x) % hkv;
+    ClassPick cp;
+    if (!class_pick(p, static_cast<int>(blockIdx.x) / hkv, hkv, cp)) return;  // (workgroup-uniform)
+    b = cp.b;
+    split = cp.split;
+    S = cp.splits;
+    ws_row0 = static_cast<int64_t>(cp.rank) * p.lmax;
+  }
 
   // ragged calls: this sequence's query tokens (workgroup-uniform; sequences of another column
-  // class run in another launch), the class's split count and this sequence's rows of split state
+  // class run in another launch)
   const MultiRows mr = kMulti ? multi_rows(p, b) : MultiRows{1, b};
   if (kMulti && !in_column_class(p, mr.L)) return;
   const int Lq = mr.L;
-  int S = p.splits;
-  int64_t ws_row0 = mr.row0;  // split-state row of this sequence's token 0
-  if (kMulti && p.cu != nullptr) {
-    const ClassRank cr = class_rank(p, b, gridDim.y);
-    S = cr.splits;
-    ws_row0 = static_cast<int64_t>(cr.rank) * p.lmax;
-    if (split >= S) return;
+  if (!(kMulti && p.cu != nullptr)) {
+    ws_row0 = mr.row0;
+  } else if (!p.dyn_splits) {  // a fixed split count over a (splits, Hkv, B) grid
+    ws_row0 = static_cast<int64_t>(class_rank(p, b, gridDim.y).rank) * p.lmax;
   }
 
   const SeqView sv = make_seq_view(p.seg, b, kvh);
@@ -569,10 +605,9 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
   p.cus = static_cast<int32_t>(cus);
   // about one workgroup per CU, at least 4 blocks per split, partial states within the workspace; a
-  // ragged call's launch caps the count at what one sequence alone would take and each launch
-  // divides the CUs among the sequences it finds in its class
-  // (ragged: at most 8, because every class launch's grid carries that many splits for every sequence)
-  int64_t splits = std::min<int64_t>({ragged ? std::min<int64_t>((cus + a->num_kv_heads - 1) / a->num_kv_heads, 8)
+  // ragged call's launch caps the count at what one sequence alone would take (and kRaggedSplitCap)
+  // and each launch divides the CUs among the sequences it finds in its class
+  int64_t splits = std::min<int64_t>({ragged ? std::min<int64_t>((cus + a->num_kv_heads - 1) / a->num_kv_heads, kRaggedSplitCap)
                                              : (cus + pairs - 1) / pairs,
                                       std::max<int64_t>(blocks / 4, 1), 1024});
   // split-state rows x splits: [B, L, Hq] rows for uniform calls, the class's sequences by rank
@@ -604,8 +639,12 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   // combine grid: one block per output row ([rows, Hq] ragged, [B, L, Hq] uniform)
   const int64_t out_rows = (ragged ? static_cast<int64_t>(a->tokens) : static_cast<int64_t>(a->batch) * a->tokens) *
                            a->num_q_heads;
-  return launch_decode(p, dim3(p.splits, a->num_kv_heads, a->batch), a->older_vscale_mode == 1, nt, cg,
-                       static_cast<int>(out_rows), s, "lkv_prefill_attn (short call on the decode kernel)");
+  // split counts chosen on the device: n sequences x S(n) splits <= ceil(CUs / Hkv) + B pairs per kv head
+  const dim3 grid = p.dyn_splits
+                        ? dim3(static_cast<unsigned>(a->num_kv_heads * ((cus + a->num_kv_heads - 1) / a->num_kv_heads + a->batch)))
+                        : dim3(p.splits, a->num_kv_heads, a->batch);
+  return launch_decode(p, grid, a->older_vscale_mode == 1, nt, cg, static_cast<int>(out_rows), s,
+                       "lkv_prefill_attn (short call on the decode kernel)");
 }
 
 }  // namespace lkv

@@ -522,15 +522,19 @@ def prefill_split_state_bytes(rows: int, num_q_heads: int, num_splits: int) -> i
     return 0 if num_splits <= 1 else rows * num_q_heads * num_splits * (HEAD_DIM + 2) * 4
 
 
+# the largest split count of a ragged call's decode-kernel classes (kRaggedSplitCap in the library)
+RAGGED_SPLIT_CAP = 32
+
+
 def ragged_split_state_bytes(batch: int, num_q_heads: int, num_kv_heads: int, max_seqlen: int, num_splits: int,
                              cu_count: int) -> int:
     """Upper bound of the split states a ragged prefill call keeps for its sequences of at most 64
     query rows per kv head (what ``lkv_prefill_workspace_bytes`` adds for them): per column class
     (16, 32, 64 columns) the worst case over the number n of its sequences of n * lmax * Hq * S(n)
-    states, S(n) = ``num_splits`` or min(8, ceil(CUs / Hkv), ceil(CUs / (n Hkv)))."""
+    states, S(n) = ``num_splits`` or min(RAGGED_SPLIT_CAP, ceil(CUs / Hkv), ceil(CUs / (n Hkv)))."""
 
     group = num_q_heads // num_kv_heads
-    cap = min(8, -(-cu_count // num_kv_heads))
+    cap = min(RAGGED_SPLIT_CAP, -(-cu_count // num_kv_heads))
     worst = 0
     for col_hi in (16, 32, 64):
         lmax = min(col_hi // group, max_seqlen)

@@ -159,6 +159,38 @@ def test_ragged_prefill_forced_tiles_and_short_only_calls():
                 assert A.max_abs(got, want) <= MAX_ABS and A.rel_l2(got, want) <= REL_L2, (lengths, tw, b)
 
 
+@pytest.mark.parametrize("paged", [False, True])
+def test_ragged_prefill_more_than_64_sequences(paged):
+    """150 sequences of 0-100 query tokens: the workgroups find their sequence by scanning
+    cu_seqlens 64 sequences per step (the tile grid's compaction and the decode classes' ranks and
+    split counts), so every sequence past the first 64 must land on its own rows too."""
+
+    rng = np.random.default_rng(90 + paged)
+    Hkv, G = 2, 4
+    lengths = [int(x) for x in rng.choice([0, 1, 1, 1, 2, 7, 12, 16, 17, 40, 100], size=150)]
+    lengths[140] = 100  # a tile-path sequence in the third step of 64
+    seg, ks, vs, meta = _ragged_case(rng, lengths, Hkv, G, paged, True)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    q = _bf(rng, (int(cu[-1]), Hkv * G, 128))
+    cu_t = torch.from_numpy(cu).to(DEV)
+    one_split = ops.prefill_attention(_t(q), causal=True, cu_seqlens_q=cu_t, max_seqlen_q=max(lengths), num_splits=1,
+                                      **seg)
+    auto = ops.prefill_attention(_t(q), causal=True, cu_seqlens_q=cu_t, max_seqlen_q=max(lengths), **seg)
+    worst = 0.0
+    for b, L in enumerate(lengths):
+        if L == 0:
+            continue
+        rows = slice(int(cu[b]), int(cu[b + 1]))
+        alone = ops.prefill_attention(_t(q[rows][None]), causal=True, num_splits=1, **_one(seg, b, meta))
+        assert torch.equal(one_split[rows], alone[0]), f"paged={paged}: sequence {b} (L={L}) differs from its own call"
+        want, _ = A.attention(q[rows].transpose(1, 0, 2)[None], ks[b], vs[b], causal_bottom_right=True)
+        want = bf16.round_bf16(want[0].transpose(1, 0, 2).astype(np.float32))
+        got = auto[rows].float().cpu().numpy()
+        worst = max(worst, A.rel_l2(got, want))
+        assert A.max_abs(got, want) <= MAX_ABS and A.rel_l2(got, want) <= REL_L2, f"paged={paged} sequence {b} (L={L})"
+    print(f"paged={paged}: 150 sequences, {sum(lengths)} rows, worst rel_l2 {worst:.2e} (automatic splits)", flush=True)
+
+
 def _rotary(positions):
     inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, device=positions.device).float() / 128))
     f = positions[..., None].float() * inv
