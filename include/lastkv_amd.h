@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 9
+#define LKV_ABI_VERSION 10
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -269,18 +269,28 @@ typedef struct lkv_prefill_args {
   const int32_t *cu_seqlens_q;
   int32_t max_seqlen_q;
   /* Key splits of the sequences that run on the decode kernel (at most 64 query rows per kv head):
-   * 0 chooses them from the grid and the workspace; n in [1, 1024] fixes n (the workspace must then
-   * also hold their split states, which lkv_prefill_workspace_bytes includes), so that a caller
-   * that fixes the split count gets the same arithmetic whatever the batch. */
+   * 0 chooses them from the grid and the workspace, and lets the tile kernel split its tiles' keys
+   * (at most 4 ways, merged by LSE) when its grid would leave CUs idle and the workspace holds the
+   * states; n in [1, 1024] fixes n (the workspace must then also hold their split states, which
+   * lkv_prefill_workspace_bytes includes) and runs the tiles unsplit, so that a caller that fixes
+   * the split count gets the same arithmetic whatever the batch. */
   int32_t num_splits;
 } lkv_prefill_args;
 
-/* Workspace bytes lkv_prefill_attn needs for these args: the fp16 V of every key block of every
+/* Workspace bytes lkv_prefill_attn wants for these args: the fp16 V of every key block of every
  * (sequence, kv head), 8 KiB per 32-token block (exact when the lengths and the ring start are
  * host constants, else bounded by the capacities), one flag byte per block (rows padded to 16
- * bytes) and one 16-byte word; or the decode kernel's split states (ragged calls, or num_splits > 1)
- * if those are larger.  Takes the same filled-in struct. */
+ * bytes) and one 16-byte word, then the states of the tile kernel's key splits (fp32 O and LSE per
+ * output row, query head and split) when its grid would leave CUs idle; or the decode kernel's
+ * split states (ragged calls, or num_splits > 1) if those are larger.  Takes the same filled-in
+ * struct. */
 int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args *args);
+
+/* The smallest workspace lkv_prefill_attn accepts for these args: lkv_prefill_workspace_bytes
+ * without the key splits' states (with less room than those need, a call splits its tiles' keys
+ * fewer ways, down to none).  No counterpart in the reference (its FA3 / FlashInfer calls manage
+ * their own scratch); for callers that size one workspace for many calls. */
+int64_t lkv_prefill_workspace_min_bytes(const lkv_prefill_args *args);
 
 int32_t lkv_prefill_attn(const lkv_prefill_args *args, lkv_stream_t stream);
 

@@ -11,7 +11,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 class LastKVNativeError(RuntimeError):
@@ -326,6 +326,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "lkv_decode_attn": (c_i32, [ctypes.POINTER(DecodeArgs), c_ptr]),
     "lkv_decode_attn_noalloc": (c_i32, [ctypes.POINTER(DecodeArgs), c_ptr]),
     "lkv_prefill_workspace_bytes": (c_i64, [ctypes.POINTER(PrefillArgs)]),
+    "lkv_prefill_workspace_min_bytes": (c_i64, [ctypes.POINTER(PrefillArgs)]),
     "lkv_prefill_attn": (c_i32, [ctypes.POINTER(PrefillArgs), c_ptr]),
     "lkv_merge_states": (c_i32, [ctypes.POINTER(MergeArgs), c_ptr]),
     "lkv_append_paged": (c_i32, [ctypes.POINTER(AppendArgs), c_ptr]),

@@ -62,6 +62,12 @@ struct PrefillParams {
   // decode_rows query rows per kv head run on the decode kernel and are skipped here.
   const int32_t* cu;
   int32_t rows, decode_rows;
+  // split-K over the keys for grids that would leave CUs idle: tile_splits key ranges per tile, each
+  // writing its rows' normalised fp32 O and base-2 LSE to ws_o [row, Hq, S, 128] / ws_lse
+  // [row, Hq, S] (row = the lse row), merged by prefill_split_combine_kernel; 1 = no split
+  int32_t tile_splits;
+  float* ws_o;
+  float* ws_lse;
 };
 
 // Query tokens of sequence b and the q / out / lse row of its token 0.
@@ -367,6 +373,7 @@ __device__ inline bool pair_needs_wide(const PrefillParams& p, int b, int kvh) {
   return tile_needs_wide(p, b, kvh, sv.nb0 + local_blocks(sv, sv.n1));
 }
 
+constexpr int kMaxTileSplits = 4;  // key splits of a tile (the wide instance marks the others of its rows empty)
 constexpr int kTileRing = 4;       // LDS block buffers of the tile kernel
 constexpr int kTileBuf = 1024;     // uint4 per block buffer (16 KiB)
 
@@ -378,13 +385,17 @@ constexpr int kTileBuf = 1024;     // uint4 per block buffer (16 KiB)
 // (i + 2) % 4, load block i + 4, one barrier.
 // The 2-wave instance (calls of at most 64 query rows per kv head, bound by HBM, not by the matrix
 // pipe) splits P into fp16 hi + lo and runs P V twice, so its probabilities carry ~22 bits
-// instead of 11.  prefill_tile runs query tile `tile` of (sequence b, kv head kvh).
+// instead of 11.  prefill_tile runs query tile `tile` of (sequence b, kv head kvh), over key split
+// `split` of p.tile_splits: split s of S' = min(S, older blocks) covers blocks [start(s),
+// start(s + 1)) with start(s) = min(s * ceil(nbt / S'), nb0 - S' + s), so every split begins with an
+// older block that every row sees (the exact maximum of its first block is then finite for every
+// row); splits from S' on are empty (their states say so).
 // kWide: the instance for tiles whose V does not fit fp16 (the pre-pass flagged one of their blocks):
 // V staged as bf16 from the caches (older blocks as bf16(V * s)), P split into bf16 hi + lo, P V and
 // the row sums on bf16 MFMAs; the fp16 instance skips those tiles and this one runs only them.
 template <int NW, int CG, bool kPaged, bool kWide = false>
 __device__ __attribute__((always_inline)) inline void prefill_tile(const PrefillParams& p, const int b, const int kvh,
-                                                                   const int tile, uint4* lds) {
+                                                                   const int tile, const int split, uint4* lds) {
   constexpr bool kSplitP = NW == 2 || kWide;
   constexpr int kStages = 2;  // register stage sets (global loads run kStages steps ahead of their LDS store)
   constexpr int kDist = 2;    // step i stores block i + kDist into the LDS ring
@@ -419,6 +430,21 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   const bool needs_wide = tile_needs_wide(p, b, kvh, nbt);
   if (kWide && !needs_wide) return;
   const float vs_older = p.vscale_mode ? p.vscale[kvh] : 1.f;  // (the wide instance's V scale)
+  // this split's blocks [kb0, kb1) (the wide instance runs every block as split 0)
+  const int S = kWide ? 1 : p.tile_splits;
+  int kb0 = 0, kb1 = nbt;
+  if (S > 1) {
+    const int se = min(S, sv.nb0);
+    if (split >= max(se, 1)) {
+      kb1 = 0;
+    } else if (se > 1) {
+      const int q = (nbt + se - 1) / se;
+      kb0 = min(split * q, sv.nb0 - se + split);
+      if (split + 1 < se) kb1 = min((split + 1) * q, sv.nb0 - se + split + 1);
+    }
+  }
+  kb0 = __builtin_amdgcn_readfirstlane(kb0);
+  kb1 = __builtin_amdgcn_readfirstlane(kb1);
 
   uint4 qf[CG][4];
   int lim[CG];  // last visible local-segment token of this lane's column
@@ -457,14 +483,14 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
     for (int nb = 0; nb < 8; ++nb) o[cg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  if (nbt > 0) {
+  if (kb1 > kb0) {
     SegBase rsrc;
     rsrc.v16 = uniform_ptr(p.v16 + (static_cast<int64_t>(b) * p.hkv + kvh) * p.v16_blocks * kBlockElems);
     rsrc.v16_bytes = p.v16_blocks * (kBlockElems * 2);
     const int lane_off = n16 * 64 + g4 * 16;
     // Loads are unconditional (indices past the end re-read the last block, an L2 hit) so that
     // the compiler can count outstanding loads for s_waitcnt.
-    const int last = nbt - 1;
+    const int last = kb1 - 1;
 
     Stage<NW> sets[kStages];
     // (the V blocks of the wide instance; the fp16 instance reads V from the workspace)
@@ -472,12 +498,12 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
     auto vs_of = [&](int blk) __attribute__((always_inline)) { return kWide && blk < sv.nb0 ? vs_older : 1.f; };
 #pragma unroll
     for (int j = 0; j < kStages; ++j)
-      stage_load<NW, kWide>(sets[j], rsrc, k_block<kPaged>(sv, min(j, last)), vb(min(j, last)), min(j, last), wave,
-                            lane_off);
+      stage_load<NW, kWide>(sets[j], rsrc, k_block<kPaged>(sv, min(kb0 + j, last)), vb(min(kb0 + j, last)),
+                            min(kb0 + j, last), wave, lane_off);
 #pragma unroll
     for (int j = 0; j < kDist; ++j) {
-      stage_store<NW, kWide>(sets[j % kStages], lds + j * kBuf, wave, lane, vs_of(min(j, last)));
-      const int lb = min(j + kStages, last);
+      stage_store<NW, kWide>(sets[j % kStages], lds + j * kBuf, wave, lane, vs_of(min(kb0 + j, last)));
+      const int lb = min(kb0 + j + kStages, last);
       stage_load<NW, kWide>(sets[j % kStages], rsrc, k_block<kPaged>(sv, lb), vb(lb), lb, wave, lane_off);
     }
     if (!kWide && needs_wide) {
@@ -486,7 +512,7 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
     }
     __syncthreads();
 
-    // S^T of block 0: sc[cg][u] holds tokens 8 * g4 + 4u .. + 3 of this lane's column n16 of
+    // S^T of block kb0: sc[cg][u] holds tokens 8 * g4 + 4u .. + 3 of this lane's column n16 of
     // group cg
     f32x4 sc[CG][2];
 #pragma unroll
@@ -508,7 +534,7 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
     // test is then the packed-probability overflow check, so the compiler keeps the QK^T MFMAs of
     // block i + 1 and the probabilities of block i in one scheduling region and interleaves them.
     {
-      const BlockRef r0 = block_range(sv, 0);
+      const BlockRef r0 = block_range(sv, kb0);
       float s0[CG][8];
 #pragma unroll
       for (int cg = 0; cg < CG; ++cg)
@@ -656,13 +682,13 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
     // Whole rounds of the ring in the loop, the 0-3 remaining blocks after it: an exit from the
     // middle of a round gives the loop header a second predecessor on which that round's stage
     // loads are still in flight, and the header then waits for every load each round.
-    int blk = 0;
+    int blk = kb0;
     // (the remaining blocks as independent tests, not nested ones: 0.5 points faster on configs 3-5)
-    for (; blk + kRing <= nbt; blk += kRing)
+    for (; blk + kRing <= kb1; blk += kRing)
       unroll_steps(std::make_integer_sequence<int, kRing>{},
                    [&](auto jc) __attribute__((always_inline)) { step(jc, blk + decltype(jc)::value); });
     unroll_steps(std::make_integer_sequence<int, kRing - 1>{}, [&](auto jc) __attribute__((always_inline)) {
-      if (blk + decltype(jc)::value < nbt) step(jc, blk + decltype(jc)::value);
+      if (blk + decltype(jc)::value < kb1) step(jc, blk + decltype(jc)::value);
     });
   }
 
@@ -673,7 +699,16 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
     const float lt = ol[cg][0];
     const float linv = lt > 0.f ? 1.f / lt : 0.f;
     const int row = row0 + 16 * cg + n16;
-    if (row < rows_total) {
+    if (row < rows_total && p.tile_splits > 1) {  // this split's state (the wide instance: split 0)
+      const int tok = row / G, h = row - tok * G;
+      const int64_t srow = ((sr.lse0 + tok) * p.hq + kvh * G + h) * p.tile_splits + (kWide ? 0 : split);
+      float* orow = p.ws_o + srow * kHeadDim;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+        *reinterpret_cast<f32x4*>(orow + 16 * nb + 4 * g4) = o[cg][nb] * linv;
+      if (g4 == 0) p.ws_lse[srow] = lt > 0.f ? rs[cg].mc + __log2f(lt) : kNegInf;
+      if (kWide && g4 < p.tile_splits - 1) p.ws_lse[srow + 1 + g4] = kNegInf;  // (the other splits, <= 3: empty)
+    } else if (row < rows_total) {
       const int tok = row / G, h = row - tok * G;
       uint16_t* orow = p.out + sr.o0 + tok * p.out_st + static_cast<int64_t>(kvh * G + h) * kHeadDim;
 #pragma unroll
@@ -738,13 +773,17 @@ template <int NW, int CG, int WPE, bool kPaged>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void prefill_kernel(
     const PrefillParams p) {
   __shared__ uint4 lds[kTileRing * kTileBuf];
+  // key splits: the grid is tile_splits copies of the tile grid, the split the slowest index
+  const int per_split = static_cast<int>(gridDim.x) / p.tile_splits;
+  const int split = static_cast<int>(blockIdx.x) / per_split;
+  const int id = static_cast<int>(blockIdx.x) - split * per_split;
   int b, kvh, tile, tiles;
   if (p.cu != nullptr) {
-    kvh = static_cast<int>(blockIdx.x) % p.hkv;
-    if (!ragged_tile(p, static_cast<int>(blockIdx.x) / p.hkv, NW * 32, b, tile)) return;  // (workgroup-uniform)
+    kvh = id % p.hkv;
+    if (!ragged_tile(p, id / p.hkv, NW * 32, b, tile)) return;  // (workgroup-uniform)
     tiles = (seq_rows(p, b).L * p.group + NW * 32 - 1) / (NW * 32);
   } else {
-    const int logical = xcd_logical_index(blockIdx.x, gridDim.x);
+    const int logical = xcd_logical_index(id, per_split);
     tiles = p.tiles;
     tile = logical % tiles;
     kvh = (logical / tiles) % p.hkv;
@@ -752,7 +791,77 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   }
   // (one call site: the tile body is inlined once)
   prefill_tile<NW, CG, kPaged>(p, __builtin_amdgcn_readfirstlane(b), __builtin_amdgcn_readfirstlane(kvh),
-                               __builtin_amdgcn_readfirstlane(p.causal ? tiles - 1 - tile : tile), lds);
+                               __builtin_amdgcn_readfirstlane(p.causal ? tiles - 1 - tile : tile),
+                               __builtin_amdgcn_readfirstlane(split), lds);
+}
+
+// Merges the key splits of one (row, query head) per wave: O = sum_s 2^(lse_s - lse) O_s with
+// lse = log2(sum_s 2^lse_s) (splits with no visible key have lse_s = -inf and weight 0), then
+// the output rounding of the unsplit path (bf16, optional bf16(bf16(o) * s)) and the natural-log
+// LSE.  Rows of sequences that are not on the tile path (a ragged call's decode rows) are skipped.
+__global__ __launch_bounds__(256) void prefill_split_combine_kernel(const PrefillParams p, int64_t rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // (row, head)
+  if (item >= rows * p.hq) return;
+  const int64_t row = item / p.hq;  // the lse row: b * L + token, or the ragged row
+  const int h = static_cast<int>(item - row * p.hq);
+  const int S = p.tile_splits;
+  const int64_t s0 = item * S;
+  // every split's state is loaded up front, beside the sequence lookup
+  float ls[kMaxTileSplits];
+  float2 x[kMaxTileSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxTileSplits; ++s) {
+    ls[s] = s < S ? p.ws_lse[s0 + s] : kNegInf;
+    x[s] = s < S ? *reinterpret_cast<const float2*>(p.ws_o + (s0 + s) * kHeadDim + 2 * lane) : float2{0.f, 0.f};
+  }
+  int b = 0;
+  int64_t tok = row;
+  SeqRows sr;
+  if (p.cu == nullptr) {
+    b = static_cast<int>(row / p.L);
+    tok = row - static_cast<int64_t>(b) * p.L;
+    sr = seq_rows(p, b);
+  } else {  // the sequence holding this row: the last b with cu[b] <= row (a wave scan, 64 per step)
+    int c_lo = 0, c_hi = 0;
+    for (int i0 = 0; i0 < p.batch; i0 += 64) {
+      const int i = i0 + lane;
+      const int c = i <= p.batch ? min(max(p.cu[i], 0), p.rows) : p.rows;  // cu[b], clamped as seq_rows does
+      const uint64_t m = __builtin_amdgcn_ballot_w64(i < p.batch && c <= row);
+      if (m == 0) break;
+      const int l = 63 - __builtin_clzll(m);
+      b = i0 + l;
+      c_lo = __shfl(c, l);
+      c_hi = l < 63 ? __shfl(c, l + 1) : min(max(p.cu[b + 1], 0), p.rows);
+    }
+    sr.L = min(max(c_hi, c_lo) - c_lo, p.L);
+    sr.o0 = static_cast<int64_t>(c_lo) * p.out_st;
+    sr.lse0 = c_lo;
+    tok = row - sr.lse0;
+    if (tok < 0 || tok >= sr.L) return;
+  }
+  if (!on_tile_path(p, sr)) return;  // (a ragged call's decode rows)
+  float m = kNegInf;
+#pragma unroll
+  for (int s = 0; s < kMaxTileSplits; ++s) m = fmaxf(m, ls[s]);
+  float l = 0.f, o0 = 0.f, o1 = 0.f;
+  if (m != kNegInf) {
+#pragma unroll
+    for (int s = 0; s < kMaxTileSplits; ++s) {
+      if (ls[s] == kNegInf) continue;  // (no visible key, or no such split: weight 0)
+      const float w = fast_exp2(ls[s] - m);
+      l += w;
+      o0 += w * x[s].x;
+      o1 += w * x[s].y;
+    }
+  }
+  const float linv = l > 0.f ? 1.f / l : 0.f;
+  uint32_t w01 = pack_bf16x2(o0 * linv, o1 * linv);
+  const int kvh = h / p.group;
+  if (p.out_scale != nullptr) w01 = pack_bf16x2(bf16_lo(w01) * p.out_scale[kvh], bf16_hi(w01) * p.out_scale[kvh]);
+  uint16_t* orow = p.out + sr.o0 + tok * p.out_st + static_cast<int64_t>(h) * kHeadDim;
+  *reinterpret_cast<uint32_t*>(orow + 2 * lane) = w01;
+  if (p.lse != nullptr && lane == 0) p.lse[row * p.hq + h] = l > 0.f ? (m + __log2f(l)) * kLn2 : kNegInf;
 }
 
 // The wide instance: one workgroup per (sequence, kv head) pair at a time, min(pairs, CUs) of them.
@@ -770,7 +879,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   for (int pair = blockIdx.x; pair < pairs; pair += gridDim.x) {
     if (!pair_needs_wide(p, pair / p.hkv, pair % p.hkv)) continue;  // (workgroup-uniform)
     for (int tile = 0; tile < p.tiles; ++tile) {
-      prefill_tile<NW, CG, kPaged, true>(p, pair / p.hkv, pair % p.hkv, tile, lds);
+      prefill_tile<NW, CG, kPaged, true>(p, pair / p.hkv, pair % p.hkv, tile, 0, lds);
       __syncthreads();  // the next tile's staging reuses the LDS ring
     }
   }
@@ -808,9 +917,72 @@ int64_t v16_region_bytes(const lkv_prefill_args* a, int64_t vblocks) {
 
 }  // namespace
 
-extern "C" int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args* a) {
+namespace {
+
+// The tile kernel's plan for a call: waves per workgroup, tiles per (sequence, kv head), the grid,
+// and the key splits it would take with room for their states.  Each wave takes 32 query rows.
+// Short calls (<= 64 rows per kv head) would take 2 waves (with tile_waves 0 they run on the decode
+// kernel instead).  Otherwise 8 waves (two per SIMD, one workgroup per CU), or 4 waves (two
+// workgroups per CU) when the 4-wave grid still leaves at most one workgroup per CU, which keeps
+// twice the CUs busy (measured on 256 CUs: at B = 1 of a config-3 piece 23 vs 18 %; from B = 2 up
+// the 8-wave tile is 0.5-1.5 points ahead).  A ragged call takes 4-wave tiles (the host does not
+// know how many of its sequences are long, and a step of decode rows and one or two prefill pieces
+// would leave half the CUs idle with 8-wave tiles) over a grid of at most ceil(T * G / rows_per_wg)
+// + B tiles per kv head.  A grid of fewer 4-wave workgroups than two per CU, or of 8-wave ones for
+// at most half the CUs, splits each tile's keys over up to 4 workgroups when the call has an older
+// segment and leaves the split counts to the library (num_splits 0): a 1024-token piece of one
+// sequence over 8K keys runs 256 4-wave workgroups, one wave per SIMD, and its key splits let a
+// second workgroup share each CU.
+struct TilePlan {
+  bool runs;          // the tile kernel runs (some sequence has > 64 rows per kv head, or tile_waves)
+  int waves;
+  int64_t tiles, wgs, rows_all;  // rows_all: the output rows (B * L, or T ragged)
+  int splits;         // key splits with room for their states
+};
+
+TilePlan tile_plan(const lkv_prefill_args* a) {
   using namespace lkv;
-  if (a == nullptr || a->batch <= 0 || a->num_kv_heads <= 0 || a->num_q_heads <= 0) return 0;
+  TilePlan t{};
+  const bool ragged = a->cu_seqlens_q != nullptr;
+  const int group = a->num_q_heads / a->num_kv_heads;
+  const int64_t seq_tokens = ragged ? std::min(a->max_seqlen_q, a->tokens) : a->tokens;
+  const int64_t rows = seq_tokens * group;
+  const int64_t heads = static_cast<int64_t>(a->num_kv_heads) * a->batch;
+  t.runs = rows > 64 || a->tile_waves != 0;
+  const bool wide = rows > 64;
+  t.waves = wide ? 8 : 2;
+  const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  if (wide && a->tile_waves != 0) {
+    t.waves = a->tile_waves;
+  } else if (wide && ragged) {
+    t.waves = 4;
+  } else if (wide) {
+    const int64_t wgs4 = (rows + 127) / 128 * heads;
+    if (wgs4 <= cus) t.waves = 4;
+  }
+  const int64_t rows_per_wg = t.waves * 32;
+  t.tiles = (rows + rows_per_wg - 1) / rows_per_wg;
+  const int64_t ragged_tiles = (static_cast<int64_t>(a->tokens) * group + rows_per_wg - 1) / rows_per_wg;
+  t.wgs = ragged ? (ragged_tiles + a->batch) * a->num_kv_heads : t.tiles * heads;
+  t.rows_all = ragged ? a->tokens : static_cast<int64_t>(a->batch) * a->tokens;
+  t.splits = 1;
+  const int64_t est = ragged ? ragged_tiles * a->num_kv_heads : t.wgs;  // the tiles that work
+  // 4-wave tiles: below two workgroups per CU; 8-wave tiles (one per CU): at most half the CUs busy
+  const bool idle = t.waves == 4 ? est < 2 * cus : (t.waves == 8 && est * 2 <= cus);
+  if (t.runs && idle && a->num_splits == 0 && a->older_k != nullptr && est > 0)
+    t.splits = static_cast<int>(std::min<int64_t>(kMaxTileSplits, (cus * (t.waves == 4 ? 2 : 1) + est - 1) / est));
+  return t;
+}
+
+// Bytes of the key splits' states: fp32 O and LSE per (output row, query head, split).
+int64_t tile_split_bytes(const lkv_prefill_args* a, const TilePlan& t, int splits) {
+  return splits > 1 ? t.rows_all * a->num_q_heads * splits * (lkv::kHeadDim + 1) * 4 : 0;
+}
+
+// The workspace a call cannot run without: the V pre-pass's region, or the decode kernel's split
+// states if larger (they are used before the pre-pass runs, in the same bytes).
+int64_t min_workspace_bytes(const lkv_prefill_args* a) {
+  using namespace lkv;
   const int64_t v16 = v16_region_bytes(a, v16_blocks(a));
   const int64_t per_row = (kHeadDim + 2) * 4;  // one split state
   if (a->cu_seqlens_q != nullptr && a->tile_waves == 0 && a->max_seqlen_q >= 1 && a->tokens > 0) {
@@ -831,6 +1003,21 @@ extern "C" int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args* a) {
   if (a->num_splits <= 1) return v16;
   // split states of the decode kernel's sequences: [B, L, Hq] rows
   return std::max(v16, static_cast<int64_t>(a->batch) * std::max(a->tokens, 0) * a->num_q_heads * a->num_splits * per_row);
+}
+
+}  // namespace
+
+extern "C" int64_t lkv_prefill_workspace_bytes(const lkv_prefill_args* a) {
+  using namespace lkv;
+  if (a == nullptr || a->batch <= 0 || a->num_kv_heads <= 0 || a->num_q_heads <= 0) return 0;
+  const TilePlan t = tile_plan(a);
+  // the tile kernel's key-split states follow the V pre-pass's region
+  return std::max(min_workspace_bytes(a), v16_region_bytes(a, v16_blocks(a)) + tile_split_bytes(a, t, t.splits));
+}
+
+extern "C" int64_t lkv_prefill_workspace_min_bytes(const lkv_prefill_args* a) {
+  if (a == nullptr || a->batch <= 0 || a->num_kv_heads <= 0 || a->num_q_heads <= 0) return 0;
+  return min_workspace_bytes(a);
 }
 
 // The tile kernel instance for this call's wave count and addressing.
@@ -907,11 +1094,13 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   // query tokens per sequence (ragged: an upper bound)
   const int64_t seq_tokens = ragged ? std::min(a->max_seqlen_q, a->tokens) : a->tokens;
   const int64_t vblocks = v16_blocks(a);
-  const int64_t need = lkv_prefill_workspace_bytes(a);
+  const int64_t need = min_workspace_bytes(a);
   LKV_REQUIRE(vblocks * kBlockElems * 2 < (1LL << 31), "too many key blocks per sequence");
   LKV_REQUIRE(vblocks == 0 || (a->workspace != nullptr && a->workspace_bytes >= need),
-              "prefill needs a workspace of %lld bytes (lkv_prefill_workspace_bytes), got %lld",
-              static_cast<long long>(need), static_cast<long long>(a->workspace_bytes));
+              "prefill needs a workspace of at least %lld bytes (lkv_prefill_workspace_bytes: %lld with the key "
+              "splits' states), got %lld",
+              static_cast<long long>(need), static_cast<long long>(lkv_prefill_workspace_bytes(a)),
+              static_cast<long long>(a->workspace_bytes));
   LKV_REQUIRE((reinterpret_cast<uintptr_t>(a->workspace) & 15) == 0, "workspace must be 16-byte aligned");
   hipStream_t s = as_stream(stream);
   // Sequences of at most 64 query rows per kv head (e.g. decode tokens, or up to 16 tokens of a GQA
@@ -954,33 +1143,19 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   p.cu = a->cu_seqlens_q;
   p.rows = a->tokens;
   p.decode_rows = ragged && short_on_decode ? 64 : -1;
-  const int64_t rows = seq_tokens * group;
   const int64_t heads = static_cast<int64_t>(a->num_kv_heads) * a->batch;
-  // Each wave takes 32 query rows.  Short calls (<= 64 rows per kv head): 2 waves.  Otherwise 8
-  // waves (two per SIMD, one workgroup per CU), or 4 waves (two workgroups per CU) when the 4-wave
-  // grid still leaves at most one workgroup per CU, which keeps twice the CUs busy (measured on 256
-  // CUs: at B = 1 of a config-3 piece 23 vs 18 %; from B = 2 up the 8-wave tile is 0.5-1.5 points ahead).
-  // A ragged call sizes the grid by its longest sequence; the tiles past a sequence's own rows exit.
-  // It takes 4-wave tiles: the host does not know how many of its sequences are long, and a step of
-  // decode rows and one or two prefill pieces would leave half the CUs idle with 8-wave tiles.
-  const bool wide = rows > 64;
-  int waves = wide ? 8 : 2;
-  if (wide && a->tile_waves != 0) {
-    waves = a->tile_waves;
-  } else if (wide && ragged) {
-    waves = 4;
-  } else if (wide) {
-    const int64_t cus = device_cu_count();
-    const int64_t wgs4 = (rows + 127) / 128 * heads;
-    if (cus > 0 && wgs4 <= cus) waves = 4;
-  }
-  const int64_t rows_per_wg = waves * 32;
-  const int64_t tiles = (rows + rows_per_wg - 1) / rows_per_wg;
-  // ragged: at most ceil(T * G / rows_per_wg) + B tiles over the sequences, each of Hkv workgroups
-  const int64_t wgs = ragged ? ((static_cast<int64_t>(a->tokens) * group + rows_per_wg - 1) / rows_per_wg + a->batch) *
-                                   a->num_kv_heads
-                             : tiles * heads;
-  LKV_REQUIRE(wgs < (1LL << 31), "too many query rows");
+  const TilePlan plan = tile_plan(a);
+  const int waves = plan.waves;
+  const int64_t tiles = plan.tiles, wgs = plan.wgs;
+  // key splits: as many as the workspace holds the states of (1 without room)
+  int splits = plan.splits;
+  const int64_t v16_bytes = v16_region_bytes(a, vblocks);
+  while (splits > 1 && v16_bytes + tile_split_bytes(a, plan, splits) > a->workspace_bytes) --splits;
+  if (vblocks == 0) splits = 1;
+  LKV_REQUIRE(wgs * splits < (1LL << 31), "too many query rows");
+  p.tile_splits = splits;
+  p.ws_o = splits > 1 ? reinterpret_cast<float*>(static_cast<uint8_t*>(a->workspace) + v16_bytes) : nullptr;
+  p.ws_lse = splits > 1 ? p.ws_o + plan.rows_all * a->num_q_heads * splits * kHeadDim : nullptr;
   p.tiles = static_cast<int32_t>(tiles);
   p.hkv = a->num_kv_heads;
   p.batch = a->batch;
@@ -998,7 +1173,7 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
       v16_stage_kernel<false, 1><<<vgrid, 256, 0, s>>>(p);
     if (const int32_t e = check_launch("lkv_prefill_attn (V pre-pass)")) return e;
   }
-  const dim3 grid(static_cast<unsigned>(wgs));
+  const dim3 grid(static_cast<unsigned>(wgs * splits));
   launch_tiles(waves, paged, grid, p, s);
   if (const int32_t e = check_launch("lkv_prefill_attn")) return e;
   if (vblocks == 0) return LKV_OK;
@@ -1007,5 +1182,10 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   // flags at a time
   const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
   launch_wide(waves, paged, static_cast<int>(std::min(heads, cus)), p, s);
-  return check_launch("lkv_prefill_attn (wide-range V)");
+  if (const int32_t e = check_launch("lkv_prefill_attn (wide-range V)")) return e;
+  if (splits == 1) return LKV_OK;
+  const int64_t items = plan.rows_all * a->num_q_heads;  // (row, query head) pairs, 4 per workgroup
+  LKV_REQUIRE((items + 3) / 4 < (1LL << 31), "too many query rows");
+  prefill_split_combine_kernel<<<static_cast<unsigned>((items + 3) / 4), 256, 0, s>>>(p, plan.rows_all);
+  return check_launch("lkv_prefill_attn (key-split merge)");
 }

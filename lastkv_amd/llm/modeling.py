@@ -154,7 +154,9 @@ class LastKVAttention(nn.Module):
         if L == 1:
             out = ops.decode_attention(qn.view(B, H, D), **segments)
         else:
-            ws = cache.prefill_workspace(ops.prefill_workspace_bytes(B, Hkv, rec, p0 + L - rec, rec % ops.BLOCK_TOKENS))
+            # (room for the tile kernel's key splits, which calls of few query tiles take)
+            ws = cache.prefill_workspace(ops.prefill_workspace_bytes(B, Hkv, rec, p0 + L - rec, rec % ops.BLOCK_TOKENS,
+                                                                     query_rows=B * L, num_q_heads=H))
             out = ops.prefill_attention(qn, causal=True, workspace=ws, **segments)
         return self.o_proj(out.reshape(B, L, H * D))
 

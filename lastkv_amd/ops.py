@@ -489,12 +489,13 @@ def prefill_attention(
     a.out, a.out_stride_b, a.out_stride_t = out.data_ptr(), out.stride(0), out.stride(1)
     a.lse = _ptr(lse)
     lib = _lib.load()
-    need = int(lib.lkv_prefill_workspace_bytes(ctypes.byref(a)))
-    if workspace is None:
-        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+    if workspace is None:  # room for the tile kernel's key splits too
+        workspace = torch.empty(max(int(lib.lkv_prefill_workspace_bytes(ctypes.byref(a))), 16), dtype=torch.uint8,
+                                device=device)
     _require(workspace.device == device and workspace.is_contiguous(), "workspace must be a contiguous tensor on the query's device")
     a.workspace = workspace.data_ptr()
     a.workspace_bytes = workspace.numel() * workspace.element_size()
+    need = int(lib.lkv_prefill_workspace_min_bytes(ctypes.byref(a)))
     _require(a.workspace_bytes >= need, f"prefill workspace too small: {a.workspace_bytes} < {need} bytes")
     _lib.check(lib.lkv_prefill_attn(ctypes.byref(a), _stream(device)), "lkv_prefill_attn")
     return out[0] if ragged else out
@@ -506,13 +507,22 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, num_splits: int) -> int
     return int(_lib.load().lkv_decode_workspace_bytes(batch, num_q_heads, num_splits))
 
 
-def prefill_workspace_bytes(batch: int, kv_heads: int, older_tokens: int, local_tokens: int, local_lead: int = 31) -> int:
+def prefill_workspace_bytes(batch: int, kv_heads: int, older_tokens: int, local_tokens: int, local_lead: int = 31,
+                            query_rows: int = 0, num_q_heads: int = 0, cu_count: int | None = None) -> int:
     """Upper bound of the prefill workspace for segments of at most ``older_tokens`` and
-    ``local_tokens`` keys (``local_lead``: the ring start's offset inside its 32-token block)."""
+    ``local_tokens`` keys (``local_lead``: the ring start's offset inside its 32-token block).  With
+    ``query_rows`` (the call's output rows: B * L, or T ragged) and ``num_q_heads`` it also holds the
+    tile kernel's key-split states: a call splits its tiles' keys (at most 4 ways) only when its tile
+    grid leaves CUs idle (fewer 4-wave workgroups of 128 rows than two per CU), so only when
+    query_rows * num_q_heads < 256 * CUs, and then needs rows * Hq * splits * 129 fp32 values."""
 
     blocks = -(-older_tokens // 32) + (-(-(local_lead + local_tokens) // 32) if local_tokens > 0 else 0)
     # fp16 V of every block, then one flag byte per block (rows padded to 16 bytes), then one 16-byte word
-    return batch * kv_heads * (blocks * 8192 + -(-blocks // 16) * 16) + 16
+    v16 = batch * kv_heads * (blocks * 8192 + -(-blocks // 16) * 16) + 16
+    cus = cu_count if cu_count is not None else (_cu_count(torch.device("cuda")) if query_rows > 0 else 0)
+    if query_rows > 0 and num_q_heads > 0 and query_rows * num_q_heads < 256 * cus:
+        v16 += query_rows * num_q_heads * 4 * (HEAD_DIM + 1) * 4
+    return v16
 
 
 def prefill_split_state_bytes(rows: int, num_q_heads: int, num_splits: int) -> int:

@@ -383,7 +383,9 @@ class LastKVFastPath:
             # device-resident lengths: the kernel sizes its fp16 V copy by the older table's width
             # and the whole ring (a ragged call's short rows share it for their split state)
             width = max(1, -(-max(r.older for r in parsed) // BLOCK))
-            need = ops.prefill_workspace_bytes(B, P.kv_heads, width * BLOCK, P.ring_tokens)
+            # (with room for the tile kernel's key splits, which steps of few prefill rows take)
+            need = ops.prefill_workspace_bytes(B, P.kv_heads, width * BLOCK, P.ring_tokens, query_rows=self.tokens,
+                                               num_q_heads=Hq, cu_count=ops._cu_count(P.device))
             if uniform:
                 need = max(need, ops.prefill_split_state_bytes(self.tokens, Hq, self.num_splits or 0))
             else:

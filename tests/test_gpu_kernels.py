@@ -127,8 +127,9 @@ def test_prefill_bidirectional_local_segment(L, Hq, Hkv, T0, n_local):
 @pytest.mark.parametrize("L,Hq,Hkv,causal", [(300, 8, 2, True), (129, 12, 12, False), (520, 32, 8, True)])
 def test_prefill_tile_waves_agree_and_match_oracle(L, Hq, Hkv, causal):
     """The 4-wave and 8-wave tiles give the same bits (blocks past a row's causal limit add exact
-    zeros), and both match the oracle; 4 x 32 and 8 x 32 row tiles end at different rows, so
-    tile edges fall inside GQA groups and causal steps."""
+    zeros) with their keys unsplit (num_splits = 1), and match the oracle, as does the automatic
+    call (whose small grid splits the tiles' keys); 4 x 32 and 8 x 32 row tiles end at different
+    rows, so tile edges fall inside GQA groups and causal steps."""
 
     rng = np.random.default_rng(L + Hq)
     B, T0, n_local = 2, 233, L + 61
@@ -146,14 +147,18 @@ def test_prefill_tile_waves_agree_and_match_oracle(L, Hq, Hkv, causal):
     outs, lses = [], []
     for tw in (4, 8, 0):
         lse = torch.empty((B, L, Hq), dtype=torch.float32, device=DEV)
-        outs.append(ops.prefill_attention(_t(q), tile_waves=tw, lse=lse, **kw))
+        outs.append(ops.prefill_attention(_t(q), tile_waves=tw, lse=lse, num_splits=1, **kw))
         lses.append(lse)
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     assert torch.equal(lses[0], lses[1]) and torch.equal(lses[0], lses[2])
     want, want_lse = A.attention(q.transpose(0, 2, 1, 3), np.concatenate([ok, lk], 2), np.concatenate([ov, lv], 2),
                                  causal_bottom_right=causal)
-    _close(outs[0], bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32)), f"tile waves L={L} Hq={Hq}")
+    want = bf16.round_bf16(want.transpose(0, 2, 1, 3).astype(np.float32))
+    _close(outs[0], want, f"tile waves L={L} Hq={Hq}")
     np.testing.assert_allclose(lses[0].cpu().numpy(), want_lse.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
+    lse = torch.empty((B, L, Hq), dtype=torch.float32, device=DEV)
+    _close(ops.prefill_attention(_t(q), lse=lse, **kw), want, f"automatic (key splits) L={L} Hq={Hq}")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse.transpose(0, 2, 1), rtol=1e-4, atol=1e-4)
     with pytest.raises(RuntimeError, match="tile_waves"):
         ops.prefill_attention(_t(q), tile_waves=5, **kw)
 
