@@ -386,10 +386,10 @@ constexpr int kTileBuf = 1024;     // uint4 per block buffer (16 KiB)
 // The 2-wave instance (calls of at most 64 query rows per kv head, bound by HBM, not by the matrix
 // pipe) splits P into fp16 hi + lo and runs P V twice, so its probabilities carry ~22 bits
 // instead of 11.  prefill_tile runs query tile `tile` of (sequence b, kv head kvh), over key split
-// `split` of p.tile_splits: split s of S' = min(S, older blocks) covers blocks [start(s),
-// start(s + 1)) with start(s) = min(s * ceil(nbt / S'), nb0 - S' + s), so every split begins with an
-// older block that every row sees (the exact maximum of its first block is then finite for every
-// row); splits from S' on are empty (their states say so).
+// `split` of p.tile_splits: split s of S' covers blocks [s q, (s + 1) q), q = ceil(nbt / S'), the
+// last one to nbt, with S' <= S the most splits that all start in the older segment ((S' - 1) q <
+// nb0), so every split begins with an older block that every row sees (the exact maximum of its
+// first block is then finite for every row); splits from S' on are empty (their states say so).
 // kWide: the instance for tiles whose V does not fit fp16 (the pre-pass flagged one of their blocks):
 // V staged as bf16 from the caches (older blocks as bf16(V * s)), P split into bf16 hi + lo, P V and
 // the row sums on bf16 MFMAs; the fp16 instance skips those tiles and this one runs only them.
@@ -434,13 +434,16 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   const int S = kWide ? 1 : p.tile_splits;
   int kb0 = 0, kb1 = nbt;
   if (S > 1) {
-    const int se = min(S, sv.nb0);
+    // as many equal splits as start inside the older segment (a short older segment would leave
+    // the last split most of the keys: slower than no split)
+    int se = min(S, sv.nb0);
+    while (se > 1 && (se - 1) * ((nbt + se - 1) / se) > sv.nb0 - 1) --se;
     if (split >= max(se, 1)) {
       kb1 = 0;
     } else if (se > 1) {
       const int q = (nbt + se - 1) / se;
-      kb0 = min(split * q, sv.nb0 - se + split);
-      if (split + 1 < se) kb1 = min((split + 1) * q, sv.nb0 - se + split + 1);
+      kb0 = split * q;
+      if (split + 1 < se) kb1 = (split + 1) * q;
     }
   }
   kb0 = __builtin_amdgcn_readfirstlane(kb0);
@@ -703,9 +706,11 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
       const int tok = row / G, h = row - tok * G;
       const int64_t srow = ((sr.lse0 + tok) * p.hq + kvh * G + h) * p.tile_splits + (kWide ? 0 : split);
       float* orow = p.ws_o + srow * kHeadDim;
+      if (lt > 0.f) {  // (an empty split's O is never read: its LSE says so)
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb)
-        *reinterpret_cast<f32x4*>(orow + 16 * nb + 4 * g4) = o[cg][nb] * linv;
+        for (int nb = 0; nb < 8; ++nb)
+          *reinterpret_cast<f32x4*>(orow + 16 * nb + 4 * g4) = o[cg][nb] * linv;
+      }
       if (g4 == 0) p.ws_lse[srow] = lt > 0.f ? rs[cg].mc + __log2f(lt) : kNegInf;
       if (kWide && g4 < p.tile_splits - 1) p.ws_lse[srow + 1 + g4] = kNegInf;  // (the other splits, <= 3: empty)
     } else if (row < rows_total) {
@@ -971,6 +976,17 @@ TilePlan tile_plan(const lkv_prefill_args* a) {
   const bool idle = t.waves == 4 ? est < 2 * cus : (t.waves == 8 && est * 2 <= cus);
   if (t.runs && idle && a->num_splits == 0 && a->older_k != nullptr && est > 0)
     t.splits = static_cast<int>(std::min<int64_t>(kMaxTileSplits, (cus * (t.waves == 4 ? 2 : 1) + est - 1) / est));
+  if (t.splits > 1 && a->older_len == nullptr && (a->local_k == nullptr || a->local_len == nullptr)) {
+    // host-constant lengths: as many equal splits as start inside the older segment for the last
+    // tile (the kernel applies the same rule per tile; a grid of splits that would all be empty
+    // would only cost their launch and the merge)
+    const int64_t nb0 = (std::min<int64_t>(std::max(a->older_len_const, 0), a->older_capacity_tokens) + kBlockTokens - 1) /
+                        kBlockTokens;
+    const int64_t lead = a->local_start ? kBlockTokens - 1 : (a->local_start_const & (kBlockTokens - 1));
+    const int64_t n1 = a->local_k == nullptr ? 0 : std::max(a->local_len_const, 0);
+    const int64_t nbt = nb0 + (n1 > 0 ? (lead + n1 + kBlockTokens - 1) / kBlockTokens : 0);
+    while (t.splits > 1 && (t.splits - 1) * ((nbt + t.splits - 1) / t.splits) > nb0 - 1) --t.splits;
+  }
   return t;
 }
 
