@@ -311,40 +311,83 @@ __device__ __attribute__((always_inline)) inline void unroll_steps(std::integer_
 // local], with the older segment as bf16(V * s) (the reference's rounded _scale()).  The
 // attention kernel's query tiles then stage V as plain copies instead of each converting it.
 // Each block also gets its flag: whether some value does not fit fp16 (magnitude 65536 or more).
-// One workgroup per kBlocks consecutive blocks of one (kv head, sequence); 256 threads x 16 values
-// per block.  Ragged calls take 8 blocks per workgroup: their grid covers every sequence, and the
-// workgroups of the sequences that are not on the tile path exit (a serving step of 31 decode rows
-// and one 1024-token row: 33 us for the pass with one block per workgroup).
+// Blocks [x kBlocks, (x + 1) kBlocks) of (kv head y, sequence b), 256 threads x 16 values per block.
+template <bool kPaged, int kBlocks>
+__device__ __attribute__((always_inline)) inline void v16_stage_blocks(const PrefillParams& p, int b, int kvh, int x);
+
+// Uniform calls (kBlocks 1): one workgroup per (block, kv head, sequence).  Ragged calls (kBlocks
+// 8): one per (8 blocks, kv head, z < Z) that converts those blocks of the tile-path sequences of
+// rank z, z + Z, ... (a
+// wave scan of cu_seqlens finds them): a grid over every sequence had mostly exiting workgroups
+// (a serving step of 31 decode rows and one 1024-token row: 33 us with one block per workgroup, 25
+// with 8 and every sequence in the grid).
 template <bool kPaged, int kBlocks>
 __global__ __launch_bounds__(256) void v16_stage_kernel(const PrefillParams p) {
-  const int kvh = blockIdx.y, b = blockIdx.z;
-  if ((blockIdx.x | kvh | b) == 0 && threadIdx.x == 0) *p.any_wide = 0.f;  // (the tile kernels run after this one)
-  if (!on_tile_path(p, seq_rows(p, b))) return;
+  const int kvh = blockIdx.y;
+  if ((blockIdx.x | blockIdx.y | blockIdx.z) == 0 && threadIdx.x == 0) *p.any_wide = 0.f;  // (the tile kernels run after this one)
+  if constexpr (kBlocks == 1) {  // (uniform calls)
+    if (on_tile_path(p, seq_rows(p, blockIdx.z))) v16_stage_blocks<kPaged, kBlocks>(p, blockIdx.z, kvh, blockIdx.x);
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  int rank = 0;
+  for (int i0 = 0; i0 < p.batch; i0 += 64) {
+    const int i = i0 + lane;
+    uint64_t m = __builtin_amdgcn_ballot_w64(i < p.batch && on_tile_path(p, seq_rows(p, i)));
+    while (m != 0) {  // (wave-uniform)
+      const int l = __builtin_ctzll(m);
+      m &= m - 1;
+      if (rank++ % static_cast<int>(gridDim.z) == static_cast<int>(blockIdx.z))
+        v16_stage_blocks<kPaged, kBlocks>(p, i0 + l, kvh, blockIdx.x);
+    }
+  }
+}
+
+template <bool kPaged, int kBlocks>
+__device__ __attribute__((always_inline)) inline void v16_stage_blocks(const PrefillParams& p, int b, int kvh, int x) {
   const SeqView sv = make_seq_view(p.seg, b, kvh);
   const int nb = sv.nb0 + local_blocks(sv, sv.n1);
   const float vs = p.vscale_mode ? p.vscale[kvh] : 1.f;
+  const int blk0 = x * kBlocks;
+  const int n = min(kBlocks, nb - blk0);  // (workgroup-uniform)
+  if (n <= 0) return;
+  // every block's loads first (one round trip for all of them), then the conversions and stores
+  uint4 raw[kBlocks][2];
+#pragma unroll
   for (int k = 0; k < kBlocks; ++k) {
-    const int blk = static_cast<int>(blockIdx.x) * kBlocks + k;
-    if (blk >= nb) return;  // (workgroup-uniform)
-    const bool older = blk < sv.nb0;
-    const uint16_t* src = (older ? sv.ov : sv.lv) + block_offset<kPaged>(sv, blk);
+    if (k >= n) break;
+    const int blk = blk0 + k;
+    const uint16_t* src = (blk < sv.nb0 ? sv.ov : sv.lv) + block_offset<kPaged>(sv, blk);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) raw[k][j] = *reinterpret_cast<const uint4*>(src + (threadIdx.x + j * 256) * 8);
+  }
+  uint32_t over = 0;  // bit k: block k holds a value fp16 cannot
+#pragma unroll
+  for (int k = 0; k < kBlocks; ++k) {
+    if (k >= n) break;
+    const int blk = blk0 + k;
     uint16_t* dst = p.v16 + ((static_cast<int64_t>(b) * p.hkv + kvh) * p.v16_blocks + blk) * kBlockElems;
-    const float s = older ? vs : 1.f;
-    bool over = false;
+    const float s = blk < sv.nb0 ? vs : 1.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int e = (threadIdx.x + j * 256) * 8;
       // bf16(v * s); bf16(v * 1) == v, so the unscaled blocks take the same instructions
-      const uint4 y = scale_frag(*reinterpret_cast<const uint4*>(src + e), s);
-      over = over || f16_overflow(y.x) || f16_overflow(y.y) || f16_overflow(y.z) || f16_overflow(y.w);
-      *reinterpret_cast<uint4*>(dst + e) = make_uint4(f16x2_bits(bf16_lo(y.x), bf16_hi(y.x)),
-                                                      f16x2_bits(bf16_lo(y.y), bf16_hi(y.y)),
-                                                      f16x2_bits(bf16_lo(y.z), bf16_hi(y.z)),
-                                                      f16x2_bits(bf16_lo(y.w), bf16_hi(y.w)));
+      const uint4 y = scale_frag(raw[k][j], s);
+      if (f16_overflow(y.x) || f16_overflow(y.y) || f16_overflow(y.z) || f16_overflow(y.w)) over |= 1u << k;
+      *reinterpret_cast<uint4*>(dst + (threadIdx.x + j * 256) * 8) =
+          make_uint4(f16x2_bits(bf16_lo(y.x), bf16_hi(y.x)), f16x2_bits(bf16_lo(y.y), bf16_hi(y.y)),
+                     f16x2_bits(bf16_lo(y.z), bf16_hi(y.z)), f16x2_bits(bf16_lo(y.w), bf16_hi(y.w)));
     }
-    const int any = __syncthreads_or(over);
-    if (threadIdx.x == 0) p.vflags[(static_cast<int64_t>(b) * p.hkv + kvh) * p.vflag_stride + blk] = any ? 1 : 0;
   }
+  // the blocks' flags: an OR over the workgroup of each thread's bits
+  __shared__ uint32_t sm_over;
+  if (threadIdx.x == 0) sm_over = 0;
+  __syncthreads();
+  if (over != 0) atomicOr(&sm_over, over);
+  __syncthreads();
+  if (threadIdx.x < n)
+    p.vflags[(static_cast<int64_t>(b) * p.hkv + kvh) * p.vflag_stride + blk0 + threadIdx.x] =
+        (sm_over >> threadIdx.x) & 1u;
+  __syncthreads();  // (sm_over is reused by the next sequence's call)
 }
 
 // Whether some block in [0, nbt) of (b, kvh) holds a V value fp16 cannot (the pre-pass's flags),
@@ -1178,7 +1221,8 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   const bool paged = a->older_block_table != nullptr || a->local_block_table != nullptr;
   if (vblocks > 0) {  // (no keys at all: every row's output is zero; the main kernel skips its loop)
     const int per_wg = ragged ? 8 : 1;
-    const dim3 vgrid(static_cast<unsigned>((vblocks + per_wg - 1) / per_wg), a->num_kv_heads, a->batch);
+    const dim3 vgrid(static_cast<unsigned>((vblocks + per_wg - 1) / per_wg), a->num_kv_heads,
+                     ragged ? std::min(a->batch, 4) : a->batch);
     if (paged && ragged)
       v16_stage_kernel<true, 8><<<vgrid, 256, 0, s>>>(p);
     else if (paged)
