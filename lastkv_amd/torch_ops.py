@@ -68,21 +68,26 @@ def prefill_attention(q: Tensor, older_k: Optional[Tensor], older_v: Optional[Te
                       local_k: Optional[Tensor], local_v: Optional[Tensor], local_len: Optional[Tensor],
                       local_len_const: int, local_start: Optional[Tensor], local_start_const: int,
                       local_table: Optional[Tensor], local_ring_blocks: int, causal: bool, sm_scale: float,
-                      out_scale: Optional[Tensor] = None) -> Tensor:
+                      out_scale: Optional[Tensor] = None, cu_seqlens_q: Optional[Tensor] = None,
+                      max_seqlen_q: int = 0, num_splits: int = 0) -> Tensor:
     """``lkv_prefill_attn``: q ``[B, L, Hq, 128]`` (the last L tokens of the local segment) ->
-    out ``[B, L, Hq, 128]``; bottom-right causal over the local segment when ``causal``."""
+    out ``[B, L, Hq, 128]``; bottom-right causal over the local segment when ``causal``.  With
+    ``cu_seqlens_q`` (int32 ``[B + 1]``) and ``max_seqlen_q`` q / out are ragged ``[T, Hq, 128]``
+    (FlashAttention's varlen form); ``num_splits`` 0 lets the library choose the key splits."""
 
     return ops.prefill_attention(
         q, older=_seg(older_k, older_v, older_table), older_len=_len(older_len, older_len_const), vscale=vscale,
         local=_seg(local_k, local_v, local_table), local_len=_len(local_len, local_len_const),
         local_start=_len(local_start, local_start_const), older_table=older_table, local_table=local_table,
-        local_ring_blocks=local_ring_blocks or None, causal=causal, sm_scale=sm_scale or None, out_scale=out_scale)
+        local_ring_blocks=local_ring_blocks or None, causal=causal, sm_scale=sm_scale or None, out_scale=out_scale,
+        cu_seqlens_q=cu_seqlens_q, max_seqlen_q=max_seqlen_q if cu_seqlens_q is not None else None,
+        num_splits=num_splits)
 
 
 @prefill_attention.register_fake
 def _(q, older_k, older_v, older_len, older_len_const, older_table, vscale, local_k, local_v, local_len,
       local_len_const, local_start, local_start_const, local_table, local_ring_blocks, causal, sm_scale,
-      out_scale=None):
+      out_scale=None, cu_seqlens_q=None, max_seqlen_q=0, num_splits=0):
     return q.new_empty(q.shape)
 
 
@@ -107,23 +112,27 @@ def qkv_epilogue(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, num_
                  q_norm_weight: Optional[Tensor], k_norm_weight: Optional[Tensor], eps: float,
                  positions: Optional[Tensor], positions_const: int, q_out: Tensor, ring_k: Tensor, ring_v: Tensor,
                  ring_table: Optional[Tensor], ring_tokens: int, deep_k: Optional[Tensor], deep_v: Optional[Tensor],
-                 deep_table: Optional[Tensor], rounding: int = 0, ring_v_mul: Optional[Tensor] = None) -> None:
+                 deep_table: Optional[Tensor], rounding: int = 0, ring_v_mul: Optional[Tensor] = None,
+                 cu_seqlens: Optional[Tensor] = None, max_seqlen: int = 0) -> None:
     """``lkv_qkv_epilogue``: RoPE + q/k RMSNorm, q written to ``q_out`` ``[B, L, Hq, 128]``, K/V
     appended to the ring (and to the shared cache ``deep_*`` when given) at ``positions + i``;
     ``rounding`` 0 = the HF torch op order, 1 = the vLLM fused_qkv order; ``ring_v_mul`` [Hkv]
-    scales the ring's V (the vLLM path's V / s rings)."""
+    scales the ring's V (the vLLM path's V / s rings).  With ``cu_seqlens`` (int32 ``[B + 1]``) and
+    ``max_seqlen`` the rows are ragged: q / k / v ``[T, heads * 128]``, q_out ``[T, Hq, 128]``."""
 
     ops.qkv_epilogue(q, k, v, cos, sin, num_q_heads=num_q_heads, num_kv_heads=num_kv_heads,
                      q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight, eps=eps,
                      positions=_len(positions, positions_const), ring=_seg(ring_k, ring_v, ring_table),
                      deep=_seg(deep_k, deep_v, deep_table), q_out=q_out, ring_table=ring_table,
                      ring_tokens=ring_tokens or None, deep_table=deep_table,
-                     rounding={v: k for k, v in ops.ROUNDINGS.items()}[rounding], ring_v_mul=ring_v_mul)
+                     rounding={v: k for k, v in ops.ROUNDINGS.items()}[rounding], ring_v_mul=ring_v_mul,
+                     cu_seqlens=cu_seqlens, max_seqlen=max_seqlen if cu_seqlens is not None else None)
 
 
 @qkv_epilogue.register_fake
 def _(q, k, v, cos, sin, num_q_heads, num_kv_heads, q_norm_weight, k_norm_weight, eps, positions, positions_const,
-      q_out, ring_k, ring_v, ring_table, ring_tokens, deep_k, deep_v, deep_table, rounding=0, ring_v_mul=None):
+      q_out, ring_k, ring_v, ring_table, ring_tokens, deep_k, deep_v, deep_table, rounding=0, ring_v_mul=None,
+      cu_seqlens=None, max_seqlen=0):
     return None
 
 

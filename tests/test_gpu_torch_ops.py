@@ -105,6 +105,43 @@ def test_epilogue_merge_norm_ops_equal_the_ctypes_calls():
     assert torch.equal(L.silu_mul(x, x), ops.silu_mul(x, x))
 
 
+def test_ragged_ops_equal_the_ctypes_calls():
+    """The varlen forms (cu_seqlens) of the prefill and epilogue operators: three sequences of 1, 40
+    and 7 query tokens in one call each, equal to the ctypes calls bit for bit, and opcheck-clean."""
+
+    g = torch.Generator(device=DEV).manual_seed(12)
+    B, Hq, Hkv, T0 = 3, 8, 2, 200
+    lengths = [1, 40, 7]
+    T = sum(lengths)
+    cu = torch.tensor([0, 1, 41, 48], dtype=torch.int32, device=DEV)
+    older = ops.TiledKV.zeros(B, Hkv, 224, DEV)
+    ops.pack_kv(_r(g, (B, Hkv, T0, 128)), _r(g, (B, Hkv, T0, 128)), older)
+    ring = ops.TiledKV.zeros(B, Hkv, 96, DEV)
+    ops.pack_kv(_r(g, (B, Hkv, 60, 128)), _r(g, (B, Hkv, 60, 128)), ring, token0=5)
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=DEV)
+    older_len, local_len, local_start = i32([T0, 150, 31]), i32([60, 60, 60]), i32([5, 5, 5])
+    q = _r(g, (T, Hq, 128))
+    want = ops.prefill_attention(q, older=older, older_len=older_len, local=ring, local_len=local_len,
+                                 local_start=local_start, causal=True, cu_seqlens_q=cu, max_seqlen_q=40)
+    args = (q, older.k, older.v, older_len, 0, None, None, ring.k, ring.v, local_len, 0, local_start, 0, None, 0, True,
+            0.0, None, cu, 40, 0)
+    assert torch.equal(L.prefill_attention(*args), want)
+    torch.library.opcheck(L.prefill_attention, args)
+    qq, kk, vv = _r(g, (T, Hq * 128)), _r(g, (T, Hkv * 128)), _r(g, (T, Hkv * 128))
+    cs = _r(g, (T, 128))
+    pos = i32([300, 41, 77])
+    rings = [ops.TiledKV.zeros(B, Hkv, 512, DEV) for _ in range(2)]
+    q_outs = [torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=DEV) for _ in range(2)]
+    ops.qkv_epilogue(qq, kk, vv, cs, cs, num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=None, k_norm_weight=None,
+                     eps=1e-6, positions=pos, ring=rings[0], q_out=q_outs[0], cu_seqlens=cu, max_seqlen=40)
+    eargs = (qq, kk, vv, cs, cs, Hq, Hkv, None, None, 1e-6, pos, 0, q_outs[1], rings[1].k, rings[1].v, None, 0, None,
+             None, None, 0, None, cu, 40)
+    L.qkv_epilogue(*eargs)
+    assert torch.equal(q_outs[0], q_outs[1])
+    assert torch.equal(rings[0].k, rings[1].k) and torch.equal(rings[0].v, rings[1].v)
+    torch.library.opcheck(L.qkv_epilogue, eargs)
+
+
 def test_opcheck():
     g = torch.Generator(device=DEV).manual_seed(13)
     B, Hq, Hkv, T0 = 2, 8, 2, 96
