@@ -11,7 +11,8 @@ Printed JSON line (one, from this single process):
   value          decode tok/s of the attention step (32 tokens / step time)
   roofline       HBM roofline of lkv_decode_attn: algorithmic bytes per layer-call
                  (K + V of 8192 tokens x 8 heads x 32 sequences + Q + O = 1,074,266,112 B) over
-                 the kernel's mean duration measured with HIP events on its stream
+                 the layer-call's mean duration: HIP events on its stream around the timed
+                 region, divided by the number of layer-calls in it
   cpu_baseline   the reference path restated with torch ops (torch.cat-free here: config 2 is
                  all shared history; F.scaled_dot_product_attention with enable_gqa) timed on
                  this host's CPU cores for a bounded sample
@@ -193,14 +194,14 @@ def decode_long_measurement(ops, torch, dev, layers: int = 32) -> dict:
               num_splits=splits, workspace=ws)
     for l in range(layers):
         ops.decode_attention(qs[l], out=outs[l], **kw)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(layers)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize()
+    ev[0].record()  # around the 32 calls, which run back to back (split kernel + combine each)
     for l in range(layers):
-        ev[l][0].record()
         ops.decode_attention(qs[l], out=outs[l], **kw)
-        ev[l][1].record()
+    ev[1].record()
     torch.cuda.synchronize()
-    us = statistics.mean(e[0].elapsed_time(e[1]) for e in ev) * 1e3
+    us = ev[0].elapsed_time(ev[1]) / layers * 1e3
     nbytes = 2 * Bl * HKV * (rec + local_len) * D * 2 + 2 * Bl * HQ * D * 2
     gbs = nbytes / (us * 1e-6) / 1e9
     del store, ring
@@ -981,13 +982,19 @@ def main() -> int:
     for _ in range(args.warmup):
         run_step(splits)
     torch.cuda.synchronize()
-    events = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(LAYERS)] for _ in range(args.steps)]
+    # Two events on the calls' stream bracket the whole timed region: the layer-calls run back to
+    # back as in a decode step, and the mean duration of one is the region's time over the number
+    # of calls (launch-to-launch gaps included).  An event pair around every call would add ~7 us
+    # per call of marker packets to both the step time and the kernel figure.
+    region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     t0 = time.perf_counter()
+    region[0].record()
     for step in range(args.steps):
-        run_step(splits, events[step])
+        run_step(splits)
+    region[1].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    kernel_ms = statistics.mean(e[0].elapsed_time(e[1]) for ev in events for e in ev)
+    kernel_ms = region[0].elapsed_time(region[1]) / (args.steps * LAYERS)
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     achieved = BYTES_PER_CALL / (kernel_ms * 1e-3) / 1e9
     peaks = peaks_measurement(ops, torch, dev)
