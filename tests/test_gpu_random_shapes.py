@@ -10,12 +10,10 @@ sweep covers 300 shapes in six tests of 50 (``pytest -x`` stops at the first fai
 seeds 5039, 5049, 5114, 5139 and 5227 are the shapes on which the 2-wave tile instance exceeded
 rel-L2 1e-3 (1.02-1.08e-3) before it split P, kept as named regression cases.  A second sweep
 draws wide calls (65-600 query rows per kv head, up to 3K keys) on the default tile path and
-reports its worst margin.  Decode runs through one and several key splits.  An opt-in long sweep
-(LKV_LONG_SWEEP=1) runs 2,000 more shapes and 100 wide calls through every tile choice."""
+reports its worst margin.  Decode runs through one and several key splits.  A long sweep runs 2,000
+more shapes (20 tests of 100) and 100 wide calls through every tile choice (4 tests of 25)."""
 
 from __future__ import annotations
-
-import os
 
 import numpy as np
 import pytest
@@ -149,19 +147,30 @@ def test_random_decode_shapes_match_oracle(seed):
 
 LONG_SWEEP_SEED0 = 20000
 LONG_SWEEP_SHAPES = 2000
+LONG_SWEEP_PART = 100
 LONG_WIDE_SEED0 = 3000
 LONG_WIDE_SHAPES = 100
+LONG_WIDE_PART = 25
 
 
-@pytest.mark.skipif(os.environ.get("LKV_LONG_SWEEP") != "1", reason="long sweep (~2 minutes): set LKV_LONG_SWEEP=1")
-def test_long_random_prefill_sweep():
-    """2,000 more shapes of the same generator (automatic choice and tile_waves 4 and 8) and 100 wide
-    calls through all three tile choices: every call within the bar; prints the worst rel-L2 per
-    kernel path (the figures quoted for the tiles' margin)."""
+@pytest.mark.parametrize("part", range(LONG_SWEEP_SHAPES // LONG_SWEEP_PART))
+def test_long_random_prefill_sweep(part):
+    """2,000 more shapes of the same generator (automatic choice and tile_waves 4 and 8) in parts of
+    100: every call within the bar; prints the worst rel-L2 per kernel path so far."""
 
-    for seed in range(LONG_SWEEP_SEED0, LONG_SWEEP_SEED0 + LONG_SWEEP_SHAPES):
+    seed0 = LONG_SWEEP_SEED0 + part * LONG_SWEEP_PART
+    for seed in range(seed0, seed0 + LONG_SWEEP_PART):
         _prefill_case(seed)
-    for seed in range(LONG_WIDE_SEED0, LONG_WIDE_SEED0 + LONG_WIDE_SHAPES):
+    print("worst rel_l2 so far by kernel: " + ", ".join(f"{k} {v:.3e}" for k, v in sorted(_worst.items())), flush=True)
+
+
+@pytest.mark.parametrize("part", range(LONG_WIDE_SHAPES // LONG_WIDE_PART))
+def test_long_random_wide_sweep(part):
+    """100 wide calls (65-600 query rows per kv head) through all three tile choices, in parts of 25;
+    the last part prints the worst rel-L2 per kernel path (the figures quoted for the tiles' margin)."""
+
+    seed0 = LONG_WIDE_SEED0 + part * LONG_WIDE_PART
+    for seed in range(seed0, seed0 + LONG_WIDE_PART):
         rng, B, Hkv, G, L, T0, ring_blocks, n1, start, causal = _wide_case(seed)
         seg, k, v = _two_segments(rng, B, Hkv, T0=max(T0, 1), n1=n1, start=start, ring_blocks=ring_blocks)
         q = _bf(rng, (B, L, G * Hkv, 128))
