@@ -251,7 +251,9 @@ typedef struct lkv_prefill_args {
    * the decode kernel (one score column per (token, head), each key read once); larger calls on the
    * MFMA tile kernel with 4 or 8 waves per workgroup chosen from the grid and the device's CU
    * count.  4 / 8: always the tile kernel, with that many waves (32 rows each) above 64 rows per
-   * kv head and 2 waves at or below. */
+   * kv head and 2 waves at or below.  In a ragged call (cu_seqlens_q) 4 / 8 set the waves of its
+   * sequences above 64 rows per kv head; its shorter sequences stay on the decode kernel unless
+   * every sequence is short, in which case all take the 2-wave tiles. */
   int32_t tile_waves;
   /* Optional output scale, fp32 [Hkv] (bf16-valued) or NULL, as in lkv_decode_args. */
   const float *out_scale;

@@ -1038,13 +1038,23 @@ int64_t tile_split_bytes(const lkv_prefill_args* a, const TilePlan& t, int split
   return splits > 1 ? t.rows_all * a->num_q_heads * splits * (lkv::kHeadDim + 1) * 4 : 0;
 }
 
+// Whether a ragged call runs its sequences of at most 64 query rows per kv head on the decode kernel:
+// with tile_waves 0, and with tile_waves 4 or 8 too when its longest sequence has more rows.  The 4-
+// and 8-wave tiles carry each probability as one fp16, whose rel-L2 over a short sequence's few
+// outputs can pass 1e-3; only a call of short sequences alone takes the 2-wave tiles (fp16 hi + lo).
+bool ragged_short_on_decode(const lkv_prefill_args* a) {
+  if (a->cu_seqlens_q == nullptr) return false;
+  const int64_t group = a->num_q_heads / a->num_kv_heads;
+  return a->tile_waves == 0 || std::min(a->max_seqlen_q, a->tokens) * group > 64;
+}
+
 // The workspace a call cannot run without: the V pre-pass's region, or the decode kernel's split
 // states if larger (they are used before the pre-pass runs, in the same bytes).
 int64_t min_workspace_bytes(const lkv_prefill_args* a) {
   using namespace lkv;
   const int64_t v16 = v16_region_bytes(a, v16_blocks(a));
   const int64_t per_row = (kHeadDim + 2) * 4;  // one split state
-  if (a->cu_seqlens_q != nullptr && a->tile_waves == 0 && a->max_seqlen_q >= 1 && a->tokens > 0) {
+  if (ragged_short_on_decode(a) && a->max_seqlen_q >= 1 && a->tokens > 0) {
     // a ragged call's decode-kernel classes: split states of their sequences, by rank in the class
     const int group = a->num_q_heads / a->num_kv_heads;
     const int L = std::min(a->max_seqlen_q, a->tokens);
@@ -1164,11 +1174,12 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   hipStream_t s = as_stream(stream);
   // Sequences of at most 64 query rows per kv head (e.g. decode tokens, or up to 16 tokens of a GQA
   // group of 4) read every key once on the decode kernel (one score column per (token, head))
-  // instead of converting V to fp16 and running 2-wave tiles; tile_waves 4 or 8 keep them on the
-  // tile kernel.  A ragged call runs its sequences of 1-16, 17-32 and 33-64 columns on the decode
-  // instance of that width (one launch per class present) and the longer ones on the tile kernel.
+  // instead of converting V to fp16 and running 2-wave tiles; tile_waves 4 or 8 keep a uniform call
+  // on the tile kernel.  A ragged call runs its sequences of 1-16, 17-32 and 33-64 columns on the
+  // decode instance of that width (one launch per class present) and the longer ones on the tile
+  // kernel, also with tile_waves 4 or 8 unless all of its sequences are short.
   const int64_t max_cols = seq_tokens * group;
-  const bool short_on_decode = a->tile_waves == 0;
+  const bool short_on_decode = a->tile_waves == 0 || ragged_short_on_decode(a);
   if (short_on_decode) {
     const int32_t bounds[4] = {0, 16, 32, 64};
     for (int c = 0; c < 3; ++c) {

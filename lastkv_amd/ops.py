@@ -441,7 +441,10 @@ def prefill_attention(
     ``workspace`` (uint8, 16-byte aligned, at least ``prefill_workspace_bytes`` of the same
     arguments) receives the fp16 V of every key block; without it one is allocated per call.
     ``tile_waves`` (0, 4 or 8) fixes the workgroup size of the tile kernel; 0 lets the library
-    choose from the grid size and the device's CU count.  ``out_scale`` as in ``decode_attention``."""
+    choose from the grid size and the device's CU count.  4 or 8 put a uniform call on the tile
+    kernel at any size; in a ragged call they apply to its sequences above 64 query rows per kv
+    head, and its shorter ones stay on the decode kernel unless all of its sequences are short.
+    ``out_scale`` as in ``decode_attention``."""
 
     _require_bf16_cuda("q", q)
     ragged = cu_seqlens_q is not None

@@ -139,8 +139,10 @@ def test_ragged_prefill_equals_per_sequence_calls_and_oracle(paged, causal):
 
 
 def test_ragged_prefill_forced_tiles_and_short_only_calls():
-    """tile_waves 4 / 8 run every sequence on the tiles; a ragged call whose sequences all have at
-    most 64 rows per kv head runs on the decode kernel alone."""
+    """tile_waves 4 / 8: a ragged call whose sequences all have at most 64 rows per kv head runs on
+    the 2-wave tiles (fp16 hi + lo probabilities), one with a longer sequence runs that one on tiles
+    of that many waves and its short sequences on the decode kernel; with tile_waves 0 a call of
+    short sequences runs on the decode kernel alone."""
 
     rng = np.random.default_rng(77)
     Hkv, G = 2, 4
@@ -189,6 +191,67 @@ def test_ragged_prefill_more_than_64_sequences(paged):
         worst = max(worst, A.rel_l2(got, want))
         assert A.max_abs(got, want) <= MAX_ABS and A.rel_l2(got, want) <= REL_L2, f"paged={paged} sequence {b} (L={L})"
     print(f"paged={paged}: 150 sequences, {sum(lengths)} rows, worst rel_l2 {worst:.2e} (automatic splits)", flush=True)
+
+
+RAGGED_SWEEP_SEED0 = 7000
+RAGGED_SWEEP_CASES = 60
+RAGGED_SWEEP_PART = 10
+
+
+def _ragged_sweep_case(seed):
+    rng = np.random.default_rng(seed)
+    B = int(rng.integers(1, 25))
+    Hkv = int(rng.choice([1, 2, 4]))
+    G = int(rng.choice([1, 2, 4, 8]))
+    pool_of_lengths = [0, 1, 1, 1, 1, 2, 3, 5, 8, 9, 16, 17, 31, 33, 64, 65, 100, 129, 250]
+    lengths = [int(x) for x in rng.choice(pool_of_lengths, size=B)]
+    if sum(lengths) == 0:
+        lengths[0] = 1
+    paged = bool(rng.integers(0, 2))
+    causal = bool(rng.integers(0, 2))
+    splits = int(rng.choice([0, 0, 1, 3]))
+    waves = int(rng.choice([0, 0, 0, 4, 8]))
+    return rng, lengths, Hkv, G, paged, causal, splits, waves
+
+
+@pytest.mark.parametrize("part", range(RAGGED_SWEEP_CASES // RAGGED_SWEEP_PART))
+def test_random_ragged_sweep(part):
+    """Seeded random ragged calls: 1-24 sequences of 0-250 query tokens (decode rows, every column
+    class of the decode kernel and tile-path rows mixed), GQA groups 1-8 over 1-4 kv heads, tiled or
+    paged caches, causal or bidirectional, automatic / 1 / 3 key splits and automatic or forced tile
+    waves, each sequence against the fp64 oracle at the north-star bar; with one split and the
+    automatic tiles every sequence also equals its own uniform call bit for bit."""
+
+    worst = 0.0
+    for seed in range(RAGGED_SWEEP_SEED0 + part * RAGGED_SWEEP_PART, RAGGED_SWEEP_SEED0 + (part + 1) * RAGGED_SWEEP_PART):
+        rng, lengths, Hkv, G, paged, causal, splits, waves = _ragged_sweep_case(seed)
+        Hq = Hkv * G
+        seg, ks, vs, meta = _ragged_case(rng, lengths, Hkv, G, paged, causal)
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        T = int(cu[-1])
+        q = _bf(rng, (T, Hq, 128))
+        lse = torch.empty((T, Hq), dtype=torch.float32, device=DEV)
+        label = (f"seed {seed}: lengths={lengths} Hkv={Hkv} G={G} paged={paged} causal={causal} "
+                 f"splits={splits} tile_waves={waves}")
+        out = ops.prefill_attention(_t(q), causal=causal, cu_seqlens_q=torch.from_numpy(cu).to(DEV),
+                                    max_seqlen_q=max(lengths), lse=lse, num_splits=splits, tile_waves=waves, **seg)
+        for b, L in enumerate(lengths):
+            if L == 0:
+                continue
+            rows = slice(int(cu[b]), int(cu[b + 1]))
+            want, want_lse = A.attention(q[rows].transpose(1, 0, 2)[None], ks[b], vs[b], causal_bottom_right=causal)
+            want = bf16.round_bf16(want[0].transpose(1, 0, 2).astype(np.float32))
+            got = out[rows].float().cpu().numpy()
+            ma, rl = A.max_abs(got, want), A.rel_l2(got, want)
+            worst = max(worst, rl)
+            assert ma <= MAX_ABS and rl <= REL_L2, f"{label}: sequence {b} (L={L}) max_abs={ma} rel_l2={rl}"
+            np.testing.assert_allclose(lse[rows].cpu().numpy(), want_lse[0].T, rtol=1e-4, atol=1e-4,
+                                       err_msg=f"{label}: lse of sequence {b}")
+            if splits == 1 and waves == 0:
+                alone = ops.prefill_attention(_t(q[rows][None]), causal=causal, num_splits=1, **_one(seg, b, meta))
+                assert torch.equal(out[rows], alone[0]), f"{label}: sequence {b} (L={L}) differs from its own call"
+        print(f"{label}: ok", flush=True)
+    print(f"part {part}: worst rel_l2 {worst:.2e}", flush=True)
 
 
 def _rotary(positions):
