@@ -17,10 +17,23 @@ namespace {
 // Value of the bf16 nearest to x (round to nearest even), as fp32.
 __device__ inline float rb(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
 
-__device__ inline float wave_sum64(float x) {
+// The torch-order RMSNorm's fp32 sum of squares of one row, in the order both epilogue forms share
+// (the reference's own reduction order is torch's and not fixed): for each of the 8 groups of dims
+// [8g, 8g + 8) with their partners 64 + 8g.., a fused multiply-add chain over the group's dims in
+// order (dim 8g + j, then 64 + 8g + j), then the groups' sums added pairwise (g xor 1, 2, 4).  Here
+// lane l holds dims l and l + 64 (the wave's row), so group g is lanes 8g .. 8g + 7.
+__device__ inline float row_sumsq_lanes(float r0, float r1, int lane) {
+  const int base = lane & ~7;
+  float ss = 0.f;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-  return x;
+  for (int e = 0; e < 8; ++e) {
+    const float a = __shfl(r0, base + e), b = __shfl(r1, base + e);
+    ss = __builtin_fmaf(a, a, ss);
+    ss = __builtin_fmaf(b, b, ss);
+  }
+#pragma unroll
+  for (int off = 8; off <= 32; off <<= 1) ss += __shfl_xor(ss, off);
+  return ss;
 }
 
 struct QkvParams {
@@ -149,7 +162,7 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const QkvParams p) {
     r0 = rb(rb(x0 * c0) + rb(-x1 * s0));
     r1 = rb(rb(x1 * c1) + rb(x0 * s1));
     if (w != nullptr) {
-      const float ss = wave_sum64(r0 * r0 + r1 * r1);
+      const float ss = row_sumsq_lanes(r0, r1, lane);
       const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHeadDim) + p.eps);
       r0 = rb(bf16_bits_to_f32(w[lane]) * rb(r0 * inv));
       r1 = rb(bf16_bits_to_f32(w[lane + 64]) * rb(r1 * inv));
@@ -285,9 +298,13 @@ __device__ inline void rope_norm_row(uint4& a, uint4& b, const RopeCS& cs, const
     rb2(r0[j], r1[j]);
   }
   if (w.on) {
+    // the sum of squares in the order row_sumsq_lanes takes (this lane is group l of the row)
     float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss += r0[j] * r0[j] + r1[j] * r1[j];
+    for (int j = 0; j < 8; ++j) {
+      ss = __builtin_fmaf(r0[j], r0[j], ss);
+      ss = __builtin_fmaf(r1[j], r1[j], ss);
+    }
     ss += __shfl_xor(ss, 1);
     ss += __shfl_xor(ss, 2);
     ss += __shfl_xor(ss, 4);

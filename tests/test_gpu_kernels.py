@@ -286,6 +286,37 @@ def test_qkv_epilogue_matches_reference_ops(B, L, p0, last, C):
         assert np.array_equal(dk.float().cpu().numpy(), got_k) and np.array_equal(dv.float().cpu().numpy(), got_v)
 
 
+@pytest.mark.parametrize("rounding", ["torch", "vllm"])
+def test_epilogue_forms_agree_bit_for_bit(rounding):
+    """The per-token kernel (calls of fewer than 16 tokens) and the block form (16 or more) sum the
+    RMSNorm squares in the same fixed order, so the same rows give the same bits either way: 72
+    tokens of 2 sequences as one call against nine calls of 8 tokens (normalised queries, ring and
+    shared-store bytes), with norm gains and a ring V multiplier on the vLLM contract."""
+
+    rng = np.random.default_rng(61 + (rounding == "vllm"))
+    B, L, Hq, Hkv, p0 = 2, 72, 16, 4, 37
+    q, k, v = _bf(rng, (B, L, Hq * 128)), _bf(rng, (B, L, Hkv * 128)), _bf(rng, (B, L, Hkv * 128))
+    cfg = M.config_8b(num_hidden_layers=2)
+    inv, sc = M.rope_inv_freq(cfg)
+    cos, sin = M.rotary_cos_sin(inv, sc, torch.arange(p0, p0 + L)[None].expand(B, L), torch.bfloat16)
+    cos, sin = cos.to(DEV), sin.to(DEV)
+    qw = torch.from_numpy(bf16.round_bf16(rng.uniform(0.5, 1.6, 128).astype(np.float32))).bfloat16().to(DEV)
+    kw = torch.from_numpy(bf16.round_bf16(rng.uniform(0.5, 1.6, 128).astype(np.float32))).bfloat16().to(DEV)
+    vmul = torch.from_numpy(rng.uniform(0.5, 2.0, Hkv).astype(np.float32)).to(DEV) if rounding == "vllm" else None
+    kwargs = dict(num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=qw, k_norm_weight=kw, eps=1e-5, rounding=rounding,
+                  ring_v_mul=vmul)
+    stores = [(ops.TiledKV.zeros(B, Hkv, 256, DEV), ops.TiledKV.zeros(B, Hkv, 128, DEV)) for _ in range(2)]
+    whole = ops.qkv_epilogue(_t(q), _t(k), _t(v), cos, sin, positions=p0, ring=stores[0][0], deep=stores[0][1], **kwargs)
+    parts = []
+    for i in range(0, L, 8):
+        sl = slice(i, i + 8)
+        parts.append(ops.qkv_epilogue(_t(q)[:, sl], _t(k)[:, sl], _t(v)[:, sl], cos[:, sl], sin[:, sl], positions=p0 + i,
+                                      ring=stores[1][0], deep=stores[1][1], **kwargs))
+    assert torch.equal(whole, torch.cat(parts, 1)), "normalised queries differ between the two forms"
+    for a, b in zip(stores[0], stores[1]):
+        assert torch.equal(a.k, b.k) and torch.equal(a.v, b.v), "cache bytes differ between the two forms"
+
+
 # ------------------------------------------------------------------ blend
 @pytest.mark.parametrize("chunk,cidx", [(64, 1), (64, 4), (1024, 2), (4, 3), (12, 5)])
 def test_blend_chunk_bit_exact(chunk, cidx):

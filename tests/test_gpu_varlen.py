@@ -295,6 +295,71 @@ def test_ragged_epilogue_equals_per_sequence_calls(rounding, lengths):
     assert torch.equal(deep_a.k, deep_b.k) and torch.equal(deep_a.v, deep_b.v), "shared-store contents differ"
 
 
+@pytest.mark.parametrize("part", range(4))
+def test_random_ragged_epilogue_sweep(part):
+    """Seeded random ragged epilogue calls (10 per part): 1-30 sequences of 0-129 tokens at positions
+    0-400, GQA 1-4 over 1-8 kv heads, tiled or paged rings and shared stores, both rounding contracts
+    (the vLLM one with a ring V multiplier), with and without the shared store; the normalised
+    queries and every ring and shared-store byte equal the per-sequence calls'."""
+
+    for case in range(10):
+        seed = 8000 + 10 * part + case
+        rng = np.random.default_rng(seed)
+        g = torch.Generator(device=DEV).manual_seed(seed)
+        B = int(rng.integers(1, 31))
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        Hq = Hkv * int(rng.choice([1, 2, 4]))
+        lengths = [int(x) for x in rng.choice([0, 1, 1, 1, 2, 3, 7, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 129], size=B)]
+        if sum(lengths) == 0:
+            lengths[-1] = 1
+        rounding = str(rng.choice(["torch", "vllm"]))
+        paged, with_deep = bool(rng.integers(0, 2)), bool(rng.integers(0, 3))
+        R, cap = 256, 576
+        pos_h = [int(x) for x in rng.integers(0, 401, B)]
+        cu = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int32, device=DEV)
+        T = int(cu[-1])
+        pos = torch.tensor(pos_h, dtype=torch.int32, device=DEV)
+        fused = torch.randn((T, (Hq + 2 * Hkv) * 128), generator=g, device=DEV).bfloat16()
+        q, k, v = fused.split([Hq * 128, Hkv * 128, Hkv * 128], dim=-1)
+        flat = torch.cat([torch.arange(pos_h[b], pos_h[b] + L, device=DEV) for b, L in enumerate(lengths)])
+        cos, sin = _rotary(flat[None])
+        qw = (torch.rand(128, generator=g, device=DEV) + 0.5).bfloat16()
+        kw = (torch.rand(128, generator=g, device=DEV) + 0.5).bfloat16()
+        vmul = (torch.rand(Hkv, generator=g, device=DEV) + 0.5) if rounding == "vllm" else None
+        kwargs = dict(num_q_heads=Hq, num_kv_heads=Hkv, q_norm_weight=qw, k_norm_weight=kw, eps=1e-5,
+                      rounding=rounding, ring_v_mul=vmul)
+        label = f"seed {seed}: lengths={lengths} Hq={Hq} Hkv={Hkv} {rounding} paged={paged} deep={with_deep}"
+        if paged:
+            rb, db = R // 32, cap // 32
+            perm = torch.from_numpy(rng.permutation(B * (rb + db))).to(DEV, torch.int32)
+            rtab, dtab = perm[:B * rb].view(B, rb).contiguous(), perm[B * rb:].view(B, db).contiguous()
+            stores = [ops.PagedKV.zeros(B * (rb + db), Hkv, DEV) for _ in range(2)]
+
+            def where(st, sl):
+                return dict(ring=st, ring_table=rtab[sl], ring_tokens=R, deep=st if with_deep else None,
+                            deep_table=dtab[sl] if with_deep else None)
+        else:
+            stores = [(ops.TiledKV.zeros(B, Hkv, R, DEV), ops.TiledKV.zeros(B, Hkv, cap, DEV)) for _ in range(2)]
+
+            def where(st, sl):
+                one = lambda c: ops.TiledKV(c.k[sl], c.v[sl])
+                return dict(ring=one(st[0]), deep=one(st[1]) if with_deep else None)
+        qa = ops.qkv_epilogue(q, k, v, cos, sin, positions=pos, cu_seqlens=cu, max_seqlen=max(lengths),
+                              **where(stores[0], slice(0, B)), **kwargs)
+        for b, L in enumerate(lengths):
+            if L == 0:
+                continue
+            rows = slice(int(cu[b]), int(cu[b + 1]))
+            qb = ops.qkv_epilogue(q[rows][None], k[rows][None], v[rows][None], cos[:, rows], sin[:, rows],
+                                  positions=pos_h[b], **where(stores[1], slice(b, b + 1)), **kwargs)
+            assert torch.equal(qa[rows], qb[0]), f"{label}: normalised queries of sequence {b} differ"
+        a_t = [stores[0]] if paged else list(stores[0])
+        b_t = [stores[1]] if paged else list(stores[1])
+        for x, y in zip(a_t, b_t):
+            assert torch.equal(x.k, y.k) and torch.equal(x.v, y.v), f"{label}: cache contents differ"
+        print(f"{label}: ok", flush=True)
+
+
 def test_serving_mixed_step_31_decode_1024_and_7_rows_match_oracle():
     """A step of 31 decode rows, one 1024-token prefill row (positions 2048-3071: 1024 older keys
     and a causal local segment of 2048) and one 7-token row, one epilogue and one attention launch
