@@ -113,6 +113,80 @@ def test_run_layer_bit_exact_vs_contiguous_twin():
     assert pool.free_pages == 64
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_run_layer_random_schedules_bit_exact_vs_twins(seed):
+    """Seeded random serving schedules against contiguous twins, bit for bit at every layer of every
+    step (one decode split on both sides): GQA 1-8 over 1-4 kv heads, a chunk size of 8-100 tokens,
+    up to 4 live sequences with random targets, arriving at random steps and freed when done (so
+    slots and pages are reused), each step scheduling a random subset of them with prompt pieces up
+    to the next chunk boundary or single tokens, and padded decode steps; at the end every page is
+    back in the pool."""
+
+    rng = np.random.default_rng(300 + seed)
+    g = torch.Generator(device=DEV).manual_seed(300 + seed)
+    layers, cap, live_max = 2, 480, 4
+    Hkv = int(rng.choice([1, 2, 4]))
+    Hq = Hkv * int(rng.choice([1, 2, 4, 8]))
+    C = int(rng.choice([8, 24, 32, 40, 64, 100]))
+    params = []
+    for _ in range(layers):
+        w = (torch.rand(128, generator=g, device=DEV) + 0.5).bfloat16()
+        vs = (torch.rand(Hkv, generator=g, device=DEV) + 0.4).bfloat16().float()
+        params.append((w, w.flip(0).contiguous(), 1e-5, vs))
+    alpha = torch.rand(layers * Hkv, generator=g, device=DEV).bfloat16().float()
+    blend = (alpha, (1 - alpha).bfloat16().float(), torch.cat([p[3] for p in params]))
+    pool = LastKVPagePool(num_layers=layers, kv_heads=Hkv, chunk_size=C, max_slots=live_max,
+                          source_pages=live_max * cap // 32 + 4, max_tokens_per_slot=cap, device=DEV)
+    free0 = pool.free_pages
+    fast = LastKVFastPath(pool, num_q_heads=Hq, layer_params=params, blend=blend, rotary=_rotary,
+                          max_batch=live_max + 2, num_splits=1)
+    live = {}  # slot -> (twin, target length, prompt length)
+    started = steps = 0
+    while steps < 200 and (live or started < 16):
+        while len(live) < live_max and started < 16 and (not live or rng.random() < 0.4):
+            target = int(rng.integers(2, 240 if rng.random() < 0.7 else cap))
+            live[fast.add_sequence()] = (_Twin(layers, Hkv, C, cap, params, blend), target,
+                                         int(rng.integers(1, target)))
+            started += 1
+        rows = []
+        for slot, (_, target, prompt) in live.items():
+            if len(live) > 1 and rng.random() < 0.2:
+                continue  # not in this step
+            p = fast.seen(slot)
+            room = min(target - p, C - p % C)
+            rows.append((slot, int(rng.integers(1, room + 1)) if p < prompt else 1))
+        if not rows:
+            continue
+        decode = all(n == 1 for _, n in rows)
+        pad = len(rows) + int(rng.integers(1, 3)) if decode and rng.random() < 0.3 else None
+        fast.prepare(rows, pad_to=pad)
+        T = fast.tokens
+        q = torch.randn((T, Hq * 128), generator=g, device=DEV).bfloat16()
+        k = torch.randn((T, Hkv * 128), generator=g, device=DEV).bfloat16()
+        v = torch.randn((T, Hkv * 128), generator=g, device=DEV).bfloat16()
+        label = f"seed {seed} (Hq {Hq}, Hkv {Hkv}, C {C}) step {steps} rows {[(n, fast.seen(sl) - n) for sl, n in rows]}"
+        for l in range(layers):
+            out = torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=DEV)
+            fast.run_layer(l, q, k, v, out)
+            start = 0
+            for slot, n in rows:
+                sl = slice(start, start + n)
+                want = live[slot][0].layer(l, q[sl], k[sl], v[sl], Hq, Hkv)
+                assert torch.equal(out[sl], want), f"{label}: layer {l} slot {slot}"
+                start += n
+        for slot, n in rows:
+            live[slot][0].advance(n)
+            assert fast.seen(slot) == live[slot][0].cache.seen_tokens
+        for slot in [sl for sl, (_, target, _) in live.items() if fast.seen(sl) >= target]:
+            fast.free_sequence(slot)
+            del live[slot]
+        steps += 1
+    for slot in list(live):
+        fast.free_sequence(slot)
+    assert pool.free_pages == free0
+    print(f"seed {seed}: Hq {Hq} Hkv {Hkv} C {C}, {steps} steps, {started} sequences", flush=True)
+
+
 def test_serving_model_ragged_batches_match_oracle():
     oracle, ours = _tiny(chunk=8)
     lengths = [37, 22, 50]
