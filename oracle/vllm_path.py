@@ -159,7 +159,8 @@ class MergedSequence:
 
     def layer(self, l: int, q, k, v, num_q_heads: int) -> np.ndarray:
         """This step's rows q [n, Hq, 128], k / v [n, Hkv, 128] (bf16-valued) through layer l; returns
-        the bf16-valued output [n, Hq, 128] before the o projection.  Attention in float64."""
+        the bf16-valued output [n, Hq, 128] before the o projection (``last_attention`` keeps the
+        attention's bf16 output before the head scale).  Attention in float64."""
 
         qn_w, kn_w, eps, s = self.params[l]
         n = q.shape[0]
@@ -182,6 +183,7 @@ class MergedSequence:
         V = np.stack(vals, axis=1)[None]
         out, _ = attention(np.transpose(qn, (1, 0, 2))[None], K, V, causal_bottom_right=True)
         o16 = bf16.round_bf16(np.transpose(out[0], (1, 0, 2)).astype(np.float32))
+        self.last_attention = o16  # the attention output before the head scale
         group = num_q_heads // Hkv
         return head_scale(o16, np.repeat(np.asarray(s, np.float32), group))
 

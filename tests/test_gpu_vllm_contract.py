@@ -5,9 +5,11 @@
    bf16(v * fp32(1 / s)), raw shared K / V; per-token and block forms, norms on and off.
 2. ``out_scale`` of the decode and prefill kernels: bf16(bf16(o) * s) of the unscaled call, bit for bit
    (decode with one and several splits, the tile kernel and short calls on the decode kernel).
-3. ``LastKVFastPath(contract="vllm")`` over ragged steps that cross chunk boundaries against the
-   oracle's merged path (``MergedSequence``): ring and shared pages bit-exact (V / s rings, raw
-   shared V, blends in the V / s domain), outputs within max-abs 2e-2 and rel-L2 1e-3.
+3. ``LastKVFastPath(contract="vllm")`` over ragged steps that cross chunk boundaries (a fixed
+   schedule and seeded random ones) against the oracle's merged path (``MergedSequence``): ring and
+   shared pages bit-exact (V / s rings, raw shared V, blends in the V / s domain); each attention
+   output within rel-L2 1e-3 and, per element, max(2e-2, one bf16 ulp) of the oracle's attention,
+   and the step's output its head scale bf16(bf16(o) * s) bit for bit.
 4. The serving model on the vLLM contract: HIP-graph decode replays equal eager steps and stay
    close to the HF-contract path's logits; ragged prefill + decode logits no further from the fp32
    reference model than the reference's own bf16 path (the two contracts are the same model in
@@ -151,7 +153,54 @@ def _page_tokens(pool: LastKVPagePool, pages: torch.Tensor, first: int, count: i
     return out
 
 
-def test_fast_path_vllm_contract_matches_merged_oracle():
+def _capture_unscaled(monkeypatch):
+    """Wraps the attention entry points the fast path calls: a call with an output scale (the vLLM
+    contract's head scale, bf16(bf16(o) * s), fused_qkv.py:130-156) runs a second time without it.
+    The test then holds the attention output itself to the north-star bar and the scaled output to
+    the exact rescale of it: the head scale's second rounding belongs to the reference's contract
+    and moves the rel-L2 of outputs measured after it (small tile calls: 8.4e-4 mean before it,
+    9.0e-4 after, over 1e-3 for 29 of 600 such calls)."""
+
+    captured = []
+    for name in ("prefill_attention", "decode_attention"):
+        real = getattr(ops, name)
+
+        def wrapper(q, *args, _real=real, out=None, out_scale=None, **kw):
+            res = _real(q, *args, out=out, out_scale=out_scale, **kw)
+            if out_scale is not None:
+                captured.append((res, _real(q, *args, out_scale=None, **kw), out_scale))
+            return res
+
+        monkeypatch.setattr(ops, name, wrapper)
+    return captured
+
+
+def _check_attention(captured, T, Hq, rows, outs, wants, label):
+    """``rows`` = (slice, oracle's pre-scale attention [n, Hq, 128]) of one layer call: the attention
+    output within rel-L2 1e-3 and, per element, max(2e-2, one bf16 ulp of the exact value); the
+    call's output equal to bf16(attention * s) bit for bit.  Returns the worst rel-L2."""
+
+    assert len(captured) == 1, f"{label}: expected one attention call, got {len(captured)}"
+    scaled, plain, s = captured.pop()
+    plain = plain.reshape(-1, Hq, 128)[:T]
+    group = Hq // s.numel()
+    assert torch.equal(outs, (plain.float() * s.repeat_interleave(group)[None, :, None]).bfloat16()), \
+        f"{label}: the output is not bf16(attention * s)"
+    got = _np(plain)
+    worst = 0.0
+    for sl, want in zip(rows, wants):
+        a, w = got[sl], want
+        e = np.floor(np.log2(np.maximum(np.abs(w), 1e-30)))
+        allow = np.maximum(2.0 ** (e - 7), MAX_ABS)
+        rl = A.rel_l2(a, w)
+        worst = max(worst, rl)
+        assert np.all(np.abs(a - w) <= allow) and rl <= REL_L2, \
+            f"{label} rows {sl}: max |err| / allowance {np.max(np.abs(a - w) / allow):.3f} rel_l2 {rl:.3e}"
+    return worst
+
+
+def test_fast_path_vllm_contract_matches_merged_oracle(monkeypatch):
+    captured = _capture_unscaled(monkeypatch)
     rng = np.random.default_rng(9)
     layers, Hq, Hkv, C, cap = 3, 8, 2, 48, 400
     params, oparams = [], []
@@ -184,15 +233,14 @@ def test_fast_path_vllm_contract_matches_merged_oracle():
         for l in range(layers):
             out = torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=DEV)
             fast.run_layer(l, _t(q.reshape(T, -1)), _t(k.reshape(T, -1)), _t(v.reshape(T, -1)), out)
-            got = _np(out)
-            start = 0
+            start, sls, wants = 0, [], []
             for i, n in rows:
                 sl = slice(start, start + n)
-                want = seqs[i].layer(l, q[sl], k[sl], v[sl], Hq)
-                ma, rl = A.max_abs(got[sl], want), A.rel_l2(got[sl], want)
-                worst = max(worst, rl)
-                assert ma <= MAX_ABS and rl <= REL_L2, f"step {step} layer {l} seq {i}: max_abs={ma} rel_l2={rl}"
+                seqs[i].layer(l, q[sl], k[sl], v[sl], Hq)
+                sls.append(sl)
+                wants.append(seqs[i].last_attention)
                 start += n
+            worst = max(worst, _check_attention(captured, T, Hq, sls, out, wants, f"step {step} layer {l}"))
         for i, n in rows:
             seqs[i].end_step(n)
     torch.cuda.synchronize()
@@ -209,6 +257,98 @@ def test_fast_path_vllm_contract_matches_merged_oracle():
             got = _page_tokens(pool, pool.src_table[slot], 0, seen, kind, ring=False)
             assert np.array_equal(got, np.stack([slab[t] for t in range(seen)], 1)), f"seq {i} shared {'KV'[kind]}"
     print(f"{len(schedule)} steps, worst rel_l2 {worst:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_fast_path_vllm_contract_random_schedules(seed, monkeypatch):
+    """Seeded random schedules on the vLLM contract against the oracle's merged path: GQA 1-8 over
+    1-4 kv heads, chunk sizes 8-64, automatic / 1 / 2 decode splits, up to 3 live sequences arriving
+    and freed at random steps (slots and pages reused), prompt pieces up to the next chunk boundary,
+    then single tokens.  At every layer of every step the attention output is within the bar and the
+    output equals its head scale bit for bit; each sequence's ring windows and shared pages are
+    bit-exact when it is freed."""
+
+    captured = _capture_unscaled(monkeypatch)
+    rng = np.random.default_rng(500 + seed)
+    layers, cap, live_max = 2, 320, 3
+    Hkv = int(rng.choice([1, 2, 4]))
+    Hq = Hkv * int(rng.choice([1, 2, 4, 8]))
+    C = int(rng.choice([8, 24, 48, 64]))
+    params, oparams = [], []
+    for _ in range(layers):
+        w = bf16.round_bf16((rng.random(128) + 0.5).astype(np.float32))
+        s = bf16.round_bf16(rng.uniform(0.4, 1.4, Hkv).astype(np.float32))
+        params.append((_t(w), _t(w[::-1]), 1e-5, torch.from_numpy(s).to(DEV)))
+        oparams.append((w, w[::-1].copy(), 1e-5, s))
+    alpha = bf16.round_bf16(rng.random((layers, Hkv)).astype(np.float32))
+    om = bf16.rsub(alpha, 1.0)
+    blend = (torch.from_numpy(alpha.reshape(-1)).to(DEV), torch.from_numpy(om.reshape(-1)).to(DEV),
+             torch.cat([p[3] for p in params]))
+    pool = LastKVPagePool(num_layers=layers, kv_heads=Hkv, chunk_size=C, max_slots=live_max,
+                          source_pages=live_max * cap // 32 + 4, max_tokens_per_slot=cap, device=DEV)
+    free0 = pool.free_pages
+    splits = int(rng.choice([0, 1, 2]))
+    fast = LastKVFastPath(pool, num_q_heads=Hq, layer_params=params, blend=blend, rotary=_rotary,
+                          max_batch=live_max + 1, num_splits=splits or None, contract="vllm")
+    label0 = f"seed {seed} (Hq {Hq}, Hkv {Hkv}, C {C}, splits {splits})"
+
+    def check_cache(slot, seq):
+        seen = fast.seen(slot)
+        rec = max(0, (seen - 1) // C * C - C)
+        for l in range(layers):
+            for kind, ring_ref in ((0, seq.ring_k[l]), (1, seq.ring_v[l])):
+                got = _page_tokens(pool, pool.ring_table[l, slot], rec, seen - rec, kind, ring=True)
+                want = np.stack([ring_ref[t] for t in range(rec, seen)], 1)
+                assert np.array_equal(got, want), f"{label0}: slot {slot} layer {l} ring {'KV'[kind]}"
+        for kind, slab in ((0, seq.slab_k), (1, seq.slab_v)):
+            got = _page_tokens(pool, pool.src_table[slot], 0, seen, kind, ring=False)
+            assert np.array_equal(got, np.stack([slab[t] for t in range(seen)], 1)), f"{label0}: slot {slot} shared"
+
+    live = {}  # slot -> (merged oracle sequence, target length, prompt length)
+    started = steps = 0
+    worst = 0.0
+    while steps < 80 and (live or started < 10):
+        while len(live) < live_max and started < 10 and (not live or rng.random() < 0.4):
+            target = int(rng.integers(2, 200))
+            live[fast.add_sequence()] = (VP.MergedSequence(layers, Hkv, C, oparams, alpha, _rotary_np), target,
+                                         int(rng.integers(1, target)))
+            started += 1
+        rows = []
+        for slot, (_, target, prompt) in live.items():
+            if len(live) > 1 and rng.random() < 0.2:
+                continue
+            p = fast.seen(slot)
+            rows.append((slot, int(rng.integers(1, min(target - p, C - p % C) + 1)) if p < prompt else 1))
+        if not rows:
+            continue
+        fast.prepare(rows)
+        for slot, _ in rows:
+            live[slot][0].begin_step()
+        T = fast.tokens
+        q, k, v = _bf(rng, (T, Hq, 128)), _bf(rng, (T, Hkv, 128)), _bf(rng, (T, Hkv, 128))
+        for l in range(layers):
+            out = torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=DEV)
+            fast.run_layer(l, _t(q.reshape(T, -1)), _t(k.reshape(T, -1)), _t(v.reshape(T, -1)), out)
+            start, sls, wants = 0, [], []
+            for slot, n in rows:
+                sl = slice(start, start + n)
+                live[slot][0].layer(l, q[sl], k[sl], v[sl], Hq)
+                sls.append(sl)
+                wants.append(live[slot][0].last_attention)
+                start += n
+            worst = max(worst, _check_attention(captured, T, Hq, sls, out, wants, f"{label0} step {steps} layer {l}"))
+        for slot, n in rows:
+            live[slot][0].end_step(n)
+        for slot in [sl for sl, (_, target, _) in live.items() if fast.seen(sl) >= target]:
+            check_cache(slot, live[slot][0])
+            fast.free_sequence(slot)
+            del live[slot]
+        steps += 1
+    for slot in list(live):
+        check_cache(slot, live[slot][0])
+        fast.free_sequence(slot)
+    assert pool.free_pages == free0
+    print(f"{label0}: {steps} steps, {started} sequences, worst rel_l2 {worst:.2e}", flush=True)
 
 
 def test_serving_model_vllm_contract_graph_and_closeness():
