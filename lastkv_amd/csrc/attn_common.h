@@ -248,7 +248,7 @@ constexpr int kRaggedSplitCap = 32;
 
 // Split-state rows x splits a ragged call's decode-kernel class needs in the worst case over the
 // number n <= batch of its sequences (lmax query tokens each): the split count is `fixed` when
-// positive, else min(cap, ceil(cus / (n * num_kv_heads))); rows of one split count nothing.
+// positive, else min(cap, max(1, floor(cus / (n * num_kv_heads)))); rows of one split count nothing.
 int64_t ragged_split_state_rows(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t lmax, int32_t cap,
                                 int32_t fixed, int32_t cus);
 

@@ -44,7 +44,7 @@ struct DecodeParams {
   // q / out (nullptr: L tokens per sequence); rows = the call's total row count.  Only sequences
   // with col_lo < tokens * group <= col_hi run in this launch.  Their split count is `splits` when
   // dyn_splits is 0, else chosen per launch on the device from the number n of sequences in the
-  // class, min(splits, ceil(cus / (n * Hkv))); their split states are laid out by the sequence's
+  // class, min(splits, max(1, floor(cus / (n * Hkv)))); their split states are laid out by the sequence's
   // rank in the class, lmax token rows each.
   const int32_t* cu;
   int32_t rows, col_lo, col_hi;
@@ -86,7 +86,7 @@ __device__ inline ClassRank class_rank(const DecodeParams& p, int b, int hkv) {
     if (b >= i0) rank += __builtin_popcountll(b - i0 >= 64 ? m : (m & ((uint64_t{1} << (b - i0)) - 1)));
   }
   int splits = p.splits;
-  if (p.dyn_splits && n > 0) splits = min(p.splits, max(1, (p.cus + n * hkv - 1) / (n * hkv)));
+  if (p.dyn_splits && n > 0) splits = min(p.splits, max(1, p.cus / (n * hkv)));
   return ClassRank{n, rank, splits};
 }
 
@@ -105,7 +105,7 @@ __device__ inline bool class_pick(const DecodeParams& p, int u, int hkv, ClassPi
     n += __builtin_popcountll(__builtin_amdgcn_ballot_w64(i < p.batch && in_column_class(p, multi_rows(p, i).L)));
   }
   if (n == 0) return false;
-  r.splits = min(p.splits, max(1, (p.cus + n * hkv - 1) / (n * hkv)));
+  r.splits = min(p.splits, max(1, p.cus / (n * hkv)));
   r.rank = u / r.splits;
   r.split = u - r.rank * r.splits;
   if (r.rank >= n) return false;
@@ -566,7 +566,7 @@ int64_t ragged_split_state_rows(int32_t batch, int32_t num_q_heads, int32_t num_
                                 int32_t fixed, int32_t cus) {
   int64_t worst = 0;
   for (int64_t n = 1; n <= batch; ++n) {
-    const int64_t S = fixed > 0 ? fixed : std::min<int64_t>(cap, (cus + n * num_kv_heads - 1) / (n * num_kv_heads));
+    const int64_t S = fixed > 0 ? fixed : std::min<int64_t>(cap, std::max<int64_t>(1, cus / (n * num_kv_heads)));
     if (S > 1) worst = std::max(worst, n * lmax * num_q_heads * S);
   }
   return worst;
@@ -604,11 +604,12 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   const int64_t pairs = static_cast<int64_t>(a->batch) * a->num_kv_heads;
   const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
   p.cus = static_cast<int32_t>(cus);
-  // about one workgroup per CU, at least 4 blocks per split, partial states within the workspace; a
-  // ragged call's launch caps the count at what one sequence alone would take (and kRaggedSplitCap)
-  // and each launch divides the CUs among the sequences it finds in its class
-  int64_t splits = std::min<int64_t>({ragged ? std::min<int64_t>((cus + a->num_kv_heads - 1) / a->num_kv_heads, kRaggedSplitCap)
-                                             : (cus + pairs - 1) / pairs,
+  // as many splits as fit one round of workgroups (one per CU), at least 4 blocks per split, partial
+  // states within the workspace; a ragged call's launch caps the count at what one sequence alone
+  // would take (and kRaggedSplitCap) and each launch divides the CUs among the sequences it finds in
+  // its class
+  int64_t splits = std::min<int64_t>({ragged ? std::min<int64_t>(std::max<int64_t>(1, cus / a->num_kv_heads), kRaggedSplitCap)
+                                             : std::max<int64_t>(1, cus / pairs),
                                       std::max<int64_t>(blocks / 4, 1), 1024});
   // split-state rows x splits: [B, L, Hq] rows for uniform calls, the class's sequences by rank
   // (lmax rows each) for ragged ones

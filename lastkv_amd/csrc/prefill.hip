@@ -1059,7 +1059,7 @@ int64_t min_workspace_bytes(const lkv_prefill_args* a) {
     const int group = a->num_q_heads / a->num_kv_heads;
     const int L = std::min(a->max_seqlen_q, a->tokens);
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-    const int cap = std::min(kRaggedSplitCap, (cus + a->num_kv_heads - 1) / a->num_kv_heads);
+    const int cap = std::min(kRaggedSplitCap, std::max(1, cus / a->num_kv_heads));
     int64_t states = 0;
     for (const int col_hi : {16, 32, 64}) {
       const int lmax = std::min(col_hi / std::max(group, 1), L);
