@@ -34,7 +34,7 @@ typedef enum lkv_status {
 #define LKV_HEAD_DIM 128
 #define LKV_BLOCK_TOKENS 32
 #define LKV_BLOCK_ELEMS 4096
-#define LKV_ABI_VERSION 10
+#define LKV_ABI_VERSION 11
 
 /* Version of this ABI (LKV_ABI_VERSION). */
 int32_t lkv_abi_version(void);
@@ -277,6 +277,13 @@ typedef struct lkv_prefill_args {
    * lkv_prefill_workspace_bytes includes) and runs the tiles unsplit, so that a caller that fixes
    * the split count gets the same arithmetic whatever the batch. */
   int32_t num_splits;
+  /* Optional host copy of cu_seqlens_q (the same batch + 1 offsets, in host memory), or NULL.  With
+   * it a ragged call plans on the host, as FlashInfer's plan() does from its host-side indptr: it
+   * launches only the decode-kernel column classes that hold a sequence, merges a class's key
+   * splits only when it has more than one, and skips the tile kernel when no sequence needs it.
+   * It must hold the device array's values (the kernels read cu_seqlens_q); a class it shows empty
+   * is not computed.  The reference's FA3 varlen call plans inside that library; no counterpart. */
+  const int32_t *cu_seqlens_q_host;
 } lkv_prefill_args;
 
 /* Workspace bytes lkv_prefill_attn wants for these args: the fp16 V of every key block of every

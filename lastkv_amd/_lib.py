@@ -11,7 +11,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblastkv_amd.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 class LastKVNativeError(RuntimeError):
@@ -133,6 +133,7 @@ class PrefillArgs(ctypes.Structure):
         ("cu_seqlens_q", c_ptr),
         ("max_seqlen_q", c_i32),
         ("num_splits", c_i32),
+        ("cu_seqlens_q_host", c_ptr),
     ]
 
 

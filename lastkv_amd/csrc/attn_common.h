@@ -238,9 +238,10 @@ __device__ inline uint4 scale_frag(uint4 v, float s) {
 // The sequences of a prefill call with col_lo < group * tokens <= col_hi <= 64 query rows per kv head
 // (tokens: the call's count, or each sequence's own in a ragged call), run on the decode kernel with
 // one score column per (query token, head) (decode.hip).  The arguments have passed
-// lkv_prefill_attn's checks; seg was filled from them.
+// lkv_prefill_attn's checks; seg was filled from them.  class_n: the number of the ragged call's
+// sequences in the class when the host knows it (from cu_seqlens_q_host), else -1.
 int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, int32_t col_lo,
-                                 int32_t col_hi, hipStream_t s);
+                                 int32_t col_hi, int32_t class_n, hipStream_t s);
 
 // The largest split count a ragged call's decode-kernel classes take (a lone sequence of the class
 // then spreads over 32 workgroups per kv head: 256 at Hkv 8).

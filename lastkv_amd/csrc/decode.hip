@@ -573,7 +573,7 @@ int64_t ragged_split_state_rows(int32_t batch, int32_t num_q_heads, int32_t num_
 }
 
 int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg, int32_t group, int32_t col_lo,
-                                 int32_t col_hi, hipStream_t s) {
+                                 int32_t col_hi, int32_t class_n, hipStream_t s) {
   DecodeParams p;
   p.seg = seg;
   p.q = static_cast<const uint16_t*>(a->q);
@@ -633,6 +633,10 @@ int32_t prefill_on_decode_kernel(const lkv_prefill_args* a, const SegParams& seg
   const int64_t state_rows = state(splits, a->num_splits > 0 ? static_cast<int32_t>(splits) : 0);
   p.ws_o = state_rows > 0 ? static_cast<float*>(a->workspace) : nullptr;
   p.ws_ml = state_rows > 0 ? p.ws_o + state_rows * kHeadDim : nullptr;
+  // the class's split count when the host knows how many sequences it holds: the count the split
+  // kernel derives from them (so one split launches no merge); a cap the kernel cannot exceed
+  if (p.dyn_splits && class_n > 0)
+    p.splits = static_cast<int32_t>(std::min<int64_t>(p.splits, std::max<int64_t>(1, cus / (int64_t{class_n} * a->num_kv_heads))));
   const bool nt = use_nontemporal(0, pairs * tokens * kHeadDim * 2 * 2);
   // the instance holds the class's widest sequence: 16, 32 or 64 columns
   const int64_t cols = std::min<int64_t>(col_hi, static_cast<int64_t>(group) * p.L);

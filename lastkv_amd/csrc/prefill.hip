@@ -1045,6 +1045,35 @@ int64_t tile_split_bytes(const lkv_prefill_args* a, const TilePlan& t, int split
   return splits > 1 ? t.rows_all * a->num_q_heads * splits * (lkv::kHeadDim + 1) * 4 : 0;
 }
 
+// A ragged call's plan from the host copy of its offsets (cu_seqlens_q_host): the number of its
+// sequences in each decode-kernel column class (1-16, 17-32, 33-64 columns) and whether any has
+// more rows per kv head, counted as the kernels count them (offsets clamped into [0, tokens],
+// counts to max_seqlen_q).
+struct HostPlan {
+  bool known;
+  int32_t class_n[3];
+  bool any_tile;
+};
+
+HostPlan host_plan(const lkv_prefill_args* a, int64_t group) {
+  HostPlan h{};
+  const int32_t* cu = a->cu_seqlens_q_host;
+  if (a->cu_seqlens_q == nullptr || cu == nullptr) return h;
+  h.known = true;
+  const int32_t lmax = std::min(a->max_seqlen_q, a->tokens);
+  for (int32_t b = 0; b < a->batch; ++b) {
+    const int32_t s0 = std::min(std::max(cu[b], 0), a->tokens);
+    const int32_t L = std::min(std::min(std::max(cu[b + 1], s0), a->tokens) - s0, lmax);
+    if (L <= 0) continue;
+    const int64_t cols = L * group;
+    if (cols > 64)
+      h.any_tile = true;
+    else
+      ++h.class_n[cols <= 16 ? 0 : cols <= 32 ? 1 : 2];
+  }
+  return h;
+}
+
 // Whether a ragged call runs its sequences of at most 64 query rows per kv head on the decode kernel:
 // with tile_waves 0, and with tile_waves 4 or 8 too when its longest sequence has more rows.  The 4-
 // and 8-wave tiles carry each probability as one fp16, whose rel-L2 over a short sequence's few
@@ -1188,14 +1217,19 @@ extern "C" int32_t lkv_prefill_attn(const lkv_prefill_args* a, lkv_stream_t stre
   const int64_t max_cols = seq_tokens * group;
   const bool short_on_decode = a->tile_waves == 0 || ragged_short_on_decode(a);
   if (short_on_decode) {
+    // (with the host copy of a ragged call's offsets: only the classes that hold a sequence)
+    const HostPlan hp = host_plan(a, group);
     const int32_t bounds[4] = {0, 16, 32, 64};
     for (int c = 0; c < 3; ++c) {
       if (max_cols <= bounds[c]) break;
       // a uniform call is one class: the one its width falls in
       if (!ragged && max_cols > bounds[c + 1]) continue;
-      if (const int32_t st = prefill_on_decode_kernel(a, p.seg, group, bounds[c], bounds[c + 1], s)) return st;
+      if (hp.known && hp.class_n[c] == 0) continue;
+      if (const int32_t st = prefill_on_decode_kernel(a, p.seg, group, bounds[c], bounds[c + 1],
+                                                      hp.known ? hp.class_n[c] : -1, s))
+        return st;
     }
-    if (max_cols <= 64) return LKV_OK;
+    if (max_cols <= 64 || (hp.known && !hp.any_tile)) return LKV_OK;
   }
   p.q = static_cast<const uint16_t*>(a->q);
   p.q_sb = a->q_stride_b;

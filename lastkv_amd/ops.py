@@ -11,6 +11,7 @@ import ctypes
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -428,6 +429,7 @@ def prefill_attention(
     cu_seqlens_q: torch.Tensor | None = None,
     max_seqlen_q: int | None = None,
     num_splits: int = 0,
+    cu_seqlens_q_host=None,
 ) -> torch.Tensor:
     """Attention of ``q`` ``[B, L, Hq, 128]`` (L query tokens per sequence, the last L tokens of
     the local segment) over ``[older | local]``; the local segment is bottom-right causal
@@ -439,7 +441,9 @@ def prefill_attention(
     segment); ``max_seqlen_q`` (a host int) bounds every L_b, and ``out`` / ``lse`` are ``[T, Hq, 128]``
     / ``[T, Hq]``.  One call runs every sequence: those of at most 64 query rows per kv head on the
     decode kernel, the others on the tile kernel.  ``num_splits`` fixes the decode kernel's key
-    splits for those sequences (0: chosen from the grid).
+    splits for those sequences (0: chosen from the grid).  ``cu_seqlens_q_host`` (optional: the same
+    offsets on the host, a sequence of ints or an int32 array) lets the call launch only the decode
+    column classes that hold a sequence and skip merges of one split; it must equal ``cu_seqlens_q``.
 
     ``workspace`` (uint8, 16-byte aligned, at least ``prefill_workspace_bytes`` of the same
     arguments) receives the fp16 V of every key block; without it one is allocated per call.
@@ -483,8 +487,16 @@ def prefill_attention(
         _require(lse.dtype == torch.float32 and lse.is_contiguous() and lse.numel() == QB * L * Hq and lse.device == device,
                  "lse must be a contiguous fp32 [B, L, Hq] tensor ([T, Hq] ragged)")
     a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = B, L, Hq, Hkv, HEAD_DIM
+    host_cu = None
     if ragged:
         a.cu_seqlens_q, a.max_seqlen_q = cu_seqlens_q.data_ptr(), int(max_seqlen_q)
+        if cu_seqlens_q_host is not None:
+            host_cu = np.ascontiguousarray(np.asarray(cu_seqlens_q_host, dtype=np.int32))
+            _require(host_cu.ndim == 1 and host_cu.size == B + 1 and host_cu[0] == 0 and bool(np.all(np.diff(host_cu) >= 0)),
+                     "cu_seqlens_q_host must hold the B + 1 non-decreasing offsets of cu_seqlens_q, from 0")
+            a.cu_seqlens_q_host = host_cu.ctypes.data
+    else:
+        _require(cu_seqlens_q_host is None, "cu_seqlens_q_host applies to ragged calls (cu_seqlens_q)")
     _require(0 <= int(num_splits) <= 1024, "num_splits must be in [0, 1024]")
     a.num_splits = int(num_splits)
     a.sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)

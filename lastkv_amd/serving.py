@@ -251,6 +251,7 @@ class LastKVFastPath:
         i32 = dict(dtype=torch.int32, device=dev)
         self._meta = torch.zeros((4, max_batch), **i32)  # positions, older_len, local_len, local_start
         self._cu = torch.zeros(max_batch + 1, **i32)  # row offsets of a ragged step (cu_seqlens)
+        self._cu_host = None  # the same offsets on the host
         self._slots = torch.zeros(max_batch, dtype=torch.long, device=dev)
         self._older_table = torch.full((max_batch, pool.src_width), pool.scratch_page, **i32)
         self._ring_table = torch.full((pool.num_layers, max_batch, pool.ring_blocks), pool.scratch_page, **i32)
@@ -377,6 +378,7 @@ class LastKVFastPath:
                 cu = np.zeros(B + 1, dtype=np.int32)
                 cu[1:] = np.cumsum([r.tokens for r in parsed])
                 P.stager.copy(self._cu[:B + 1], cu)
+                self._cu_host = cu  # (the attention call plans its launches from the host copy)
                 pos = torch.from_numpy(np.concatenate([np.arange(r.position, r.position + r.tokens)
                                                        for r in parsed])).to(P.device, non_blocking=True)[None, :]
             self._row_rope = [self.rotary(pos)]
@@ -472,7 +474,8 @@ class LastKVFastPath:
                               older=P.pool, older_table=self._older_table[:B, :width], older_len=older_len[:B],
                               vscale=vs, local=P.pool, local_table=ring_tab[:B], local_ring_blocks=P.ring_blocks,
                               local_len=local_len[:B], local_start=local_start[:B], out_scale=out_scale,
-                              cu_seqlens_q=cu, max_seqlen_q=self.max_rows, num_splits=self.num_splits or 0)
+                              cu_seqlens_q=cu, max_seqlen_q=self.max_rows, num_splits=self.num_splits or 0,
+                              cu_seqlens_q_host=self._cu_host)
         return output
 
 

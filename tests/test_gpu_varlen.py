@@ -193,6 +193,44 @@ def test_ragged_prefill_more_than_64_sequences(paged):
     print(f"paged={paged}: 150 sequences, {sum(lengths)} rows, worst rel_l2 {worst:.2e} (automatic splits)", flush=True)
 
 
+@pytest.mark.parametrize("case", range(6))
+def test_ragged_host_offsets_plan_the_same_results(case):
+    """cu_seqlens_q_host (the offsets on the host) only plans the launches: decode column classes that
+    hold no sequence are not launched, a class of one split gets no merge, and a call without a
+    sequence above 64 rows per kv head runs no tile kernel (also when max_seqlen_q overstates its
+    longest sequence); outputs and LSE equal the call without it, bit for bit."""
+
+    rng = np.random.default_rng(600 + case)
+    lengths = [[1] * 9, [1, 3, 2, 1], [5, 0, 7, 1], [1] * 5 + [100], [40, 100, 33], [0, 1, 16, 17, 70, 1, 2]][case]
+    max_seqlen = max(lengths) + (150 if case in (0, 2) else 0)
+    Hkv, G = 2, 4
+    Hq = Hkv * G
+    seg, ks, vs, _ = _ragged_case(rng, lengths, Hkv, G, case % 2 == 1, True)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    T = int(cu[-1])
+    q = _bf(rng, (T, Hq, 128))
+    cu_t = torch.from_numpy(cu).to(DEV)
+    outs, lses = [], []
+    for host in (None, cu):
+        lse = torch.full((T, Hq), 7.0, dtype=torch.float32, device=DEV)
+        out = ops.prefill_attention(_t(q), causal=True, cu_seqlens_q=cu_t, max_seqlen_q=max_seqlen, lse=lse,
+                                    cu_seqlens_q_host=host, **seg)
+        outs.append(out)
+        lses.append(lse)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(lses[0], lses[1]), f"lengths {lengths}"
+    for b, L in enumerate(lengths):
+        if L == 0:
+            continue
+        rows = slice(int(cu[b]), int(cu[b + 1]))
+        want, _ = A.attention(q[rows].transpose(1, 0, 2)[None], ks[b], vs[b], causal_bottom_right=True)
+        want = bf16.round_bf16(want[0].transpose(1, 0, 2).astype(np.float32))
+        got = outs[1][rows].float().cpu().numpy()
+        assert A.max_abs(got, want) <= MAX_ABS and A.rel_l2(got, want) <= REL_L2, (lengths, b)
+    with pytest.raises(ValueError, match="cu_seqlens_q_host"):
+        ops.prefill_attention(_t(q), causal=True, cu_seqlens_q=cu_t, max_seqlen_q=max_seqlen,
+                              cu_seqlens_q_host=cu[:-1], **seg)
+
+
 RAGGED_SWEEP_SEED0 = 7000
 RAGGED_SWEEP_CASES = 60
 RAGGED_SWEEP_PART = 10
