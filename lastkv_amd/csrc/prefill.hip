@@ -99,25 +99,10 @@ __device__ inline bool on_tile_path(const PrefillParams& p, const SeqRows& sr) {
   return sr.L > 0 && static_cast<int64_t>(sr.L) * p.group > p.decode_rows;
 }
 
+// Two values as packed fp16, rounded toward zero: exact for bf16 values of magnitude 2^-17 to 65280
+// and for zero (below 2^-17 fp16's subnormals keep them to a multiple of 2^-24).
 __device__ inline uint32_t f16x2_bits(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-}
-
-// 8 bf16 -> 8 fp16 (exact in range); with kScale the value is bf16(v * s) first.
-template <bool kScale>
-__device__ inline uint4 v_to_f16(uint4 v, float s) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  auto cv = [s](uint32_t w) -> uint32_t {
-    float lo = bf16_lo(w), hi = bf16_hi(w);
-    if (kScale) {  // one v_cvt_pk_bf16_f32 rounds both products
-      const uint32_t packed = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo * s, hi * s}), bf16x2));
-      lo = bf16_lo(packed);
-      hi = bf16_hi(packed);
-    }
-    return f16x2_bits(lo, hi);
-  };
-  return make_uint4(cv(v.x), cv(v.y), cv(v.z), cv(v.w));
 }
 
 // Whether either bf16 of a packed pair is finite with magnitude >= 65536 (exponent field 143-254):
