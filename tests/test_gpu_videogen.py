@@ -81,10 +81,23 @@ def _t(x):
     return torch.from_numpy(np.ascontiguousarray(x)).to(DEV, torch.bfloat16)
 
 
-@pytest.mark.parametrize("B,S,keep,H", [(1, 200, 70, 4), (2, 96, 32, 2), (1, 136, None, 3), (1, 64, 1000, 2)])
-def test_wan_rollout_matches_oracle(B, S, keep, H):
+def _random_rollout(seed):
+    rng = np.random.default_rng(740 + seed)
+    S = int(rng.integers(5, 260))
+    keep = [None, int(rng.integers(1, 2 * S)), 10 ** 6][int(rng.integers(0, 3))]
+    return int(rng.integers(1, 3)), S, keep, int(rng.integers(1, 7)), int(rng.integers(3, 7))
+
+
+@pytest.mark.parametrize("B,S,keep,H,blocks", [(1, 200, 70, 4, 5), (2, 96, 32, 2, 5), (1, 136, None, 3, 5),
+                                               (1, 64, 1000, 2, 5)] + [_random_rollout(i) for i in range(6)])
+def test_wan_rollout_matches_oracle(B, S, keep, H, blocks):
+    """Block-causal rollouts through WanKVCache against the oracle: every layer's attention of every
+    pass (denoising and the clean update pass) and the history after each commit; the four fixed
+    cases and six seeded random ones (block sizes 5-259 tokens, kept prefixes short, long or the
+    whole history, 1-6 heads, 3-6 blocks)."""
+
     rng = np.random.default_rng(S + (keep or 0))
-    L, blocks = 3, 5
+    L = 3
     total = S * (blocks - 1)
     cache = WanKVCache(num_layers=L, num_heads=H, block_tokens=S, total_tokens=total, keep_tokens=keep, batch=B,
                        device=DEV)
