@@ -107,6 +107,36 @@ def test_incremental_decoding_across_boundaries(segments):
     _no_worse_than_reference_bf16(torch.cat(logits, 1), want, ref16, f"segments {segments}")
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_incremental_decoding_random_segmentations(seed):
+    """Chunk sizes 4-64 with seeded random call segmentations (pieces of 1 token to 2 chunks, crossing
+    boundaries anywhere, then single tokens), B = 1 or 2: logits no further from the fp32 oracle
+    than the reference's bf16 path, and the cache's region lengths after every call."""
+
+    rng = np.random.default_rng(900 + seed)
+    C = [4, 8, 12, 20, 48, 64][seed]
+    B = int(rng.integers(1, 3))
+    segments = []
+    while sum(segments) < 5 * C + 20:
+        segments.append(int(rng.integers(1, 2 * C + 1)))
+    segments += [1] * int(rng.integers(3, 12))
+    oracle, ours = _tiny(C)
+    tokens = torch.randint(3, 97, (B, sum(segments)), generator=torch.Generator().manual_seed(seed)).to(DEV)
+    cache, start, logits = None, 0, []
+    with torch.inference_mode():
+        want, _ = _o32(oracle)(tokens)
+        ref16, _ = _o16(oracle)(tokens)
+        for size in segments:
+            out = ours(tokens[:, start:start + size], past_key_values=cache)
+            logits.append(out.logits)
+            cache = out.past_key_values
+            start += size
+            assert cache.get_seq_length() == start
+            assert cache.deep is None or cache.deep[0].shape[2] == start // C * C
+            assert all(kv is None or kv[0].shape[2] == start % C for kv in cache.current)
+    _no_worse_than_reference_bf16(torch.cat(logits, 1), want, ref16, f"seed {seed}: C={C} B={B} segments {segments}")
+
+
 def test_cache_contents_match_oracle_cache():
     """current[0] equals the oracle's layer-0 K/V (same inputs); deep (the final layer's K/V,
     after the bf16 cascade) is within rel-L2 1e-2 of the oracle's; previous[l] is the reference's
