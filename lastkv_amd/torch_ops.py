@@ -69,11 +69,13 @@ def prefill_attention(q: Tensor, older_k: Optional[Tensor], older_v: Optional[Te
                       local_len_const: int, local_start: Optional[Tensor], local_start_const: int,
                       local_table: Optional[Tensor], local_ring_blocks: int, causal: bool, sm_scale: float,
                       out_scale: Optional[Tensor] = None, cu_seqlens_q: Optional[Tensor] = None,
-                      max_seqlen_q: int = 0, num_splits: int = 0) -> Tensor:
+                      max_seqlen_q: int = 0, num_splits: int = 0, cu_seqlens_q_host: Optional[Tensor] = None) -> Tensor:
     """``lkv_prefill_attn``: q ``[B, L, Hq, 128]`` (the last L tokens of the local segment) ->
     out ``[B, L, Hq, 128]``; bottom-right causal over the local segment when ``causal``.  With
     ``cu_seqlens_q`` (int32 ``[B + 1]``) and ``max_seqlen_q`` q / out are ragged ``[T, Hq, 128]``
-    (FlashAttention's varlen form); ``num_splits`` 0 lets the library choose the key splits."""
+    (FlashAttention's varlen form), and ``cu_seqlens_q_host`` (the same offsets as an int32 CPU
+    tensor, optional) lets the call plan its launches on the host; ``num_splits`` 0 lets the library
+    choose the key splits."""
 
     return ops.prefill_attention(
         q, older=_seg(older_k, older_v, older_table), older_len=_len(older_len, older_len_const), vscale=vscale,
@@ -81,13 +83,13 @@ def prefill_attention(q: Tensor, older_k: Optional[Tensor], older_v: Optional[Te
         local_start=_len(local_start, local_start_const), older_table=older_table, local_table=local_table,
         local_ring_blocks=local_ring_blocks or None, causal=causal, sm_scale=sm_scale or None, out_scale=out_scale,
         cu_seqlens_q=cu_seqlens_q, max_seqlen_q=max_seqlen_q if cu_seqlens_q is not None else None,
-        num_splits=num_splits)
+        num_splits=num_splits, cu_seqlens_q_host=None if cu_seqlens_q_host is None else cu_seqlens_q_host.numpy())
 
 
 @prefill_attention.register_fake
 def _(q, older_k, older_v, older_len, older_len_const, older_table, vscale, local_k, local_v, local_len,
       local_len_const, local_start, local_start_const, local_table, local_ring_blocks, causal, sm_scale,
-      out_scale=None, cu_seqlens_q=None, max_seqlen_q=0, num_splits=0):
+      out_scale=None, cu_seqlens_q=None, max_seqlen_q=0, num_splits=0, cu_seqlens_q_host=None):
     return q.new_empty(q.shape)
 
 

@@ -127,6 +127,10 @@ def test_ragged_ops_equal_the_ctypes_calls():
             0.0, None, cu, 40, 0)
     assert torch.equal(L.prefill_attention(*args), want)
     torch.library.opcheck(L.prefill_attention, args)
+    # the same with the host copy of the offsets (an int32 CPU tensor), which only plans the launches
+    hargs = args + (cu.cpu(),)
+    assert torch.equal(L.prefill_attention(*hargs), want)
+    torch.library.opcheck(L.prefill_attention, hargs)
     qq, kk, vv = _r(g, (T, Hq * 128)), _r(g, (T, Hkv * 128)), _r(g, (T, Hkv * 128))
     cs = _r(g, (T, 128))
     pos = i32([300, 41, 77])
