@@ -292,7 +292,7 @@ def epilogue_measurement(ops, torch, dev, reps: int = 20) -> dict:
     layer's tiled ring (bf16).  Algorithmic bytes: q/k/v read once, q written once, k/v written once,
     the cos/sin rows read once; compared with a device copy of the same number of bytes.  Timed with
     q, k, v as separate tensors (the HF module's three projections) and as row views of one fused
-    projection output (the serving path's layout)."""
+    projection output (the serving path's layout), the latter also with the vLLM rounding contract."""
 
     B, L = 32, 2048
     g = torch.Generator(device=dev).manual_seed(8)
@@ -328,6 +328,18 @@ def epilogue_measurement(ops, torch, dev, reps: int = 20) -> dict:
     e1.record()
     torch.cuda.synchronize()
     us_fused = e0.elapsed_time(e1) * 1e3 / reps
+    # the vLLM rounding contract on the same layout (ring V scaled by 1 / s; the same tensors read
+    # and written, so the same algorithmic bytes)
+    vkw = dict(kw, rounding="vllm", ring_v_mul=torch.full((HKV,), 0.75, device=dev))
+    for _ in range(3):
+        ops.qkv_epilogue(fq, fk, fv, cos, sin, **vkw)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        ops.qkv_epilogue(fq, fk, fv, cos, sin, **vkw)
+    e1.record()
+    torch.cuda.synchronize()
+    us_vllm = e0.elapsed_time(e1) * 1e3 / reps
     del qkv, fq, fk, fv
     T = B * L
     nbytes = T * (HQ + 2 * HKV) * D * 2 + T * HQ * D * 2 + T * 2 * HKV * D * 2 + T * 2 * D * 2
@@ -349,6 +361,8 @@ def epilogue_measurement(ops, torch, dev, reps: int = 20) -> dict:
         "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
         "fused_projection_us_per_call": round(us_fused, 1),
         "fused_projection_hbm_frac": round(nbytes / us_fused / 1e3 / HBM_PEAK_GBS, 4),
+        "vllm_rounding_fused_us_per_call": round(us_vllm, 1),
+        "vllm_rounding_fused_hbm_frac": round(nbytes / us_vllm / 1e3 / HBM_PEAK_GBS, 4),
         "same_bytes_device_copy_us": round(copy_us, 1), "copy_gbps": round(nbytes / copy_us / 1e3, 1),
         "frac_of_copy": round(copy_us / us, 4),
     }
