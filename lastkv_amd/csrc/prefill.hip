@@ -377,21 +377,47 @@ __device__ __attribute__((always_inline)) inline void v16_stage_blocks(const Pre
 
 // Whether some block in [0, nbt) of (b, kvh) holds a V value fp16 cannot (the pre-pass's flags),
 // read 16 flags per load over the wave.
-__device__ inline bool tile_needs_wide(const PrefillParams& p, int b, int kvh, int nbt) {
+// The flags of blocks [i, i + 16) of a flag row, those at or past nbt cleared (by masks, not by an
+// indexed write, which would put the word in LDS).
+__device__ inline uint4 flags_below(uint4 w, int i, int nbt) {
+  const int valid = nbt - i;  // flags of this word that count (0-16)
+  auto mask = [valid](int word) {
+    const int n = min(max(valid - 4 * word, 0), 4);  // bytes of this 32-bit word that count
+    return n == 4 ? 0xffffffffu : (1u << (8 * n)) - 1u;
+  };
+  return make_uint4(w.x & mask(0), w.y & mask(1), w.z & mask(2), w.w & mask(3));
+}
+
+// Whether some block in [0, nbt) of (b, kvh) holds a V value fp16 cannot (the pre-pass's flags), in
+// two parts so that the load's latency can pass under other loads: flags_peek issues each lane's
+// first 16 flags (the row's first 1024 blocks), flags_any masks them, reads any further ones and
+// takes the wave's ballot.
+struct FlagPeek {
+  uint4 w;
+};
+
+__device__ inline FlagPeek flags_peek(const PrefillParams& p, int b, int kvh, int nbt) {
+  const uint8_t* f = p.vflags + (static_cast<int64_t>(b) * p.hkv + kvh) * p.vflag_stride;
+  const int i = (threadIdx.x & 63) * 16;
+  FlagPeek r{make_uint4(0, 0, 0, 0)};
+  if (i < nbt) r.w = *reinterpret_cast<const uint4*>(f + i);
+  return r;
+}
+
+__device__ inline bool flags_any(const FlagPeek& pk, const PrefillParams& p, int b, int kvh, int nbt) {
   const uint8_t* f = p.vflags + (static_cast<int64_t>(b) * p.hkv + kvh) * p.vflag_stride;
   const int lane = threadIdx.x & 63;
-  bool any = false;
-  for (int i = lane * 16; i < nbt; i += 64 * 16) {
-    uint4 w = *reinterpret_cast<const uint4*>(f + i);
-    // flags past nbt (other blocks of the row, or padding) do not count
-    const int valid = min(16, nbt - i);
-    if (valid < 16) {
-      uint32_t* ww = reinterpret_cast<uint32_t*>(&w);
-      for (int k = valid; k < 16; ++k) ww[k >> 2] &= ~(0xffu << (8 * (k & 3)));
-    }
+  uint4 w = flags_below(pk.w, lane * 16, nbt);
+  bool any = (w.x | w.y | w.z | w.w) != 0;
+  for (int i = lane * 16 + 64 * 16; i < nbt; i += 64 * 16) {
+    w = flags_below(*reinterpret_cast<const uint4*>(f + i), i, nbt);
     any |= (w.x | w.y | w.z | w.w) != 0;
   }
   return __builtin_amdgcn_ballot_w64(any) != 0;
+}
+
+__device__ inline bool tile_needs_wide(const PrefillParams& p, int b, int kvh, int nbt) {
+  return flags_any(flags_peek(p, b, kvh, nbt), p, b, kvh, nbt);
 }
 
 // Whether some key block of (b, kvh) holds a V value fp16 cannot, over all nb of its blocks.
@@ -453,10 +479,15 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
   const int wg_last_row = min(rows_total, wg_row0 + kRowsPerWg) - 1;
   const int nbt = __builtin_amdgcn_readfirstlane(sv.nb0 + local_blocks(sv, visible_local(p, sv, sr.L, wg_last_row / G)));
   // The tiles that read a V block fp16 cannot hold belong to the wide instance: it leaves the other
-  // tiles at once, and the fp16 instance leaves these at its prologue's barrier, so that the flag
-  // load overlaps its first loads.  (Both workgroup-uniform.)
-  const bool needs_wide = tile_needs_wide(p, b, kvh, nbt);
-  if (kWide && !needs_wide) return;
+  // tiles at once, and the fp16 instance leaves these at its prologue's barrier, reducing the flags
+  // only after its first Q and K / V loads are issued, so that the flag load's latency passes under
+  // theirs.  (Both workgroup-uniform.)
+  const FlagPeek flag_peek = flags_peek(p, b, kvh, nbt);
+  bool needs_wide = false;
+  if (kWide) {
+    needs_wide = flags_any(flag_peek, p, b, kvh, nbt);
+    if (!needs_wide) return;
+  }
   const float vs_older = p.vscale_mode ? p.vscale[kvh] : 1.f;  // (the wide instance's V scale)
   // this split's blocks [kb0, kb1) (the wide instance runs every block as split 0)
   const int S = kWide ? 1 : p.tile_splits;
@@ -537,6 +568,7 @@ __device__ __attribute__((always_inline)) inline void prefill_tile(const Prefill
       const int lb = min(kb0 + j + kStages, last);
       stage_load<NW, kWide>(sets[j % kStages], rsrc, k_block<kPaged>(sv, lb), vb(lb), lb, wave, lane_off);
     }
+    if (!kWide) needs_wide = flags_any(flag_peek, p, b, kvh, nbt);
     if (!kWide && needs_wide) {
       if (threadIdx.x == 0) *p.any_wide = 1.f;
       return;
