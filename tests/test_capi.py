@@ -118,3 +118,54 @@ def test_noalloc_decode_rejections_before_any_launch(batch, splits, workspace, m
     a.workspace, a.workspace_bytes = (16, workspace) if workspace else (None, 0)
     assert lib.lkv_decode_attn_noalloc(ctypes.byref(a), None) == 1
     assert message in lib.lkv_last_error()
+
+
+@pytest.mark.parametrize("field,value,message", [("num_splits", 2000, b"num_splits"), ("max_seqlen_q", 0, b"max_seqlen_q")])
+def test_prefill_ragged_and_split_arguments_rejected(field, value, message):
+    """A ragged call (cu_seqlens_q set) needs max_seqlen_q >= 1; num_splits stays within [0, 1024]."""
+
+    lib = _lib.load()
+    a = _lib.PrefillArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim, a.causal = 2, 6, 8, 2, 128, 1
+    a.q = a.out = a.cu_seqlens_q = 16
+    a.max_seqlen_q = 4
+    setattr(a, field, value)
+    assert lib.lkv_prefill_attn(ctypes.byref(a), None) == 1
+    assert message in lib.lkv_last_error()
+
+
+def _qkv_args():
+    a = _lib.QkvArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.batch, a.tokens, a.num_q_heads, a.num_kv_heads, a.head_dim = 1, 4, 8, 2, 128
+    a.q = a.k = a.v = a.cos = a.sin = a.q_out = a.ring_k = a.ring_v = 16
+    a.ring_tokens, a.ring_num_slots = 64, 1
+    return a
+
+
+@pytest.mark.parametrize("field,value,message", [("head_dim", 64, b"head_dim"), ("rounding", 2, b"rounding"),
+                                                 ("ring_tokens", 40, b"multiple of 32"), ("q", None, b"null tensor"),
+                                                 ("ring_num_slots", 0, b"ring_num_slots"),
+                                                 ("position_const", -1, b"negative position")])
+def test_epilogue_rejects_bad_arguments_before_any_launch(field, value, message):
+    lib = _lib.load()
+    a = _qkv_args()
+    setattr(a, field, value)
+    assert lib.lkv_qkv_epilogue(ctypes.byref(a), None) == 1
+    assert message in lib.lkv_last_error()
+
+
+@pytest.mark.parametrize("field,value,message", [("chunk_len", 96, b"chunk longer than the ring"),
+                                                 ("deep_capacity_tokens", 32, b"deep capacity"),
+                                                 ("alpha", None, b"null pointer"), ("kv_heads", 0, b"bad sizes")])
+def test_blend_rejects_bad_arguments_before_any_launch(field, value, message):
+    lib = _lib.load()
+    a = _lib.BlendArgs()
+    a.struct_size = ctypes.sizeof(a)
+    a.layers, a.batch, a.kv_heads, a.chunk_start, a.chunk_len = 1, 1, 2, 32, 32
+    a.ring_tokens, a.deep_capacity_tokens = 64, 128
+    a.ring_k = a.ring_v = a.deep_k = a.deep_v = a.alpha = a.one_minus_alpha = 16
+    setattr(a, field, value)
+    assert lib.lkv_blend_chunk(ctypes.byref(a), None) == 1
+    assert message in lib.lkv_last_error()
