@@ -29,6 +29,7 @@ Two rounding contracts (``contract=``):
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 
 import numpy as np
@@ -260,6 +261,13 @@ class LastKVFastPath:
         self._q_out = torch.empty((max_batch, num_q_heads, ops.HEAD_DIM), dtype=torch.bfloat16, device=dev)
         self._decode_ws = torch.empty(16, dtype=torch.uint8, device=dev)
         self._prefill_ws = torch.empty(16, dtype=torch.uint8, device=dev)
+        # The reference's runtime self-check (RMARIN_MERGED_CHECK, fastpath.py:198-202), also read as
+        # LASTKV_MERGED_CHECK: "1" recomputes every eager layer call in two passes from the same pool
+        # and reports the distance (_merged_check); "2" also hands the two-pass result to the model.
+        mode = os.environ.get("LASTKV_MERGED_CHECK") or os.environ.get("RMARIN_MERGED_CHECK")
+        self.check = mode in ("1", "2")
+        self.check_replace = mode == "2"
+        self._check_calls = 0
         self.rows: list[_Row] = []
         self.batch = 0  # rows of this step, padding included
         self.tokens = 0  # query tokens of this step, padding included
@@ -457,6 +465,8 @@ class LastKVFastPath:
                 seg["older_table"] = self._older_table[:B, :width]
                 ops.prefill_attention(q_out, causal=True, out=output[:T].view(B, n, Hq, 128),
                                       workspace=self._prefill_ws, num_splits=self.num_splits or 0, **seg)
+            if self.check:
+                self._merged_check(layer_index, q_out.view(B, n, Hq, 128), output[:T].view(B, n, Hq, 128), seg)
             return output
         # ragged step (prefill pieces and decode tokens of different lengths): one epilogue and one
         # attention call over the rows back to back (cu_seqlens), as the reference's single varlen
@@ -470,13 +480,50 @@ class LastKVFastPath:
             deep=P.pool if top else None, deep_table=self._older_table[:B] if top else None,
             q_out=self._q_out[:T], cu_seqlens=cu, max_seqlen=self.max_rows, **epi)
         width = max(1, -(-max(r.older for r in self.rows) // BLOCK))
+        seg = dict(older=P.pool, older_table=self._older_table[:B, :width], older_len=older_len[:B], vscale=vs,
+                   local=P.pool, local_table=ring_tab[:B], local_ring_blocks=P.ring_blocks, local_len=local_len[:B],
+                   local_start=local_start[:B], out_scale=out_scale)
         ops.prefill_attention(q_out, causal=True, out=output[:T].view(T, Hq, 128), workspace=self._prefill_ws,
-                              older=P.pool, older_table=self._older_table[:B, :width], older_len=older_len[:B],
-                              vscale=vs, local=P.pool, local_table=ring_tab[:B], local_ring_blocks=P.ring_blocks,
-                              local_len=local_len[:B], local_start=local_start[:B], out_scale=out_scale,
                               cu_seqlens_q=cu, max_seqlen_q=self.max_rows, num_splits=self.num_splits or 0,
-                              cu_seqlens_q_host=self._cu_host)
+                              cu_seqlens_q_host=self._cu_host, **seg)
+        if self.check:
+            self._merged_check(layer_index, q_out, output[:T].view(T, Hq, 128), seg, ragged=(cu, self.max_rows))
         return output
+
+    def _merged_check(self, layer_index: int, q: torch.Tensor, out: torch.Tensor, seg: dict, ragged=None) -> None:
+        """The reference's merged-path self-check (``_merged_check``, fastpath.py:737-773): the layer
+        call again in two passes from the same pool, the older segment alone (every key visible) and
+        the ring segment alone (bottom-right causal), each with its LSE, merged exactly
+        (``merge_states``; a sequence without older keys has LSE -inf there); prints the relative L2
+        distance of the one-pass output to it for the first 192 calls and for any call above 0.02,
+        and with ``check_replace`` writes the two-pass result into ``out``.  Eager calls only: a call
+        made under HIP graph capture is not checked."""
+
+        if torch.cuda.is_current_stream_capturing():
+            return
+        H = out.shape[-2]
+        rg = {} if ragged is None else dict(cu_seqlens_q=ragged[0], max_seqlen_q=ragged[1])
+        older = {k: seg[k] for k in ("older", "older_table", "older_len", "vscale")}
+        local = {k: seg[k] for k in ("local", "local_table", "local_ring_blocks", "local_len", "local_start")}
+        so, lo = torch.empty_like(out), torch.empty_like(out)
+        sl = torch.empty(out.shape[:-1], dtype=torch.float32, device=out.device)
+        ll = torch.empty_like(sl)
+        ops.prefill_attention(q, causal=False, out=so, lse=sl, out_scale=seg["out_scale"], **older, **rg)
+        ops.prefill_attention(q, causal=True, out=lo, lse=ll, out_scale=seg["out_scale"], **local, **rg)
+        ref, _ = ops.merge_states(so.reshape(-1, H, ops.HEAD_DIM), sl.reshape(-1, H), lo.reshape(-1, H, ops.HEAD_DIM),
+                                  ll.reshape(-1, H))
+        real = sum(r.tokens for r in self.rows)  # (a padded decode step's empty rows follow)
+        got, want = out.reshape(-1, H, ops.HEAD_DIM)[:real].float(), ref[:real].float()
+        rel = float((want - got).norm() / want.norm().clamp(min=1e-6))
+        self._check_calls += 1
+        if self._check_calls <= 32 * 6 or rel > 0.02:
+            print({"lastkv_merged_check": {"layer": layer_index, "batch": len(self.rows), "tokens": real,
+                                           "older": [r.older for r in self.rows][:4],
+                                           "local": [r.local for r in self.rows][:4], "rel": round(rel, 5),
+                                           "out_absmax": round(float(got.abs().max()), 2),
+                                           "ref_absmax": round(float(want.abs().max()), 2)}}, flush=True)
+        if self.check_replace:
+            out.reshape(-1, H, ops.HEAD_DIM)[:real].copy_(ref[:real])
 
 
 def fuse_linears(mods) -> tuple[torch.Tensor, torch.Tensor | None]:

@@ -328,3 +328,94 @@ def test_vllm_impl_adapter_runs_the_fast_path(contract):
         assert impl.forward(SimpleNamespace(rmarin_layer_index=0), q, k, v, None, None, out) is out and not out.any()
     finally:
         VB.set_current(None)
+
+
+@pytest.mark.parametrize("contract", ["hf", "vllm"])
+def test_merged_check_reports_two_pass_agreement(contract, monkeypatch, capsys):
+    """LASTKV_MERGED_CHECK=1 (the reference's RMARIN_MERGED_CHECK, fastpath.py:198-202, 737-773):
+    every eager layer call is recomputed in two passes from the same pool (older segment, ring
+    segment, exact LSE merge) and reported; over uniform prefill, ragged and padded decode steps
+    that cross chunk boundaries the one-pass output stays within 5e-3 (rel-L2) of it.  Mode 2 hands
+    the two-pass result to the model; under graph capture nothing is checked and replays still
+    equal eager steps."""
+
+    import ast
+
+    monkeypatch.setenv("LASTKV_MERGED_CHECK", "1")
+    g = torch.Generator(device=DEV).manual_seed(11)
+    layers, Hq, Hkv, C, cap = 2, 8, 2, 48, 640
+    params = []
+    for l in range(layers):
+        w = (torch.rand(128, generator=g, device=DEV) + 0.5).bfloat16()
+        vs = (torch.rand(Hkv, generator=g, device=DEV) + 0.4).bfloat16().float()
+        params.append((w, w.flip(0).contiguous(), 1e-5, vs))
+    alpha = torch.rand(layers * Hkv, generator=g, device=DEV).bfloat16().float()
+    blend = (alpha, (1 - alpha).bfloat16().float(), torch.cat([p[3] for p in params]))
+    pool = LastKVPagePool(num_layers=layers, kv_heads=Hkv, chunk_size=C, max_slots=4, source_pages=64,
+                          max_tokens_per_slot=cap, device=DEV)
+    fast = LastKVFastPath(pool, num_q_heads=Hq, layer_params=params, blend=blend, rotary=_rotary, max_batch=6,
+                          contract=contract)
+    assert fast.check and not fast.check_replace
+    slots = [fast.add_sequence() for _ in range(3)]
+    schedule = [([(0, 48), (1, 48), (2, 48)], None), ([(0, 48), (1, 20), (2, 5)], None),
+                ([(1, 28), (0, 48), (2, 43)], None), ([(0, 1), (1, 1)], 4), ([(2, 30), (0, 2), (1, 1)], None)]
+    schedule += [([(0, 1), (1, 1), (2, 1)], 5 if i % 2 else None) for i in range(20)]
+    calls = 0
+    for rows, pad in schedule:
+        fast.prepare([(slots[i], n) for i, n in rows], pad_to=pad)
+        T = fast.tokens
+        q = torch.randn((T, Hq * 128), generator=g, device=DEV).bfloat16()
+        k = torch.randn((T, Hkv * 128), generator=g, device=DEV).bfloat16()
+        v = torch.randn((T, Hkv * 128), generator=g, device=DEV).bfloat16()
+        for l in range(layers):
+            fast.run_layer(l, q, k, v, torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=DEV))
+            calls += 1
+    reports = [ast.literal_eval(line)["lastkv_merged_check"] for line in capsys.readouterr().out.splitlines()
+               if line.startswith("{'lastkv_merged_check'")]
+    assert len(reports) == calls, (len(reports), calls)
+    worst = max(r["rel"] for r in reports)
+    with capsys.disabled():
+        print(f"{contract}: {calls} layer calls checked, worst rel-L2 {worst:.2e}", flush=True)
+    assert worst < 5e-3
+    assert any(r["older"][0] > 0 for r in reports), "no call had an older segment"
+
+    # mode 2: the output is the two-pass result
+    fast.check_replace = True
+    fast.prepare([(slots[i], 1) for i in range(3)])
+    T = fast.tokens
+    q = torch.randn((T, Hq * 128), generator=g, device=DEV).bfloat16()
+    k = torch.randn((T, Hkv * 128), generator=g, device=DEV).bfloat16()
+    v = torch.randn((T, Hkv * 128), generator=g, device=DEV).bfloat16()
+    out = torch.empty((T, Hq, 128), dtype=torch.bfloat16, device=DEV)
+    fast.run_layer(0, q, k, v, out)
+    rep = [ast.literal_eval(line)["lastkv_merged_check"] for line in capsys.readouterr().out.splitlines()
+           if line.startswith("{'lastkv_merged_check'")]
+    assert len(rep) == 1 and torch.isfinite(out.float()).all()
+
+
+def test_merged_check_skips_graph_capture(monkeypatch, capsys):
+    """With the check on, a captured decode step checks nothing and its replays equal eager steps
+    (the eager runner's calls, and the graph's one eager warm-up step, are checked and left
+    unchanged)."""
+
+    monkeypatch.setenv("LASTKV_MERGED_CHECK", "1")
+    _, ours = _tiny(chunk=8)
+    eager = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=96, num_splits=2)
+    graphed = LastKVServingModel(ours, max_batch=4, max_tokens_per_slot=96, num_splits=2)
+    assert eager.fast.check and graphed.fast.check
+    prompts = [torch.arange(3, 14, device=DEV), torch.tensor([1, 5, 17, 33, 2], device=DEV)]
+    se = [eager.add_sequence() for _ in prompts]
+    sg = [graphed.add_sequence() for _ in prompts]
+    with torch.inference_mode():
+        t_eager = _prefill(eager, se, prompts, 8)
+        t_graph = _prefill(graphed, sg, prompts, 8)
+        graph = graphed.decode_graph(sg)
+        capsys.readouterr()
+        for i in range(12):
+            le = eager.step([(s, t_eager[j:j + 1]) for j, s in enumerate(se)])
+            lg, ng = graph.step(t_graph)
+            assert torch.equal(le, lg), f"step {i}"
+            t_eager, t_graph = le.argmax(-1), ng.clone()
+    lines = [l for l in capsys.readouterr().out.splitlines() if l.startswith("{'lastkv_merged_check'")]
+    # the eager runner's 12 steps and the graph's eager warm-up step before its capture
+    assert len(lines) == 13 * len(ours.model.layers), len(lines)
