@@ -14,8 +14,9 @@
 namespace lkv {
 namespace {
 
-// Value of the bf16 nearest to x (round to nearest even), as fp32.
-__device__ inline float rb(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+// Value of the bf16 nearest to x (round to nearest even), as fp32, in one v_cvt_pk_bf16_f32: with
+// bf16(0) = 0 as the low half, the packed word is that fp32 value (no shift or mask to unpack it).
+__device__ inline float rb(float x) { return __uint_as_float(pack_bf16x2(0.f, x)); }
 
 // The torch-order RMSNorm's fp32 sum of squares of one row, in the order both epilogue forms share
 // (the reference's own reduction order is torch's and not fixed): for each of the 8 groups of dims
@@ -275,16 +276,16 @@ __device__ inline RopeCS rope_cs(uint4 ca, uint4 cb, uint4 sa, uint4 sb) {
   return RopeCS{{ca}, {cb}, {sa}, {sb}};
 }
 
-// Rounds a and b to bf16 with one v_cvt_pk_bf16_f32 (round to nearest even, as rb).
+// Rounds a and b to bf16 (round to nearest even), one instruction each (rb): two conversions
+// cost less than one v_cvt_pk_bf16_f32 of the pair and the two instructions unpacking it.
 __device__ inline void rb2(float& a, float& b) {
-  const uint32_t u = pack_bf16x2(a, b);
-  a = bf16_lo(u);
-  b = bf16_hi(u);
+  a = rb(a);
+  b = rb(b);
 }
 
 // RoPE then RMSNorm of the row held by an 8-lane group (lane l: dims 8l.. in a / 64 + 8l.. in b),
-// every bf16 operation of the reference rounded in the same order (two roundings per
-// v_cvt_pk_bf16_f32; the last one is the packing of the output).
+// every bf16 operation of the reference rounded in the same order (rb; the last rounding is the
+// packing of the output).
 __device__ inline void rope_norm_row(uint4& a, uint4& b, const RopeCS& cs, const NormW& w, float eps) {
   float x0[8], x1[8], r0[8], r1[8];
   unpack8(a, x0), unpack8(b, x1);
