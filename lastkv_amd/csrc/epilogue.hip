@@ -360,8 +360,12 @@ __device__ inline void rope_norm_row_vllm(uint4& a, uint4& b, const RopeCS& cs, 
   b = pack8(r1);
 }
 
+// kMode 1: the vLLM order (fixed at compile time); kMode 0: either order, by `rounding` at run time.
+// (A block kernel specialised to the HF order measured slower for q, k, v as separate tensors:
+// 311-316 against 305-310 us at config 3's prefill call, same box, four rounds.)
+template <int kMode>
 __device__ inline void rope_norm_row_any(uint4& a, uint4& b, const RopeCS& cs, const NormW& w, float eps, int rounding) {
-  if (rounding == 0)
+  if (kMode == 0 && rounding == 0)
     rope_norm_row(a, b, cs, w, eps);
   else
     rope_norm_row_vllm(a, b, cs, w, eps);
@@ -392,6 +396,17 @@ __device__ inline void store_nt(uint16_t* dst, uint4 v) {
   __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dst));
 }
 
+// The cos or sin values of lane l's dims: dims [0, 64) only in the vLLM order, whose rotation takes
+// them for both halves (the block kernel's vLLM instance then issues half the loads).
+template <int kRounding>
+__device__ inline void load_cs(const uint16_t* row, int l, uint4& a, uint4& b) {
+  a = *reinterpret_cast<const uint4*>(row + 8 * l);
+  if constexpr (kRounding == 0)
+    b = *reinterpret_cast<const uint4*>(row + 64 + 8 * l);
+  else
+    b = make_uint4(0, 0, 0, 0);
+}
+
 // query heads of one token per 8-lane group (one cos / sin load for all; measured at config 3's
 // prefill call shape: 2 heads 310 us, 4 heads 313 us, 8 heads 335 us per call)
 constexpr int kQRows = 2;
@@ -404,6 +419,7 @@ struct QItem {
 // grp = (b, i, head group).  The loads are unconditional (a group past the end rereads the last
 // one, heads past Hq the last head) so that the compiler can count them for s_waitcnt and the next
 // group's loads stay in flight while this one is computed.
+template <int kRounding>
 __device__ inline void q_item_load(const QkvParams& p, int32_t grp, int32_t groups, int hgroups, int l, QItem& it) {
   grp = grp < groups ? grp : groups - 1;
   const int h0 = grp % hgroups * kQRows;
@@ -413,10 +429,11 @@ __device__ inline void q_item_load(const QkvParams& p, int32_t grp, int32_t grou
 #pragma unroll
   for (int r = 0; r < kQRows; ++r)
     load_row_nt(qrow + static_cast<int64_t>(min(h0 + r, p.hq - 1)) * kHeadDim, l, it.xa[r], it.xb[r]);
-  load_row(p.cos + b * p.cs_sb + i * p.cs_st, l, it.ca, it.cb);
-  load_row(p.sin + b * p.cs_sb + i * p.cs_st, l, it.sa, it.sb);
+  load_cs<kRounding>(p.cos + b * p.cs_sb + i * p.cs_st, l, it.ca, it.cb);
+  load_cs<kRounding>(p.sin + b * p.cs_sb + i * p.cs_st, l, it.sa, it.sb);
 }
 
+template <int kRounding>
 __device__ inline void q_item_store(const QkvParams& p, int32_t grp, int32_t groups, int hgroups, int l, const NormW& w,
                                     QItem& it) {
   if (grp >= groups) return;
@@ -428,14 +445,17 @@ __device__ inline void q_item_store(const QkvParams& p, int32_t grp, int32_t gro
 #pragma unroll
   for (int r = 0; r < kQRows; ++r) {
     if (h0 + r >= p.hq) break;
-    rope_norm_row_any(it.xa[r], it.xb[r], cs, w, p.eps, p.rounding);
+    rope_norm_row_any<kRounding>(it.xa[r], it.xb[r], cs, w, p.eps, p.rounding);
     store_nt(dst + r * kHeadDim + 8 * l, it.xa[r]);
     store_nt(dst + r * kHeadDim + 64 + 8 * l, it.xb[r]);
   }
 }
 
 // Workgroups [0, kv_wgs) take one (sequence, 32-position block, kv head) each; the rest 32 groups of
-// kQRows query rows (heads [kQRows j, kQRows j + kQRows) of one token, j < ceil(Hq / kQRows)).
+// kQRows query rows (heads [kQRows j, kQRows j + kQRows) of one token, j < ceil(Hq / kQRows)).  The
+// vLLM order runs instance 1 (half the cos / sin loads, 74 instead of 92 VGPRs: 280-282 against
+// 284-287 us at config 3's prefill call), the HF order instance 0.
+template <int kRounding>
 __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32_t kv_wgs, int32_t kv_blocks) {
   __shared__ uint16_t sv[kHeadDim * kVStride];
   const int t = threadIdx.x, l = t & (kRowLanes - 1);
@@ -446,8 +466,8 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
     if (grp >= groups) return;
     const NormW w = norm_weights(p.qw, l);
     QItem it;
-    q_item_load(p, grp, groups, hgroups, l, it);
-    q_item_store(p, grp, groups, hgroups, l, w, it);
+    q_item_load<kRounding>(p, grp, groups, hgroups, l, it);
+    q_item_store<kRounding>(p, grp, groups, hgroups, l, w, it);
     return;
   }
   const int kv = static_cast<int>(blockIdx.x);
@@ -475,9 +495,9 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
     uint4 ka, kb, ca, cb, sa, sb, va, vb;
     load_row_nt(p.k + tok_off(p, b, i, row, p.k_sb, p.k_st) + static_cast<int64_t>(g) * kHeadDim, l, ka, kb);
     load_row_nt(p.v + tok_off(p, b, i, row, p.v_sb, p.v_st) + static_cast<int64_t>(g) * kHeadDim, l, va, vb);
-    load_row(p.cos + tok_off(p, b, i, row, p.cs_sb, p.cs_st), l, ca, cb);
-    load_row(p.sin + tok_off(p, b, i, row, p.cs_sb, p.cs_st), l, sa, sb);
-    rope_norm_row_any(ka, kb, rope_cs(ca, cb, sa, sb), kw, p.eps, p.rounding);
+    load_cs<kRounding>(p.cos + tok_off(p, b, i, row, p.cs_sb, p.cs_st), l, ca, cb);
+    load_cs<kRounding>(p.sin + tok_off(p, b, i, row, p.cs_sb, p.cs_st), l, sa, sb);
+    rope_norm_row_any<kRounding>(ka, kb, rope_cs(ca, cb, sa, sb), kw, p.eps, p.rounding);
     // dims [8l, 8l + 8) and [64 + 8l, 64 + 8l + 8) of token w are 16 contiguous bytes each in a K tile
     const int ko0 = k_tile_offset(w, 8 * l), ko1 = k_tile_offset(w, 64 + 8 * l);
     if (ring_ok) {
@@ -712,8 +732,12 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
     const int64_t kv_wgs = static_cast<int64_t>(a->batch) * a->num_kv_heads * kv_blocks;
     const int64_t wgs = kv_wgs + (q_groups + 31) / 32;
     LKV_REQUIRE(wgs < (1LL << 31) && q_groups < (1LL << 31) - 32, "too many tokens in one call");
-    qkv_block_kernel<<<static_cast<unsigned>(wgs), 256, 0, as_stream(stream)>>>(p, static_cast<int32_t>(kv_wgs),
-                                                                              static_cast<int32_t>(kv_blocks));
+    if (p.rounding == 0)
+      qkv_block_kernel<0><<<static_cast<unsigned>(wgs), 256, 0, as_stream(stream)>>>(p, static_cast<int32_t>(kv_wgs),
+                                                                                 static_cast<int32_t>(kv_blocks));
+    else
+      qkv_block_kernel<1><<<static_cast<unsigned>(wgs), 256, 0, as_stream(stream)>>>(p, static_cast<int32_t>(kv_wgs),
+                                                                                 static_cast<int32_t>(kv_blocks));
   } else {
     const int blocks = static_cast<int>((items + 3) / 4);
     qkv_epilogue_kernel<<<blocks, 256, 0, as_stream(stream)>>>(p);
