@@ -286,6 +286,52 @@ def test_qkv_epilogue_matches_reference_ops(B, L, p0, last, C):
         assert np.array_equal(dk.float().cpu().numpy(), got_k) and np.array_equal(dv.float().cpu().numpy(), got_v)
 
 
+@pytest.mark.parametrize("L", [8, 40])
+def test_qkv_epilogue_signed_zeros_and_tiny_values(L):
+    """Rows of zeros (both signs), zeros mixed into ordinary rows and rows of tiny values (whose
+    rotary products are fp32 denormals) through both epilogue forms (8 tokens: one wave per (token,
+    head); 40: the block form), against the reference's bf16 torch ops on the CPU: every bit equal,
+    the sign of each zero included, up to the RMSNorm summation-order flips the other epilogue tests
+    allow (at most 0.1 % of values, one ulp)."""
+
+    rng = np.random.default_rng(400 + L)
+    B, Hq, Hkv, p0 = 2, 8, 2, 5
+
+    def rows(heads):
+        x = _bf(rng, (B, L, heads, 128))
+        x[0, 0] = 0.0                                          # a token of +0 rows
+        x[0, 1] = -0.0                                         # and of -0 rows
+        x[1, 2, :, ::3] = np.where(rng.random((heads, 43)) < 0.5, 0.0, -0.0)  # zeros among values
+        x[1, 3] = bf16.round_bf16((rng.standard_normal((heads, 128)) * 1e-36).astype(np.float32))
+        return x.reshape(B, L, heads * 128)
+
+    q, k, v = rows(Hq), rows(Hkv), _bf(rng, (B, L, Hkv * 128))
+    cfg = M.config_8b(num_hidden_layers=2)
+    inv, sc = M.rope_inv_freq(cfg)
+    cos, sin = M.rotary_cos_sin(inv, sc, torch.arange(p0, p0 + L)[None].expand(B, L), torch.bfloat16)
+    qw = torch.linspace(0.7, 1.3, 128).bfloat16()
+    kw = torch.linspace(1.2, 0.8, 128).bfloat16()
+    ring = ops.TiledKV.zeros(B, Hkv, ops.ring_tokens_for_chunk(32), DEV)
+    q_out = ops.qkv_epilogue(_t(q), _t(k), _t(v), cos.to(DEV), sin.to(DEV), num_q_heads=Hq, num_kv_heads=Hkv,
+                             q_norm_weight=qw.to(DEV), k_norm_weight=kw.to(DEV), eps=1e-5, positions=p0, ring=ring)
+    tq = torch.from_numpy(q).bfloat16().view(B, L, Hq, 128).transpose(1, 2)
+    tk = torch.from_numpy(k).bfloat16().view(B, L, Hkv, 128).transpose(1, 2)
+    rq, rk = M.apply_rope(tq, tk, cos, sin)
+    qn, kn = M.RMSNorm(128, 1e-5).bfloat16(), M.RMSNorm(128, 1e-5).bfloat16()
+    with torch.no_grad():
+        qn.weight.copy_(qw)
+        kn.weight.copy_(kw)
+        rq, rk = qn(rq), kn(rk)
+    want_q = rq.transpose(1, 2).float().numpy()
+    got_q = q_out.float().cpu().numpy()
+    assert np.count_nonzero(want_q == 0) > 1000 and np.count_nonzero(np.signbit(want_q) & (want_q == 0)) > 100
+    frac, ulp = _ulp_stats(got_q, want_q)
+    assert frac <= 1e-3 and ulp <= 1, (frac, ulp)
+    got_k = torch.cat([ops.unpack_kv(ring, p0 + i, 1)[0] for i in range(L)], 2).float().cpu().numpy()
+    frac, ulp = _ulp_stats(got_k, rk.float().numpy())
+    assert frac <= 1e-3 and ulp <= 1, (frac, ulp)
+
+
 @pytest.mark.parametrize("rounding", ["torch", "vllm"])
 def test_epilogue_forms_agree_bit_for_bit(rounding):
     """The per-token kernel (calls of fewer than 16 tokens) and the block form (16 or more) sum the
