@@ -68,6 +68,10 @@ def test_epilogue_vllm_rounding_bit_exact(L, norms):
     rng = np.random.default_rng(100 + L)
     B, Hq, Hkv, p0 = 2, 8, 2, 37
     q, k, v = _bf(rng, (B, L, Hq, 128), 2.0), _bf(rng, (B, L, Hkv, 128), 2.0), _bf(rng, (B, L, Hkv, 128), 2.0)
+    for x in (q, k):  # rows of +0 and of -0, and a row of tiny values (denormal rotary products)
+        x[0, 0] = 0.0
+        x[1, 0] = -0.0
+        x[1, L - 1] = bf16.round_bf16((rng.standard_normal(x.shape[2:]) * 1e-36).astype(np.float32))
     c, s = _rotary_np(p0 + np.arange(L))
     qw = bf16.round_bf16((rng.random(128) + 0.5).astype(np.float32)) if norms else None
     kw = bf16.round_bf16((rng.random(128) + 0.5).astype(np.float32)) if norms else None
@@ -85,11 +89,12 @@ def test_epilogue_vllm_rounding_bit_exact(L, norms):
     cq, sq = c[None, :, None], s[None, :, None]
     want_q = VP.rope_rms(q, cq, sq, qw, 1e-5)
     want_k = VP.rope_rms(k, cq, sq, kw, 1e-5)
-    assert np.array_equal(_np(q_out), want_q), f"q L={L}"
+    bits = lambda x: np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)  # (the sign of each zero too)
+    assert np.array_equal(bits(_np(q_out)), bits(want_q)), f"q L={L}"
     rk, rv = ops.unpack_kv(ring, p0, L)
     dk, dv = ops.unpack_kv(deep, p0, L)
-    assert np.array_equal(_np(rk), want_k.transpose(0, 2, 1, 3)), f"ring K L={L}"
-    assert np.array_equal(_np(dk), want_k.transpose(0, 2, 1, 3)), f"deep K L={L}"
+    assert np.array_equal(bits(_np(rk)), bits(want_k.transpose(0, 2, 1, 3))), f"ring K L={L}"
+    assert np.array_equal(bits(_np(dk)), bits(want_k.transpose(0, 2, 1, 3))), f"deep K L={L}"
     assert np.array_equal(_np(rv), VP.ring_value(v, inv).transpose(0, 2, 1, 3)), f"ring V / s L={L}"
     assert np.array_equal(_np(dv), v.transpose(0, 2, 1, 3)), f"deep raw V L={L}"
     # the two contracts differ (other rounding points), the torch-order call leaves the ring V raw
