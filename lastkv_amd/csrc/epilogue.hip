@@ -411,6 +411,11 @@ __device__ inline void load_cs(const uint16_t* row, int l, uint4& a, uint4& b) {
 // prefill call shape: 2 heads 310 us, 4 heads 313 us, 8 heads 335 us per call)
 constexpr int kQRows = 2;
 
+// kv heads per K/V workgroup: they share each token's cos / sin loads (measured at config 3's
+// prefill call, same box, four rounds: vLLM order 265-268 against 284-287 us with one head per
+// workgroup, HF order 313-316 against 320-328 us with the fused projection's rows)
+constexpr int kKvPerWg = 2;
+
 // The query rows of one 8-lane group: kQRows heads of one token and the token's cos / sin rows.
 struct QItem {
   uint4 xa[kQRows], xb[kQRows], ca, cb, sa, sb;
@@ -451,13 +456,13 @@ __device__ inline void q_item_store(const QkvParams& p, int32_t grp, int32_t gro
   }
 }
 
-// Workgroups [0, kv_wgs) take one (sequence, 32-position block, kv head) each; the rest 32 groups of
+// Workgroups [0, kv_wgs) take one (sequence, 32-position block, pair of kv heads) each; the rest 32 groups of
 // kQRows query rows (heads [kQRows j, kQRows j + kQRows) of one token, j < ceil(Hq / kQRows)).  The
 // vLLM order runs instance 1 (half the cos / sin loads, 74 instead of 92 VGPRs: 280-282 against
 // 284-287 us at config 3's prefill call), the HF order instance 0.
 template <int kRounding>
 __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32_t kv_wgs, int32_t kv_blocks) {
-  __shared__ uint16_t sv[kHeadDim * kVStride];
+  __shared__ uint16_t sv[kKvPerWg * kHeadDim * kVStride];
   const int t = threadIdx.x, l = t & (kRowLanes - 1);
   if (static_cast<int>(blockIdx.x) >= kv_wgs) {
     const int hgroups = (p.hq + kQRows - 1) / kQRows;
@@ -470,8 +475,11 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
     q_item_store<kRounding>(p, grp, groups, hgroups, l, w, it);
     return;
   }
+  // kv heads 2 gp and 2 gp + 1 (if present) of one (sequence, 32-position block): each token's
+  // cos / sin rows are loaded once for both
   const int kv = static_cast<int>(blockIdx.x);
-  const int jr = kv % kv_blocks, g = (kv / kv_blocks) % p.hkv, b = kv / (kv_blocks * p.hkv);
+  const int hpairs = (p.hkv + kKvPerWg - 1) / kKvPerWg;
+  const int jr = kv % kv_blocks, gp = (kv / kv_blocks) % hpairs, b = kv / (kv_blocks * hpairs);
   const int p0 = p.pos ? p.pos[b] : p.pos_c;
   if (p0 < 0) return;  // (uniform over the workgroup)
   // this sequence's tokens: rows [r0, r0 + n) of a ragged call, else tokens [0, p.tokens)
@@ -488,54 +496,77 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
   const int dslot = p.d_tab ? 0 : (p.deep_slot ? p.deep_slot[b] : b);
   const bool deep_ok = p.dk != nullptr && dslot >= 0 && dslot < p.deep_slots && blk * kBlockTokens < p.deep_cap;
   const int rblk = ((blk * kBlockTokens) % p.ring_tokens) >> 5;
-  const int64_t roff = ring_ok ? rslot * p.r_ss + g * p.r_hs + write_block(p.r_tab, p.r_tab_stride, p.r_page, p.r_npages, b, rblk) : 0;
-  const int64_t doff = deep_ok ? dslot * p.d_ss + g * p.d_hs + write_block(p.d_tab, p.d_tab_stride, p.d_page, p.d_npages, b, blk) : 0;
+  const int64_t rbase = ring_ok ? rslot * p.r_ss + write_block(p.r_tab, p.r_tab_stride, p.r_page, p.r_npages, b, rblk) : 0;
+  const int64_t dbase = deep_ok ? dslot * p.d_ss + write_block(p.d_tab, p.d_tab_stride, p.d_page, p.d_npages, b, blk) : 0;
+  const int g0 = gp * kKvPerWg, ng = min(kKvPerWg, p.hkv - g0);  // (uniform)
   const NormW kw = norm_weights(p.kw, l);
   if (valid) {
-    uint4 ka, kb, ca, cb, sa, sb, va, vb;
-    load_row_nt(p.k + tok_off(p, b, i, row, p.k_sb, p.k_st) + static_cast<int64_t>(g) * kHeadDim, l, ka, kb);
-    load_row_nt(p.v + tok_off(p, b, i, row, p.v_sb, p.v_st) + static_cast<int64_t>(g) * kHeadDim, l, va, vb);
+    static_assert(kKvPerWg == 2, "the K/V path below holds two heads");
+    uint4 ka0, kb0, va0, vb0, ka1, kb1, va1, vb1, ca, cb, sa, sb;
+    const int64_t go0 = static_cast<int64_t>(g0) * kHeadDim, go1 = static_cast<int64_t>(min(g0 + 1, p.hkv - 1)) * kHeadDim;
+    const uint16_t* krow = p.k + tok_off(p, b, i, row, p.k_sb, p.k_st);
+    const uint16_t* vrow = p.v + tok_off(p, b, i, row, p.v_sb, p.v_st);
+    load_row_nt(krow + go0, l, ka0, kb0);
+    load_row_nt(vrow + go0, l, va0, vb0);
+    load_row_nt(krow + go1, l, ka1, kb1);  // (a missing second head rereads the first)
+    load_row_nt(vrow + go1, l, va1, vb1);
     load_cs<kRounding>(p.cos + tok_off(p, b, i, row, p.cs_sb, p.cs_st), l, ca, cb);
     load_cs<kRounding>(p.sin + tok_off(p, b, i, row, p.cs_sb, p.cs_st), l, sa, sb);
-    rope_norm_row_any<kRounding>(ka, kb, rope_cs(ca, cb, sa, sb), kw, p.eps, p.rounding);
+    const RopeCS cs = rope_cs(ca, cb, sa, sb);
     // dims [8l, 8l + 8) and [64 + 8l, 64 + 8l + 8) of token w are 16 contiguous bytes each in a K tile
     const int ko0 = k_tile_offset(w, 8 * l), ko1 = k_tile_offset(w, 64 + 8 * l);
-    if (ring_ok) {
-      store_nt(p.rk + roff + ko0, ka);
-      store_nt(p.rk + roff + ko1, kb);
-    }
-    if (deep_ok) {
-      store_nt(p.dk + doff + ko0, ka);
-      store_nt(p.dk + doff + ko1, kb);
-    }
-    const uint16_t* ea = reinterpret_cast<const uint16_t*>(&va);
-    const uint16_t* eb = reinterpret_cast<const uint16_t*>(&vb);
+    auto head = [&](int h, uint4 ka, uint4 kb, uint4 va, uint4 vb) __attribute__((always_inline)) {
+      rope_norm_row_any<kRounding>(ka, kb, cs, kw, p.eps, p.rounding);
+      const int g = g0 + h;
+      if (ring_ok) {
+        store_nt(p.rk + rbase + g * p.r_hs + ko0, ka);
+        store_nt(p.rk + rbase + g * p.r_hs + ko1, kb);
+      }
+      if (deep_ok) {
+        store_nt(p.dk + dbase + g * p.d_hs + ko0, ka);
+        store_nt(p.dk + dbase + g * p.d_hs + ko1, kb);
+      }
+      const uint16_t* ea = reinterpret_cast<const uint16_t*>(&va);
+      const uint16_t* eb = reinterpret_cast<const uint16_t*>(&vb);
+      uint16_t* svh = sv + h * (kHeadDim * kVStride);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      sv[(8 * l + e) * kVStride + w] = ea[e];
-      sv[(64 + 8 * l + e) * kVStride + w] = eb[e];
-    }
+      for (int e = 0; e < 8; ++e) {
+        svh[(8 * l + e) * kVStride + w] = ea[e];
+        svh[(64 + 8 * l + e) * kVStride + w] = eb[e];
+      }
+    };
+    head(0, ka0, kb0, va0, vb0);
+    if (ng > 1) head(1, ka1, kb1, va1, vb1);
   }
   __syncthreads();
-  // V tile: element (token w, dim d) at d * 32 + w; 512 runs of 8 tokens of one dim.  The ring
-  // takes bf16(v * rv_mul[g]) on the vLLM path, the deep store the raw V.
+  // V tiles: element (token w, dim d) at d * 32 + w; 512 runs of 8 tokens of one dim per head.  The
+  // ring takes bf16(v * rv_mul[g]) on the vLLM path, the deep store the raw V.
   const int lo = max(0, p0 - blk * kBlockTokens), hi = min(kBlockTokens, p0 + n - blk * kBlockTokens);
-  const float vm = p.rv_mul != nullptr ? p.rv_mul[g] : 1.f;
 #pragma unroll
-  for (int run = t; run < kHeadDim * 4; run += 256) {
-    const int d = run >> 2, w0 = 8 * (run & 3);
-    if (w0 + 8 <= lo || w0 >= hi) continue;
-    const uint4 x = *reinterpret_cast<const uint4*>(sv + d * kVStride + w0);
-    const uint4 xr = p.rv_mul != nullptr ? scale8(x, vm) : x;
-    if (w0 >= lo && w0 + 8 <= hi) {
-      if (ring_ok) store_nt(p.rv + roff + d * kBlockTokens + w0, xr);
-      if (deep_ok) store_nt(p.dv + doff + d * kBlockTokens + w0, x);
-    } else {  // a block edge of the call: only its own tokens
-      const uint16_t* e = reinterpret_cast<const uint16_t*>(&x);
-      const uint16_t* er = reinterpret_cast<const uint16_t*>(&xr);
-      for (int j = max(lo - w0, 0); j < min(hi - w0, 8); ++j) {
-        if (ring_ok) p.rv[roff + d * kBlockTokens + w0 + j] = er[j];
-        if (deep_ok) p.dv[doff + d * kBlockTokens + w0 + j] = e[j];
+  for (int h = 0; h < kKvPerWg; ++h) {
+    if (h >= ng) break;
+    const int g = g0 + h;
+    const int64_t roff = rbase + g * p.r_hs, doff = dbase + g * p.d_hs;
+    const float vm = p.rv_mul != nullptr ? p.rv_mul[g] : 1.f;
+    const uint16_t* svh = sv + h * (kHeadDim * kVStride);
+#pragma unroll
+    for (int run = t; run < kHeadDim * 4; run += 256) {
+      const int d = run >> 2, w0 = 8 * (run & 3);
+      if (w0 + 8 <= lo || w0 >= hi) continue;
+      const uint4 x = *reinterpret_cast<const uint4*>(svh + d * kVStride + w0);
+      const uint4 xr = p.rv_mul != nullptr ? scale8(x, vm) : x;
+      if (w0 >= lo && w0 + 8 <= hi) {
+        if (ring_ok) store_nt(p.rv + roff + d * kBlockTokens + w0, xr);
+        if (deep_ok) store_nt(p.dv + doff + d * kBlockTokens + w0, x);
+      } else {  // a block edge of the call: only its own tokens
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(&x);
+        const uint16_t* er = reinterpret_cast<const uint16_t*>(&xr);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {  // (constant indices: the 8 values stay in registers)
+          if (w0 + j < lo || w0 + j >= hi) continue;
+          if (ring_ok) p.rv[roff + d * kBlockTokens + w0 + j] = er[j];
+          if (deep_ok) p.dv[doff + d * kBlockTokens + w0 + j] = e[j];
+        }
       }
     }
   }
@@ -729,7 +760,7 @@ extern "C" int32_t lkv_qkv_epilogue(const lkv_qkv_args* a, lkv_stream_t stream) 
                           aligned(a->deep_v, a->deep_page_stride, 0);
   if (block_form) {
     const int64_t q_groups = rows * ((a->num_q_heads + kQRows - 1) / kQRows);
-    const int64_t kv_wgs = static_cast<int64_t>(a->batch) * a->num_kv_heads * kv_blocks;
+    const int64_t kv_wgs = static_cast<int64_t>(a->batch) * ((a->num_kv_heads + kKvPerWg - 1) / kKvPerWg) * kv_blocks;
     const int64_t wgs = kv_wgs + (q_groups + 31) / 32;
     LKV_REQUIRE(wgs < (1LL << 31) && q_groups < (1LL << 31) - 32, "too many tokens in one call");
     if (p.rounding == 0)
