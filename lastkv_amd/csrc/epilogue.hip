@@ -254,6 +254,31 @@ struct NormW {
   bool on;
 };
 
+// The same weights unpacked to fp32 once (the query rows: each thread normalises several rows with
+// them; the K/V rows keep them packed, where the registers matter more).
+struct Unpacked8 {
+  float v[8];
+  __device__ float operator[](int j) const { return v[j]; }
+};
+struct NormWU {
+  Unpacked8 w0, w1;
+  bool on;
+};
+
+__device__ inline NormW norm_weights(const uint16_t* w, int l);
+
+__device__ inline NormWU norm_weights_unpacked(const uint16_t* w, int l) {
+  const NormW p = norm_weights(w, l);
+  NormWU r;
+  r.on = p.on;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    r.w0.v[j] = p.w0[j];
+    r.w1.v[j] = p.w1[j];
+  }
+  return r;
+}
+
 __device__ inline NormW norm_weights(const uint16_t* w, int l) {
   NormW r;
   r.on = w != nullptr;
@@ -286,7 +311,8 @@ __device__ inline void rb2(float& a, float& b) {
 // RoPE then RMSNorm of the row held by an 8-lane group (lane l: dims 8l.. in a / 64 + 8l.. in b),
 // every bf16 operation of the reference rounded in the same order (rb; the last rounding is the
 // packing of the output).
-__device__ inline void rope_norm_row(uint4& a, uint4& b, const RopeCS& cs, const NormW& w, float eps) {
+template <class NW>
+__device__ inline void rope_norm_row(uint4& a, uint4& b, const RopeCS& cs, const NW& w, float eps) {
   float x0[8], x1[8], r0[8], r1[8];
   unpack8(a, x0), unpack8(b, x1);
 #pragma unroll
@@ -327,7 +353,8 @@ __device__ inline void rope_norm_row(uint4& a, uint4& b, const RopeCS& cs, const
 // whose squares the reference accumulates in order with fused multiply-adds; adjacent groups are
 // then added pairwise (lane xor 1, 2, 4) and the two halves last.  cos / sin of dims [0, 64) rotate
 // both halves.
-__device__ inline void rope_norm_row_vllm(uint4& a, uint4& b, const RopeCS& cs, const NormW& w, float eps) {
+template <class NW>
+__device__ inline void rope_norm_row_vllm(uint4& a, uint4& b, const RopeCS& cs, const NW& w, float eps) {
 #pragma clang fp contract(off)
   float x0[8], x1[8], r0[8], r1[8];
   unpack8(a, x0), unpack8(b, x1);
@@ -363,8 +390,8 @@ __device__ inline void rope_norm_row_vllm(uint4& a, uint4& b, const RopeCS& cs, 
 // kMode 1: the vLLM order (fixed at compile time); kMode 0: either order, by `rounding` at run time.
 // (A block kernel specialised to the HF order measured slower for q, k, v as separate tensors:
 // 311-316 against 305-310 us at config 3's prefill call, same box, four rounds.)
-template <int kMode>
-__device__ inline void rope_norm_row_any(uint4& a, uint4& b, const RopeCS& cs, const NormW& w, float eps, int rounding) {
+template <int kMode, class NW>
+__device__ inline void rope_norm_row_any(uint4& a, uint4& b, const RopeCS& cs, const NW& w, float eps, int rounding) {
   if (kMode == 0 && rounding == 0)
     rope_norm_row(a, b, cs, w, eps);
   else
@@ -438,8 +465,8 @@ __device__ inline void q_item_load(const QkvParams& p, int32_t grp, int32_t grou
   load_cs<kRounding>(p.sin + b * p.cs_sb + i * p.cs_st, l, it.sa, it.sb);
 }
 
-template <int kRounding>
-__device__ inline void q_item_store(const QkvParams& p, int32_t grp, int32_t groups, int hgroups, int l, const NormW& w,
+template <int kRounding, class NW>
+__device__ inline void q_item_store(const QkvParams& p, int32_t grp, int32_t groups, int hgroups, int l, const NW& w,
                                     QItem& it) {
   if (grp >= groups) return;
   const int h0 = grp % hgroups * kQRows;
@@ -469,7 +496,7 @@ __global__ __launch_bounds__(256) void qkv_block_kernel(const QkvParams p, int32
     const int32_t groups = (p.cu ? 1 : p.batch) * p.tokens * hgroups;  // < 2^31 (checked by the host)
     const int32_t grp = (static_cast<int32_t>(blockIdx.x) - kv_wgs) * 32 + (t >> 3);
     if (grp >= groups) return;
-    const NormW w = norm_weights(p.qw, l);
+    const NormWU w = norm_weights_unpacked(p.qw, l);
     QItem it;
     q_item_load<kRounding>(p, grp, groups, hgroups, l, it);
     q_item_store<kRounding>(p, grp, groups, hgroups, l, w, it);
